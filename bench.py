@@ -1,0 +1,258 @@
+"""Benchmark of the catena MI355X hot path (one GPU).
+
+Headline workload: bf16 GEMM M=N=K=4096, fp32
+accumulate, bf16 output, NN row-major, fixed reduction order.  One "step" is
+one launch of that GEMM on inputs already resident in HBM.  The same JSON line
+carries, under "extra", the KV-cache decode attention (configs[3]: B=32,
+H=32, D=128, L=4096) and the decode-shape GEMMs, each with its
+own roofline, because BASELINE.json's metric names both GEMM TFLOP/s and
+attention HBM GB/s.
+
+Timing: W untimed warmup launches, then K launches bracketed by stream
+synchronisation and HIP events recorded on the library's own stream (the
+stream every kernel is launched on).  Inputs come from the library's seeded
+device RNG.  The cpu_baseline leg times the CPU oracle (the reference's
+sequential arithmetic restated in C, gcc -O2 -ffp-contract=off) on a bounded
+sample of the same workload on this host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "catena-lang_amd"))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+import catena_amd as ca  # noqa: E402
+
+METRIC = "det. bf16 GEMM TFLOP/s (%MFMA peak); KV-cache decode attention HBM GB/s"
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+
+class HipEvents:
+    """hipEvent timing on a given stream through libamdhip64."""
+
+    def __init__(self, stream: int):
+        self.hip = ctypes.CDLL("libamdhip64.so")
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                                 ctypes.c_void_p]
+        self.stream = ctypes.c_void_p(stream)
+        self.a, self.b = ctypes.c_void_p(), ctypes.c_void_p()
+        assert self.hip.hipEventCreate(ctypes.byref(self.a)) == 0
+        assert self.hip.hipEventCreate(ctypes.byref(self.b)) == 0
+
+    def start(self):
+        assert self.hip.hipEventRecord(self.a, self.stream) == 0
+
+    def stop_ms(self) -> float:
+        assert self.hip.hipEventRecord(self.b, self.stream) == 0
+        assert self.hip.hipEventSynchronize(self.b) == 0
+        ms = ctypes.c_float()
+        assert self.hip.hipEventElapsedTime(ctypes.byref(ms), self.a, self.b) == 0
+        return ms.value
+
+
+def timed(fn, steps: int, warmup: int, ev: HipEvents) -> float:
+    """Average ms per call of fn over `steps` calls after `warmup` calls."""
+    for i in range(warmup):
+        fn(i)
+    ca.synchronize()
+    ev.start()
+    for i in range(steps):
+        fn(i)
+    ms = ev.stop_ms()
+    ca.synchronize()
+    return ms / steps
+
+
+def output_hash(buf: ca.Buffer) -> str:
+    import hashlib
+    return hashlib.sha256(buf.read(np.uint8).tobytes()).hexdigest()[:16]
+
+
+# ------------------------------------------------------------------ workloads
+def bench_gemm(steps, warmup, ev):
+    n = m = k = 4096
+    a, b, c = ca.Buffer(n * k * 2), ca.Buffer(k * m * 2), ca.Buffer(n * m * 2)
+    ca.fill_normal_bf16(a, n * k, 3, 0, 1.0)
+    ca.fill_normal_bf16(b, k * m, 4, 0, 1.0)
+    ca.gemm_bf16(a, b, c, n, m, k)
+    h0 = output_hash(c)
+    ms = timed(lambda i: ca.gemm_bf16(a, b, c, n, m, k), steps, warmup, ev)
+    flop = 2.0 * n * m * k
+    tflops = flop / (ms * 1e-3) / 1e12
+    return {"ms": ms, "tflops": tflops, "flop": flop, "bitwise_run_to_run": output_hash(c) == h0,
+            "inputs": (a, b)}
+
+
+def bench_decode_gemm(steps, warmup, ev):
+    """M=16 x (N=11008, K=4096) and (N=4096, K=11008).  Four
+    weight copies per shape rotate so the 90 MB weights cannot sit in the
+    256 MB Infinity Cache between launches."""
+    res = {}
+    M = 16
+    copies = 4
+    for (N, K) in [(11008, 4096), (4096, 11008)]:
+        x = ca.Buffer(M * K * 2)
+        ca.fill_normal_bf16(x, M * K, 7, 0, 1.0)
+        ws = []
+        for c in range(copies):
+            w = ca.Buffer(K * N * 2)
+            ca.fill_normal_bf16(w, K * N, 8, c, 0.02)
+            ws.append(w)
+        y = ca.Buffer(M * N * 2)
+        ms = timed(lambda i: ca.gemm_bf16(x, ws[i % copies], y, M, N, K), steps, warmup, ev)
+        nbytes = 2.0 * N * K + 2.0 * M * K + 2.0 * M * N
+        res[f"N{N}_K{K}"] = {"us": ms * 1e3, "GB/s": nbytes / (ms * 1e-3) / 1e9,
+                             "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                             "bytes_per_launch": nbytes}
+        del ws
+    return res
+
+
+def bench_attention(steps, warmup, ev):
+    B, H, L, D = 32, 32, 4096, 128
+    q = ca.Buffer(B * H * D * 2)
+    k = ca.Buffer(B * H * L * D * 2)
+    v = ca.Buffer(B * H * L * D * 2)
+    ca.fill_normal_bf16(q, B * H * D, 41, 0, 1.0)
+    ca.fill_normal_bf16(k, B * H * L * D, 41, 1, 1.0)
+    ca.fill_normal_bf16(v, B * H * L * D, 41, 2, 1.0)
+    lens = ca.Buffer.from_array(np.full(B, L, np.uint32))
+    o = ca.Buffer(B * H * D * 4)
+    scale = float(np.float32(1.0 / math.sqrt(D)))
+    call = lambda i: ca.attn_decode_bf16(q, k, v, lens, o, B, H, L, D, scale)  # noqa: E731
+    call(0)
+    h0 = output_hash(o)
+    ms = timed(call, steps, warmup, ev)
+    nbytes = 2.0 * B * H * L * D * 2 + B * H * D * 2 + B * H * D * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"us": ms * 1e3, "GB/s": gbs, "frac_hbm": gbs / PEAK_HBM_GBS, "bytes_per_launch": nbytes,
+            "bitwise_run_to_run": output_hash(o) == h0, "inputs": (q, k, v)}
+
+
+# ------------------------------------------------------------------ CPU baseline
+def cpu_baseline_gemm(a_buf, b_buf, rows: int, threads: int):
+    import oracle
+    n = k = m = 4096
+    a16 = a_buf.read(np.uint16, (n, k))
+    b16 = b_buf.read(np.uint16, (k, m))
+    sel = np.arange(rows, dtype=np.uint64)
+    oracle.matmul_bf16(a16, b16, rows=sel[:1], threads=1)  # warm
+    t0 = time.perf_counter()
+    oracle.matmul_bf16(a16, b16, rows=sel, threads=threads)
+    dt = time.perf_counter() - t0
+    flop = 2.0 * rows * m * k
+    return {"value": flop / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{rows} of 4096 output rows of the 4096^3 bf16 GEMM, sequential "
+                      f"k-ascending f32 fold (oracle/catena_oracle.c, gcc -O2 "
+                      f"-ffp-contract=off), {dt:.1f} s"}
+
+
+def cpu_baseline_attention(q, k, v, heads: int, threads: int):
+    import oracle
+    B, H, L, D = 32, 32, 4096, 128
+    # read the first `heads` (b, h) slices only
+    hl = np.arange(heads, dtype=np.uint32)
+    q16 = q.read(np.uint16, (B, H, D))
+    nbh = heads
+    kk = k.read(np.uint16, (nbh * L * D,)).reshape(1, nbh, L, D)
+    vv = v.read(np.uint16, (nbh * L * D,)).reshape(1, nbh, L, D)
+    qq = q16.reshape(1, B * H, D)[:, :nbh]
+    lens = np.array([L], np.uint32)
+    scale = float(np.float32(1.0 / math.sqrt(D)))
+    t0 = time.perf_counter()
+    oracle.attn_decode(qq, kk, vv, lens, scale, threads=threads)
+    dt = time.perf_counter() - t0
+    nbytes = nbh * (2.0 * L * D * 2 + D * 2 + D * 4)
+    del hl
+    return {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{nbh} of 1024 (batch, head) slices, {dt:.1f} s"}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", choices=["gemm", "all"], default="all")
+    args = ap.parse_args(argv)
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path "
+              "(the GEMM would shard by output columns and attention by (batch, head); "
+              "see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    ca.init(0)
+    ev = HipEvents(ca.stream())
+    print("[bench] bf16 GEMM 4096^3", file=sys.stderr, flush=True)
+    g = bench_gemm(args.steps, args.warmup, ev)
+    extra = {}
+    if args.only == "all":
+        print("[bench] decode attention B32 H32 L4096 D128", file=sys.stderr, flush=True)
+        at = bench_attention(max(5, args.steps // 5), max(2, args.warmup // 5), ev)
+        print("[bench] decode GEMMs M=16", file=sys.stderr, flush=True)
+        dg = bench_decode_gemm(max(20, args.steps), args.warmup, ev)
+        extra = {
+            "decode_attention": {
+                "workload": "B=32 H=32 D=128 L=4096 bf16 KV, f32 softmax/out, bitwise vs sequential oracle",
+                "us_per_launch": at["us"], "GB/s": at["GB/s"], "bitwise_run_to_run": at["bitwise_run_to_run"],
+                "roofline": {"bound": "hbm", "achieved": at["GB/s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                             "frac": at["frac_hbm"], "traffic": None},
+                "bytes_per_launch": at["bytes_per_launch"]},
+            "decode_gemm_m16": dg,
+        }
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = max(1, min(16, len(os.sched_getaffinity(0))))
+        print(f"[bench] cpu baseline ({threads} threads)", file=sys.stderr, flush=True)
+        a, b = g["inputs"]
+        cpu = cpu_baseline_gemm(a, b, rows=96, threads=threads)
+        if args.only == "all":
+            q, k, v = at["inputs"]
+            extra["decode_attention"]["cpu_baseline"] = cpu_baseline_attention(q, k, v, 64, threads)
+
+    tflops = g["tflops"]
+    line = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(g["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded device RNG, N(0,1) bf16)",
+        "config": {"workload": "bf16 GEMM M=N=K=4096, fp32 accumulate, bf16 out, NN row-major, "
+                               "fixed K order (BASELINE configs[1])",
+                   "M": 4096, "N": 4096, "K": 4096, "parallelism": "single GPU"},
+        "bitwise_run_to_run": g["bitwise_run_to_run"],
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,94 @@
+"""Build libcatena_mi355x: gfx950 code objects + the host C-ABI library.
+
+Kernels (csrc/kernels/*.hip) are compiled for gfx950 only into raw code
+objects (lib/<name>.co) that the host library loads with hipModuleLoad.
+Flags keep the reference's arithmetic contract (no FMA contraction, no
+fast-math: catena-lang/src/runtime/artifact.rs:59-71) and disable packed
+fp32 instruction selection.  The host side (csrc/host/*.cpp) is plain C++17
+compiled with g++ against the HIP runtime.
+
+Usage: python catena-lang_amd/build.py [--jobs N]
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import glob
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+KDIR = os.path.join(HERE, "csrc", "kernels")
+HDIR = os.path.join(HERE, "csrc", "host")
+OUT = os.path.join(HERE, "lib")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = os.path.join(ROCM, "bin", "hipcc")
+
+KERNEL_FLAGS = [
+    "-x", "hip", "--offload-arch=gfx950", "--offload-device-only", "--no-gpu-bundle-output",
+    "-O3", "-std=c++17", "-ffp-contract=off", "-fno-fast-math",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+]
+HOST_FLAGS = [
+    "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", "-Wno-unused-parameter",
+    "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", f"-I{os.path.join(ROOT, 'include')}",
+]
+HOST_LIBS = [f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-ldl", "-pthread"]
+
+LIB_NAME = "libcatena_mi355x.so"
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    err = "\n".join(l for l in r.stderr.splitlines() if "not a recognized feature" not in l
+                    and "is not a recognized feature for this target" not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"command failed ({r.returncode}): {' '.join(cmd)}\n{err}")
+    return err
+
+
+def build_kernel(src: str) -> str:
+    name = os.path.splitext(os.path.basename(src))[0]
+    out = os.path.join(OUT, name + ".co")
+    tmp = out + ".tmp"
+    _run([HIPCC, *KERNEL_FLAGS, "-c", src, "-o", tmp])
+    os.replace(tmp, out)
+    return out
+
+
+def build_host() -> str:
+    srcs = sorted(glob.glob(os.path.join(HDIR, "*.cpp")))
+    out = os.path.join(OUT, LIB_NAME)
+    tmp = out + ".tmp"
+    cxx = os.environ.get("CXX", "g++")
+    _run([cxx, *HOST_FLAGS, *srcs, "-o", tmp, *HOST_LIBS])
+    os.replace(tmp, out)
+    return out
+
+
+def build(jobs: int = 8) -> list[str]:
+    if not os.path.exists(HIPCC):
+        raise RuntimeError(f"hipcc not found at {HIPCC}")
+    os.makedirs(OUT, exist_ok=True)
+    srcs = sorted(glob.glob(os.path.join(KDIR, "*.hip")))
+    with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        futs = [ex.submit(build_kernel, s) for s in srcs]
+        futs.append(ex.submit(build_host))
+        return [f.result() for f in futs]
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--jobs", type=int, default=min(8, os.cpu_count() or 1))
+    args = ap.parse_args(argv)
+    for p in build(args.jobs):
+        print(os.path.relpath(p, ROOT))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

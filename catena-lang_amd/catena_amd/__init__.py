@@ -1,0 +1,347 @@
+"""ctypes binding of libcatena_mi355x (include/catena_mi355x.h).
+
+This is plumbing for Python callers (tests, bench, smoke): every call goes
+through the C ABI into the native library and its gfx950 kernels.  There is
+no Python or CPU fallback; if the library or its code objects are missing,
+`lib()` raises.
+
+Layout mirrors the C header:
+  * device/pool:   init, Buffer (catena_mem_t), synchronize, stream
+  * kernel ABI:    gemm_f32_exact, gemm_bf16, attn_decode_bf16, softmax_f32, ...
+  * program ABI:   program_* functions (fail-stop: they trap on bad input)
+  * runtime:       Runtime (catena_runtime_*), mirrors Runtime::from_sources /
+                   exec / mem_* of catena-lang/src/runtime/runtime.rs:104-247
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.dirname(_HERE)
+LIB_DIR = os.path.join(PKG_DIR, "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libcatena_mi355x.so")
+
+CATENA_OK = 0
+STATUS_NAMES = {0: "OK", 1: "INVALID_ARGUMENT", 2: "UNSUPPORTED", 3: "HIP", 4: "OUT_OF_MEMORY",
+                5: "NOT_INITIALIZED", 6: "LOAD"}
+
+# catena_value_kind_t (ValueKind, catena-lang/src/runtime/value.rs:15-21)
+KIND_BOOL, KIND_U32, KIND_U64, KIND_F32, KIND_MEM = range(5)
+KIND_NAMES = {0: "Bool", 1: "U32", 2: "U64", 3: "F32", 4: "Mem"}
+
+EXEC_OK = 0
+EXEC_UNKNOWN_SOURCE_FUNCTION = 1
+EXEC_INPUT_ARITY_MISMATCH = 2
+EXEC_OUTPUT_ARITY_MISMATCH = 3
+EXEC_TYPE_MISMATCH = 4
+INIT_PARSE = 10
+INIT_NO_LOWERING = 11
+INIT_SIGNATURE_MISMATCH = 12
+INIT_DIALECT = 13
+INIT_DEVICE = 14
+
+
+class CatenaError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"[{STATUS_NAMES.get(status, status)}] {message}")
+        self.status = status
+
+
+class Mem(ctypes.Structure):
+    """catena_mem_t: {void* data; uint64_t len} (bytes)."""
+    _fields_ = [("data", ctypes.c_void_p), ("len", ctypes.c_uint64)]
+
+
+class _ValueUnion(ctypes.Union):
+    _fields_ = [("b", ctypes.c_uint8), ("u32", ctypes.c_uint32), ("u64", ctypes.c_uint64),
+                ("f32", ctypes.c_float), ("mem", Mem)]
+
+
+class Value(ctypes.Structure):
+    """catena_value_t: tagged Value (catena-lang/src/runtime/value.rs:5-12)."""
+    _fields_ = [("kind", ctypes.c_int), ("as_", _ValueUnion)]
+
+    @staticmethod
+    def bool(v: bool) -> "Value":
+        x = Value(); x.kind = KIND_BOOL; x.as_.b = 1 if v else 0; return x
+
+    @staticmethod
+    def u32(v: int) -> "Value":
+        x = Value(); x.kind = KIND_U32; x.as_.u32 = v; return x
+
+    @staticmethod
+    def u64(v: int) -> "Value":
+        x = Value(); x.kind = KIND_U64; x.as_.u64 = v; return x
+
+    @staticmethod
+    def f32(v: float) -> "Value":
+        x = Value(); x.kind = KIND_F32; x.as_.f32 = v; return x
+
+    @staticmethod
+    def mem(m: Mem) -> "Value":
+        x = Value(); x.kind = KIND_MEM; x.as_.mem = m; return x
+
+    def get(self):
+        k = self.kind
+        if k == KIND_BOOL:
+            return self.as_.b
+        if k == KIND_U32:
+            return self.as_.u32
+        if k == KIND_U64:
+            return self.as_.u64
+        if k == KIND_F32:
+            return self.as_.f32
+        return self.as_.mem
+
+
+_lib = None
+_vp = ctypes.c_void_p
+_u64 = ctypes.c_uint64
+_u32 = ctypes.c_uint32
+_f32 = ctypes.c_float
+_int = ctypes.c_int
+
+# name -> (restype, argtypes); the list is the header's full export surface.
+SIGNATURES = {
+    "catena_mi355x_init": (_int, [_int]),
+    "catena_mi355x_last_error": (ctypes.c_char_p, []),
+    "catena_mi355x_stream": (_vp, []),
+    "catena_mi355x_synchronize": (_int, []),
+    "catena_mem_alloc": (_int, [_u64, ctypes.POINTER(Mem)]),
+    "catena_mem_free": (_int, [ctypes.POINTER(Mem)]),
+    "catena_mem_write": (_int, [Mem, _u64, _vp, _u64]),
+    "catena_mem_read": (_int, [Mem, _u64, _vp, _u64]),
+    "catena_pool_stats": (_int, [ctypes.POINTER(_u64)] * 3),
+    "catena_pool_trim": (_int, []),
+    "catena_mi355x_gemm_f32_exact": (_int, [_vp, _vp, _vp, _u64, _u64, _u64]),
+    "catena_mi355x_gemm_bf16": (_int, [_vp, _vp, _vp, _u64, _u64, _u64, _int]),
+    "catena_mi355x_attn_decode_bf16": (_int, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _f32]),
+    "catena_mi355x_softmax_f32": (_int, [_vp, _vp, _u64, _u64]),
+    "catena_mi355x_exp_approx_f32": (_int, [_vp, _vp, _u64]),
+    "catena_mi355x_fill_normal_bf16": (_int, [_vp, _u64, _u64, _u64, _f32]),
+    "catena_mi355x_fill_uniform_f32": (_int, [_vp, _u64, _u64, _u64]),
+    "program_matmul_2x2_via_mem": (None, [Mem, Mem] + [_u64] * 6 + [ctypes.POINTER(Mem)]),
+    "program_matmul_right_identity_2x2_via_mem": (None, [Mem, _u64, _u64, ctypes.POINTER(Mem)]),
+    "program_matmul_left_identity_2x2_via_mem": (None, [Mem, _u64, _u64, ctypes.POINTER(Mem)]),
+    "program_nn_softmax": (None, [Mem, ctypes.POINTER(Mem)]),
+    "program_math_exp_approx": (None, [_f32, ctypes.POINTER(_f32)]),
+    "program_bf16_matmul_via_mem": (None, [Mem, Mem] + [_u64] * 6 + [ctypes.POINTER(Mem)]),
+    "program_attn_decode_via_mem": (None, [Mem, Mem, Mem, Mem] + [_u64] * 4 + [_f32, ctypes.POINTER(Mem)]),
+    "catena_runtime_from_sources": (_int, [ctypes.POINTER(ctypes.c_char_p), ctypes.c_size_t,
+                                           ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "catena_runtime_destroy": (None, [_vp]),
+    "catena_runtime_exec": (_int, [_vp, ctypes.c_char_p, ctypes.POINTER(Value), ctypes.c_size_t,
+                                   ctypes.POINTER(Value), ctypes.c_size_t]),
+    "catena_runtime_last_error_detail": (_int, [ctypes.POINTER(ctypes.c_int64)] * 3),
+    "catena_runtime_program_count": (ctypes.c_size_t, [_vp]),
+    "catena_runtime_program_name": (ctypes.c_char_p, [_vp, ctypes.c_size_t]),
+    "catena_runtime_mem_u64": (_int, [_vp, ctypes.POINTER(_u64), ctypes.c_size_t, ctypes.POINTER(Value)]),
+    "catena_runtime_mem_f32": (_int, [_vp, ctypes.POINTER(_f32), ctypes.c_size_t, ctypes.POINTER(Value)]),
+}
+
+
+def lib():
+    """Load libcatena_mi355x.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: run `python catena-lang_amd/build.py` "
+                               "(or __graft_entry__.build()) first")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return (lib().catena_mi355x_last_error() or b"").decode()
+
+
+def check(status: int) -> None:
+    if status != CATENA_OK:
+        raise CatenaError(status, last_error())
+
+
+def init(device: int = 0) -> None:
+    check(lib().catena_mi355x_init(device))
+
+
+def synchronize() -> None:
+    check(lib().catena_mi355x_synchronize())
+
+
+def stream() -> int:
+    s = lib().catena_mi355x_stream()
+    if not s:
+        raise CatenaError(5, last_error())
+    return s
+
+
+def pool_stats():
+    a, b, c = _u64(), _u64(), _u64()
+    check(lib().catena_pool_stats(ctypes.byref(a), ctypes.byref(b), ctypes.byref(c)))
+    return {"bytes_live": a.value, "bytes_cached": b.value, "device_allocs": c.value}
+
+
+class Buffer:
+    """Owning handle of a pool buffer (catena_mem_t); freed on close/GC."""
+
+    def __init__(self, nbytes: int = 0, mem: Mem | None = None):
+        if mem is not None:
+            self.mem = mem
+        else:
+            self.mem = Mem()
+            check(lib().catena_mem_alloc(int(nbytes), ctypes.byref(self.mem)))
+
+    @classmethod
+    def from_array(cls, arr: np.ndarray) -> "Buffer":
+        arr = np.ascontiguousarray(arr)
+        b = cls(arr.nbytes)
+        b.write(arr)
+        return b
+
+    @property
+    def ptr(self) -> int:
+        return self.mem.data or 0
+
+    @property
+    def nbytes(self) -> int:
+        return self.mem.len
+
+    def write(self, arr: np.ndarray, offset: int = 0) -> None:
+        arr = np.ascontiguousarray(arr)
+        check(lib().catena_mem_write(self.mem, offset, arr.ctypes.data_as(_vp), arr.nbytes))
+
+    def read(self, dtype, shape=None, offset: int = 0) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        count = (self.mem.len - offset) // dtype.itemsize if shape is None else int(np.prod(shape))
+        out = np.empty(count, dtype)
+        check(lib().catena_mem_read(self.mem, offset, out.ctypes.data_as(_vp), out.nbytes))
+        return out if shape is None else out.reshape(shape)
+
+    def close(self) -> None:
+        if getattr(self, "mem", None) is not None and self.mem.data and _lib is not None:
+            check(_lib.catena_mem_free(ctypes.byref(self.mem)))
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ------------------------------------------------------------------ kernel ABI
+def _p(x) -> int:
+    return x.ptr if isinstance(x, Buffer) else int(x)
+
+
+def gemm_f32_exact(a, b, c, n: int, m: int, k: int) -> None:
+    check(lib().catena_mi355x_gemm_f32_exact(_p(a), _p(b), _p(c), n, m, k))
+
+
+def gemm_bf16(a, b, c, n: int, m: int, k: int, out_f32: bool = False) -> None:
+    check(lib().catena_mi355x_gemm_bf16(_p(a), _p(b), _p(c), n, m, k, 1 if out_f32 else 0))
+
+
+def attn_decode_bf16(q, k, v, lens, o, batch: int, heads: int, max_len: int, head_dim: int,
+                     scale: float) -> None:
+    check(lib().catena_mi355x_attn_decode_bf16(_p(q), _p(k), _p(v), _p(lens), _p(o), batch, heads,
+                                               max_len, head_dim, scale))
+
+
+def softmax_f32(x, y, rows: int, n: int) -> None:
+    check(lib().catena_mi355x_softmax_f32(_p(x), _p(y), rows, n))
+
+
+def exp_approx_f32(x, y, n: int) -> None:
+    check(lib().catena_mi355x_exp_approx_f32(_p(x), _p(y), n))
+
+
+def fill_normal_bf16(out, n: int, seed: int, stream_id: int, scale: float = 1.0) -> None:
+    check(lib().catena_mi355x_fill_normal_bf16(_p(out), n, seed, stream_id, scale))
+
+
+def fill_uniform_f32(out, n: int, seed: int, stream_id: int) -> None:
+    check(lib().catena_mi355x_fill_uniform_f32(_p(out), n, seed, stream_id))
+
+
+# ------------------------------------------------------------------ runtime
+class ExecError(RuntimeError):
+    def __init__(self, status: int, message: str, index: int, expected: int, actual: int):
+        super().__init__(message)
+        self.status, self.index, self.expected, self.actual = status, index, expected, actual
+
+
+class Runtime:
+    """Mirror of catena's Runtime (catena-lang/src/runtime/runtime.rs:24-247)."""
+
+    def __init__(self, sources=(), dialect: str = "hip"):
+        L = lib()
+        enc = [s.encode() for s in sources]
+        arr = (ctypes.c_char_p * max(1, len(enc)))(*enc)
+        h = _vp()
+        st = L.catena_runtime_from_sources(arr, len(enc), dialect.encode(), ctypes.byref(h))
+        if st != 0:
+            raise ExecError(st, last_error(), -1, -1, -1)
+        self._h = h
+
+    def programs(self) -> list[str]:
+        L = lib()
+        return [L.catena_runtime_program_name(self._h, i).decode()
+                for i in range(L.catena_runtime_program_count(self._h))]
+
+    def mem_f32(self, values) -> Value:
+        a = np.ascontiguousarray(values, np.float32)
+        v = Value()
+        check(lib().catena_runtime_mem_f32(self._h, a.ctypes.data_as(ctypes.POINTER(_f32)), a.size,
+                                           ctypes.byref(v)))
+        return v
+
+    def mem_u64(self, values) -> Value:
+        a = np.ascontiguousarray(values, np.uint64)
+        v = Value()
+        check(lib().catena_runtime_mem_u64(self._h, a.ctypes.data_as(ctypes.POINTER(_u64)), a.size,
+                                           ctypes.byref(v)))
+        return v
+
+    def exec(self, name: str, args, n_outputs: int) -> list[Value]:
+        L = lib()
+        ins = (Value * max(1, len(args)))(*args)
+        outs = (Value * max(1, n_outputs))()
+        st = L.catena_runtime_exec(self._h, name.encode(), ins, len(args), outs, n_outputs)
+        if st != 0:
+            i, e, a = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+            L.catena_runtime_last_error_detail(ctypes.byref(i), ctypes.byref(e), ctypes.byref(a))
+            raise ExecError(st, last_error(), i.value, e.value, a.value)
+        return list(outs)[:n_outputs]
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().catena_runtime_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def mem_to_array(m: Mem, dtype) -> np.ndarray:
+    """Host copy of a runtime Mem (Mem::to_f32_vec / to_u64_vec,
+    catena-lang/src/runtime/mem.rs:44-70): asserts len % itemsize == 0."""
+    dtype = np.dtype(dtype)
+    assert m.len % dtype.itemsize == 0
+    out = np.empty(m.len // dtype.itemsize, dtype)
+    check(lib().catena_mem_read(m, 0, out.ctypes.data_as(_vp), out.nbytes))
+    return out
+
+
+def mem_free(m: Mem) -> None:
+    check(lib().catena_mem_free(ctypes.byref(m)))

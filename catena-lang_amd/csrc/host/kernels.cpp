@@ -1,0 +1,166 @@
+// Kernel ABI: shape checks, variant selection and launches.
+#include <cstdint>
+#include <cstdlib>
+
+#include "internal.h"
+
+using namespace catena;
+
+namespace {
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+
+// k per wave for the decode kernel: aim for ~1500 waves in flight (1024
+// SIMDs on MI355X), in whole 32-k MFMA steps.  CATENA_DECODE_KW overrides.
+uint32_t decode_kw(uint64_t n_cols, uint64_t k) {
+  const char* env = getenv("CATENA_DECODE_KW");
+  if (env && *env) {
+    long v = strtol(env, nullptr, 10);
+    if (v >= 32 && v % 32 == 0) return (uint32_t)v;
+  }
+  const uint64_t blocks = ceil_div(n_cols, 128);
+  uint64_t kw = ceil_div(k * blocks, 1536);
+  kw = ceil_div(kw, 32) * 32;
+  if (kw < 64) kw = 64;
+  if (kw > k) kw = ceil_div(k, 32) * 32;
+  return (uint32_t)kw;
+}
+}  // namespace
+
+extern "C" {
+
+int catena_mi355x_gemm_f32_exact(const float* a, const float* b, float* c, uint64_t n, uint64_t m,
+                                 uint64_t k) {
+  int st = ensure_init();
+  if (st) return st;
+  if (n == 0 || m == 0) return CATENA_OK;
+  if (!c || (k > 0 && (!a || !b))) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
+  const uint64_t gx = ceil_div(m, 64), gy = ceil_div(n, 64);
+  if (gx > 0x7FFFFFFFu || gy > 65535u) return fail(CATENA_ERR_UNSUPPORTED, "matrix too large");
+  void* args[] = {&a, &b, &c, &n, &m, &k};
+  return launch(KernelId::GemmF32Exact, dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, args);
+}
+
+int catena_mi355x_gemm_bf16(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, uint64_t m,
+                            uint64_t k, int out_f32) {
+  int st = ensure_init();
+  if (st) return st;
+  if (n == 0 || m == 0) return CATENA_OK;
+  if (!c || (k > 0 && (!a || !b))) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
+  Device& d = device();
+
+  // decode shape: <= 16 rows of activations against a K x N weight
+  if (n <= 16 && k > 0 && m % 8 == 0 && k % 8 == 0 && aligned16(a) && aligned16(b) &&
+      aligned16(c)) {
+    const uint32_t M = (uint32_t)n;
+    const uint32_t kw = decode_kw(m, k);
+    const uint64_t chunks = ceil_div(k, kw);
+    const uint64_t S = ceil_div(chunks, 4);
+    const uint64_t gx = ceil_div(m, 128);
+    if (S > 65535 || gx > 0x7FFFFFFFu) return fail(CATENA_ERR_UNSUPPORTED, "decode grid too large");
+    if (out_f32 == 0) {
+      float* P = nullptr;
+      if (S > 1) {
+        void* ws = nullptr;
+        st = workspace(S * M * m * sizeof(float), &ws);
+        if (st) return st;
+        P = static_cast<float*>(ws);
+      }
+      const uint16_t* X = a;
+      const uint16_t* W = b;
+      uint16_t* Y = static_cast<uint16_t*>(c);
+      uint64_t N = m, K = k;
+      void* args[] = {&X, &W, &Y, &P, (void*)&M, &N, &K, (void*)&kw};
+      st = launch(KernelId::GemmBf16Decode, dim3((unsigned)gx, (unsigned)S), dim3(256), 0, args);
+      if (st || S == 1) return st;
+      uint32_t S32 = (uint32_t)S;
+      const uint64_t total4 = (uint64_t)M * m / 4;
+      const float* Pc = P;
+      void* rargs[] = {&Pc, &Y, (void*)&M, &N, &S32};
+      return launch(KernelId::GemmBf16DecodeReduce, dim3((unsigned)ceil_div(total4, 256)), dim3(256),
+                    0, rargs);
+    }
+  }
+
+  const bool tile_ok = n % 256 == 0 && m % 256 == 0 && k % 64 == 0 && k > 0 && aligned16(a) &&
+                       aligned16(b);
+  const size_t lds = 2ull * 2 * 256 * 72 * sizeof(uint16_t);  // 147456 B
+  if (lds > d.max_lds) return fail(CATENA_ERR_UNSUPPORTED, "device LDS %zu < %zu", d.max_lds, lds);
+  const uint64_t tiles = ceil_div(n, 256) * ceil_div(m, 256);
+  if (tiles > 0x7FFFFFFFu) return fail(CATENA_ERR_UNSUPPORTED, "matrix too large");
+  KernelId id = tile_ok ? (out_f32 ? KernelId::GemmBf16TileF32 : KernelId::GemmBf16TileBf16)
+                        : (out_f32 ? KernelId::GemmBf16EdgeF32 : KernelId::GemmBf16EdgeBf16);
+  void* args[] = {&a, &b, &c, &n, &m, &k};
+  return launch(id, dim3((unsigned)tiles), dim3(256), lds, args);
+}
+
+int catena_mi355x_attn_decode_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                   const uint32_t* lens, float* o, uint32_t batch, uint32_t heads,
+                                   uint32_t max_len, uint32_t head_dim, float scale) {
+  int st = ensure_init();
+  if (st) return st;
+  if (head_dim != 128)
+    return fail(CATENA_ERR_UNSUPPORTED, "attention head_dim %u unsupported (only 128)", head_dim);
+  const uint64_t bh = (uint64_t)batch * heads;
+  if (bh == 0) return CATENA_OK;
+  if (!q || !lens || !o || (max_len > 0 && (!k || !v)))
+    return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
+  if (!aligned16(k) || !aligned16(v))
+    return fail(CATENA_ERR_INVALID_ARGUMENT, "K/V caches must be 16-byte aligned");
+  if (bh > 0x7FFFFFFFu) return fail(CATENA_ERR_UNSUPPORTED, "too many heads");
+  Device& d = device();
+  const size_t lds = 128 * 4 + 20480 + 64 + (size_t)max_len * 4;
+  if (lds > d.max_lds)
+    return fail(CATENA_ERR_UNSUPPORTED, "max_len %u needs %zu B of LDS (device has %zu)", max_len,
+                lds, d.max_lds);
+  void* args[] = {&q, &k, &v, &lens, &o, &heads, &max_len, &scale};
+  return launch(KernelId::AttnDecodeD128, dim3((unsigned)bh), dim3(256), lds, args);
+}
+
+int catena_mi355x_softmax_f32(const float* x, float* y, uint64_t rows, uint64_t n) {
+  int st = ensure_init();
+  if (st) return st;
+  if (rows == 0 || n == 0) return CATENA_OK;
+  if (!x || !y) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
+  if (n >= 0x7FFFFFFFull) return fail(CATENA_ERR_UNSUPPORTED, "softmax length too large");
+  if (rows > 0x7FFFFFFFull) return fail(CATENA_ERR_UNSUPPORTED, "too many rows");
+  void* args[] = {&x, &y, &n};
+  return launch(KernelId::SoftmaxRows, dim3((unsigned)rows), dim3(256), 0, args);
+}
+
+int catena_mi355x_exp_approx_f32(const float* x, float* y, uint64_t n) {
+  int st = ensure_init();
+  if (st) return st;
+  if (n == 0) return CATENA_OK;
+  if (!x || !y) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
+  const uint64_t g = ceil_div(n, 256);
+  if (g > 0x7FFFFFFFull) return fail(CATENA_ERR_UNSUPPORTED, "too many elements");
+  void* args[] = {&x, &y, &n};
+  return launch(KernelId::ExpApprox, dim3((unsigned)g), dim3(256), 0, args);
+}
+
+int catena_mi355x_fill_normal_bf16(uint16_t* out, uint64_t n, uint64_t seed, uint64_t stream,
+                                   float scale) {
+  int st = ensure_init();
+  if (st) return st;
+  if (n == 0) return CATENA_OK;
+  if (!out) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
+  const uint64_t g = ceil_div(n, 256);
+  if (g > 0x7FFFFFFFull) return fail(CATENA_ERR_UNSUPPORTED, "too many elements");
+  void* args[] = {&out, &n, &seed, &stream, &scale};
+  return launch(KernelId::FillNormalBf16, dim3((unsigned)g), dim3(256), 0, args);
+}
+
+int catena_mi355x_fill_uniform_f32(float* out, uint64_t n, uint64_t seed, uint64_t stream) {
+  int st = ensure_init();
+  if (st) return st;
+  if (n == 0) return CATENA_OK;
+  if (!out) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
+  const uint64_t g = ceil_div(n, 256);
+  if (g > 0x7FFFFFFFull) return fail(CATENA_ERR_UNSUPPORTED, "too many elements");
+  void* args[] = {&out, &n, &seed, &stream};
+  return launch(KernelId::FillUniformF32, dim3((unsigned)g), dim3(256), 0, args);
+}
+
+}  // extern "C"

@@ -1,0 +1,252 @@
+// KV-cache decode attention (one query token per sequence), bf16 cache,
+// f32 softmax, f32 output, bitwise equal to the sequential composition of
+// the reference's own pieces:
+//   s_t = (fold_{d asc} from +0 of q_d * k_{t,d}) * scale
+//         -- f32.matmul.cell-dot order, catena-lang/stdlib/matrix.hex:236-256
+//   m   = f32.max-env fold from -inf        (catena-lang/stdlib/sum.hex:73-84)
+//   den = f32.add-env fold from +0 of exp~(s_t - m)  (catena-lang/stdlib/nn.hex:93-114)
+//   p_t = exp~(s_t - m) / den                (catena-lang/stdlib/nn.hex:75-90)
+//   o_d = fold_{t asc} from +0 of p_t * v_{t,d}
+// exp~ is math.exp-approx (catena-lang/stdlib/math.hex:148-199).
+//
+// One workgroup (4 waves) per (batch, head); layouts q[B][H][128],
+// k/v[B][H][L][128] (bf16, head-major, one 256-byte row per position),
+// lens[B] (positions used per sequence, clamped to L), o[B][H][128] f32.
+//
+// K pass: each wave takes 64-row blocks (blocks w, w+4, ...).  A block is
+// moved in four 32-wide d segments: a coalesced 16-byte-per-lane global load
+// (4 lanes per 64-byte row segment), a write into the wave's private LDS
+// slice, and a read back in which lane l owns row l, so every score is one
+// lane's d-ascending chain of v_mul_f32 + v_add_f32.  The next segment's
+// loads are issued before the current one is folded.
+// Softmax: the max is the exact parallel form of the sequential fold (see
+// FirstMax in common.h); exp~ is elementwise; the denominator is the one
+// truly sequential fold and runs in one lane over LDS; p_t is one correctly
+// rounded division per element.
+// V pass: waves 0 and 1 own 64 output columns each (lane = column) and walk
+// t ascending through 64-row batches staged in LDS, with the next batch's
+// loads in flight while the current one is folded.  Every K and V byte is
+// read from HBM once.
+#include "common.h"
+
+namespace {
+constexpr int D = 128;
+constexpr int KSTAGE_ROW = 80;                // bytes: 64 B of data + 16 B pad
+constexpr int KSTAGE_WAVE = 64 * KSTAGE_ROW;  // 5120 B per wave
+constexpr int STAGE_BYTES = 4 * KSTAGE_WAVE;  // 20480 B (V pass uses 2 x 8192)
+
+CATENA_DEV void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+CATENA_DEV int wave_max_i32(int v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    int o = __shfl_xor(v, off, 64);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+CATENA_DEV FirstMax wave_first_max(FirstMax a) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    FirstMax b;
+    b.v = __shfl_xor(a.v, off, 64);
+    b.i = (uint32_t)__shfl_xor((int)a.i, off, 64);
+    a = first_max_combine(a, b);
+  }
+  return a;
+}
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(256) void catena_attn_decode_bf16_d128(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ v, const uint32_t* __restrict__ lens, float* __restrict__ o,
+    uint32_t H, uint32_t L, float scale) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  float* qf = reinterpret_cast<float*>(smem);                  // [128]
+  unsigned char* stage = smem + D * 4;                         // [STAGE_BYTES]
+  int* red_i = reinterpret_cast<int*>(smem + D * 4 + STAGE_BYTES);        // [4]
+  float* red_v = reinterpret_cast<float*>(red_i + 4);                     // [4]
+  uint32_t* red_u = reinterpret_cast<uint32_t*>(red_v + 4);               // [4]
+  float* sp = reinterpret_cast<float*>(smem + D * 4 + STAGE_BYTES + 64);  // [L]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const uint64_t bh = blockIdx.x;
+  const uint32_t b = (uint32_t)(bh / H);
+  uint32_t len = lens[b];
+  if (len > L) len = L;
+
+  const uint16_t* kb = k + bh * (uint64_t)L * D;
+  const uint16_t* vb = v + bh * (uint64_t)L * D;
+  if (tid < D) qf[tid] = bf16_to_f32(q[bh * D + tid]);
+  __syncthreads();
+
+  // ---------------------------------------------------------------- K pass
+  {
+    unsigned char* st = stage + wave * KSTAGE_WAVE;
+    const uint32_t nblk = (len + 63) / 64;
+    // this wave's (block, segment) steps, flattened
+    const uint32_t my_blocks = nblk > (uint32_t)wave ? (nblk - wave + 3) / 4 : 0;
+    const uint32_t steps = my_blocks * 4;
+    const int lrow = lane >> 2, lchunk = lane & 3;
+    auto gload = [&](uint32_t step, u32x4_t r[4]) {
+      const uint32_t blk = wave + 4 * (step >> 2), seg = step & 3;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t t = blk * 64 + lrow + 16 * i;
+        if (t < len)
+          r[i] = __builtin_nontemporal_load(
+              reinterpret_cast<const u32x4_t*>(kb + (uint64_t)t * D + seg * 32 + lchunk * 8));
+        else
+          r[i] = u32x4_t{0u, 0u, 0u, 0u};
+      }
+    };
+    u32x4_t cur[4], nxt[4];
+    if (steps) gload(0, cur);
+    float acc = __uint_as_float(0u);
+    for (uint32_t step = 0; step < steps; ++step) {
+      const uint32_t seg = step & 3;
+      const bool more = step + 1 < steps;
+      if (more) gload(step + 1, nxt);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<u32x4_t*>(st + (lrow + 16 * i) * KSTAGE_ROW + lchunk * 16) = cur[i];
+      wave_sync();
+      if (seg == 0) acc = __uint_as_float(0u);
+      const unsigned char* myrow = st + lane * KSTAGE_ROW;
+#pragma unroll
+      for (int ch = 0; ch < 4; ++ch) {
+        const u32x4_t kv = *reinterpret_cast<const u32x4_t*>(myrow + ch * 16);
+        const f32x4_t q0 = *reinterpret_cast<const f32x4_t*>(qf + seg * 32 + ch * 8);
+        const f32x4_t q1 = *reinterpret_cast<const f32x4_t*>(qf + seg * 32 + ch * 8 + 4);
+        float p;
+        p = q0[0] * bf16lo(kv[0]); acc = acc + p;
+        p = q0[1] * bf16hi(kv[0]); acc = acc + p;
+        p = q0[2] * bf16lo(kv[1]); acc = acc + p;
+        p = q0[3] * bf16hi(kv[1]); acc = acc + p;
+        p = q1[0] * bf16lo(kv[2]); acc = acc + p;
+        p = q1[1] * bf16hi(kv[2]); acc = acc + p;
+        p = q1[2] * bf16lo(kv[3]); acc = acc + p;
+        p = q1[3] * bf16hi(kv[3]); acc = acc + p;
+      }
+      if (seg == 3) {
+        const uint32_t t = (wave + 4 * (step >> 2)) * 64 + lane;
+        if (t < len) sp[t] = acc * scale;
+      }
+      wave_sync();
+      if (more) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cur[i] = nxt[i];
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---------------------------------------------------------------- max
+  int lastnan = -1;
+  for (uint32_t t = tid; t < len; t += 256)
+    if (sp[t] != sp[t]) lastnan = (int)t;
+  lastnan = wave_max_i32(lastnan);
+  if (lane == 0) red_i[wave] = lastnan;
+  __syncthreads();
+  int J = red_i[0];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) J = red_i[w] > J ? red_i[w] : J;
+
+  FirstMax fm{__uint_as_float(0xFF800000u), 0xFFFFFFFFu};
+  for (uint32_t t = tid; t < len; t += 256)
+    if ((int)t > J) fm = first_max_combine(fm, FirstMax{sp[t], t});
+  fm = wave_first_max(fm);
+  if (lane == 0) {
+    red_v[wave] = fm.v;
+    red_u[wave] = fm.i;
+  }
+  __syncthreads();
+  FirstMax all{red_v[0], red_u[0]};
+#pragma unroll
+  for (int w = 1; w < 4; ++w) all = first_max_combine(all, FirstMax{red_v[w], red_u[w]});
+  float mx;
+  if (len > 0 && J == (int)len - 1)
+    mx = sp[len - 1];
+  else
+    mx = (all.i == 0xFFFFFFFFu) ? __uint_as_float(0xFF800000u) : all.v;
+  __syncthreads();  // everyone has read sp[len-1] / red_* before sp is rewritten
+
+  // ---------------------------------------------------------------- exp~, denominator
+  for (uint32_t t = tid; t < len; t += 256) {
+    const float shifted = sp[t] - mx;
+    sp[t] = exp_approx(shifted);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float den = __uint_as_float(0u);
+    const uint32_t n4 = len / 4;
+    const f32x4_t* s4 = reinterpret_cast<const f32x4_t*>(sp);
+    for (uint32_t i = 0; i < n4; ++i) {
+      const f32x4_t e = s4[i];
+      den = den + e[0];
+      den = den + e[1];
+      den = den + e[2];
+      den = den + e[3];
+    }
+    for (uint32_t t = n4 * 4; t < len; ++t) den = den + sp[t];
+    red_v[0] = den;
+  }
+  __syncthreads();
+  const float den = red_v[0];
+  for (uint32_t t = tid; t < len; t += 256) sp[t] = sp[t] / den;
+  __syncthreads();
+
+  // ---------------------------------------------------------------- V pass
+  if (wave >= 2) return;
+  {
+    unsigned char* st = stage + wave * 8192;  // [64 rows][64 cols] bf16
+    const int vrow = lane >> 3, vchunk = lane & 7;
+    const uint64_t colbase = (uint64_t)wave * 64;
+    const uint32_t nb = (len + 63) / 64;
+    auto gload = [&](uint32_t bt, u32x4_t r[8]) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t t = bt * 64 + vrow + 8 * i;
+        if (t < len)
+          r[i] = __builtin_nontemporal_load(
+              reinterpret_cast<const u32x4_t*>(vb + (uint64_t)t * D + colbase + vchunk * 8));
+        else
+          r[i] = u32x4_t{0u, 0u, 0u, 0u};
+      }
+    };
+    u32x4_t rv[8];
+    if (nb) gload(0, rv);
+    float acc = __uint_as_float(0u);
+    const uint16_t* st16 = reinterpret_cast<const uint16_t*>(st);
+    for (uint32_t bt = 0; bt < nb; ++bt) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        *reinterpret_cast<u32x4_t*>(st + (vrow + 8 * i) * 128 + vchunk * 16) = rv[i];
+      wave_sync();
+      if (bt + 1 < nb) gload(bt + 1, rv);
+      const uint32_t t0 = bt * 64;
+      const uint32_t rows = (len - t0) < 64u ? (len - t0) : 64u;
+      if (rows == 64) {
+#pragma unroll 16
+        for (uint32_t r = 0; r < 64; ++r) {
+          const float pv = sp[t0 + r];
+          const float prod = pv * bf16_to_f32(st16[r * 64 + lane]);
+          acc = acc + prod;
+        }
+      } else {
+        for (uint32_t r = 0; r < rows; ++r) {
+          const float prod = sp[t0 + r] * bf16_to_f32(st16[r * 64 + lane]);
+          acc = acc + prod;
+        }
+      }
+      wave_sync();
+    }
+    o[bh * D + colbase + lane] = acc;
+  }
+}

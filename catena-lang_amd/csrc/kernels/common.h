@@ -1,0 +1,114 @@
+// Device-side helpers shared by the gfx950 kernels.
+//
+// Every kernel in this directory is compiled with -ffp-contract=off
+// -fno-fast-math (build.py), the flag contract of the reference's generated
+// module (catena-lang/src/runtime/artifact.rs:59-71): `a * b + c` stays a
+// separately rounded multiply and add, never an FMA.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+#define CATENA_DEV __device__ __forceinline__
+
+// catena_u32_bitcast_f32 / catena_f32_bitcast_u32
+// (catena-lang/src/codegen/prelude.rs:64-80)
+CATENA_DEV float u32_as_f32(uint32_t b) { return __uint_as_float(b); }
+CATENA_DEV uint32_t f32_as_u32(float f) { return __float_as_uint(f); }
+
+// Exact bf16 -> f32 widening of the low / high half of a packed dword.
+CATENA_DEV float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+CATENA_DEV float bf16hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+CATENA_DEV float bf16_to_f32(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+
+// f32 -> bf16 round-to-nearest-even; NaN keeps sign and top payload and is
+// made quiet.  Integer formulation so the CPU oracle (or_f32_to_bf16) and the
+// device agree bit for bit.
+CATENA_DEV uint32_t f32_to_bf16_bits(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x0040u;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+CATENA_DEV uint32_t pack_bf16x2(float lo, float hi) {
+  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+}
+
+// f32.round-to-u32 = (uint32_t)nearbyintf(x) (catena-lang/src/codegen/
+// gpu.rs:642-655), with the device conversion's defined behaviour spelled
+// out: NaN and values <= 0 give 0, values >= 2^32 saturate.
+CATENA_DEV uint32_t round_to_u32(float x) {
+  float r = __builtin_rintf(x);
+  if (r != r) return 0u;
+  if (r <= 0.0f) return 0u;
+  if (r >= 4294967296.0f) return 0xFFFFFFFFu;
+  return (uint32_t)r;
+}
+
+// math.exp-approx-nonneg (catena-lang/stdlib/math.hex:148-183); one IEEE
+// operation per hexpr node, operands in source order.
+CATENA_DEV float exp_approx_nonneg(float x) {
+  const float inv_ln2 = u32_as_f32(0x3FB8AA3Bu);
+  const float ln2_hi = u32_as_f32(0x3F317200u);
+  const float ln2_lo = u32_as_f32(0x35BFBE8Eu);
+  const float c0 = u32_as_f32(0x3F7FF8FCu);
+  const float c1 = u32_as_f32(0x3F809C7Eu);
+  const float c2 = u32_as_f32(0x3EEF1187u);
+  const float c3 = u32_as_f32(0x3E738A8Bu);
+  float scaled = x * inv_ln2;
+  uint32_t k_u32 = round_to_u32(scaled);
+  float k_f32 = (float)k_u32;
+  float k_ln2_hi = k_f32 * ln2_hi;
+  float k_ln2_lo = k_f32 * ln2_lo;
+  float r1 = x - k_ln2_hi;
+  float xr = r1 - k_ln2_lo;
+  float xr_c3 = xr * c3;
+  float p2 = c2 + xr_c3;
+  float xr_p2 = xr * p2;
+  float p1 = c1 + xr_p2;
+  float xr_p1 = xr * p1;
+  float poly = c0 + xr_p1;
+  uint32_t biased = k_u32 + 0x7Fu;           // u32.add wraps
+  uint32_t pow2_bits = biased * 0x00800000u;  // u32.mul wraps
+  return poly * u32_as_f32(pow2_bits);
+}
+
+// math.exp-approx (catena-lang/stdlib/math.hex:185-199)
+CATENA_DEV float exp_approx(float x) {
+  const float zero = (float)0u;
+  const float one = u32_as_f32(0x3F800000u);
+  float neg_x = -x;
+  bool is_negative = x < zero;
+  float magnitude = is_negative ? neg_x : x;
+  float base = exp_approx_nonneg(magnitude);
+  float reciprocal = one / base;  // correctly rounded (no fast-math)
+  return is_negative ? reciprocal : base;
+}
+
+// Exact parallel form of the f32.max-env fold (catena-lang/stdlib/
+// sum.hex:73-84: acc = (acc >= x) ? acc : x from acc = -inf, ascending).
+// Without NaNs the fold returns the FIRST element that compares equal to the
+// maximum (ties, including +0 == -0, keep the earlier one).  A NaN resets
+// the fold: the result is then the last NaN itself if it is the final
+// element, otherwise the first-max of the elements after the last NaN.
+// Callers reduce (last_nan_index) first, then (value, index) pairs over the
+// indices after it with first_max_combine, which is associative and
+// commutative, so any reduction tree gives the sequential fold's bits.
+struct FirstMax {
+  float v;
+  uint32_t i;  // 0xFFFFFFFF = empty (-inf sentinel)
+};
+
+CATENA_DEV FirstMax first_max_combine(FirstMax a, FirstMax b) {
+  if (a.i == 0xFFFFFFFFu) return b;
+  if (b.i == 0xFFFFFFFFu) return a;
+  if (a.v > b.v) return a;
+  if (b.v > a.v) return b;
+  return (a.i < b.i) ? a : b;  // equal (incl. +0/-0): earlier index wins
+}

@@ -1,0 +1,235 @@
+/*
+ * catena_mi355x.h -- C ABI of the MI355X-native catena hot path.
+ *
+ * Two layers, both plain C (pointers, sizes, status codes; no torch types):
+ *
+ *  1. The program ABI that catena's generated module exports and that its
+ *     runtime calls through libffi (catena-lang/src/runtime/executor.rs:47-106,
+ *     signature table catena-lang/src/runtime/signature.rs:18-72, emitted by
+ *     catena-lang/src/codegen/gpu.rs:235-285).  Symbols are
+ *     `program_` + the source name with every non-alphanumeric mapped to `_`
+ *     (catena-lang/src/codegen/mod.rs:379-388); inputs by value, outputs as
+ *     pointers, return void, and assertion / GPU failures are fail-stop
+ *     (message on stderr, then a trap: catena-lang/src/codegen/prelude.rs:38-55).
+ *
+ *  2. The kernel ABI those programs lower to ("catena_mi355x_*"), which
+ *     returns a status and never traps, plus the device buffer pool that
+ *     replaces the reference's per-buffer managed allocation
+ *     (catena-lang/src/runtime/mem.rs:152-171, hipFree on drop :119-125).
+ *
+ *  3. The runtime mirror ("catena_runtime_*") of Runtime::from_sources /
+ *     Runtime::exec / Value (catena-lang/src/runtime/runtime.rs:104-247,
+ *     catena-lang/src/runtime/value.rs:5-49).
+ *
+ * Everything runs on one device and one library-owned HIP stream.  Kernel
+ * ABI calls are stream-ordered (asynchronous); program ABI calls and
+ * catena_runtime_exec synchronise before returning, like the generated host
+ * wrapper (catena-lang/src/codegen/ops/materializec.rs:123-141).
+ */
+#ifndef CATENA_MI355X_H
+#define CATENA_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* catena_mem_t: by-value fat pointer, len in BYTES.
+ * Reference: catena-lang/src/codegen/prelude.rs:28-31 and
+ * catena-lang/src/runtime/executor.rs:14-19 (CatenaMem).  Here `data` is a
+ * device pointer owned by the pool; len == 0 means data == NULL
+ * (catena-lang/src/codegen/ops/materializec.rs:114). */
+typedef struct catena_mem {
+  void *data;
+  uint64_t len;
+} catena_mem_t;
+
+typedef enum catena_status {
+  CATENA_OK = 0,
+  CATENA_ERR_INVALID_ARGUMENT = 1,
+  CATENA_ERR_UNSUPPORTED = 2,
+  CATENA_ERR_HIP = 3,
+  CATENA_ERR_OUT_OF_MEMORY = 4,
+  CATENA_ERR_NOT_INITIALIZED = 5,
+  CATENA_ERR_LOAD = 6
+} catena_status_t;
+
+/* ------------------------------------------------------------------ */
+/* library / device                                                     */
+
+/* Select the device, create the library stream, load the gfx950 code
+ * objects (hipModuleLoad) that sit next to this library.  Idempotent.
+ * Replaces GpuRuntime::load (catena-lang/src/runtime/mem.rs:134-150) and the
+ * per-Runtime hipcc + dlopen of catena-lang/src/runtime/artifact.rs:44-103. */
+int catena_mi355x_init(int device);
+/* Message of the last failing call on this thread ("" if none). */
+const char *catena_mi355x_last_error(void);
+/* The hipStream_t every launch goes to (for events / interop). */
+void *catena_mi355x_stream(void);
+int catena_mi355x_synchronize(void);
+
+/* ------------------------------------------------------------------ */
+/* device buffer pool                                                    */
+
+/* Allocate len bytes of device memory (size-classed, cached free lists).
+ * Replaces Mem allocation (catena-lang/src/runtime/mem.rs:152-171). */
+int catena_mem_alloc(uint64_t len, catena_mem_t *out);
+/* Return a buffer to the pool and null the handle.  Stream-ordered: work
+ * already queued on the library stream may still use it.  Replaces
+ * Mem::drop -> hipFree (catena-lang/src/runtime/mem.rs:119-125). */
+int catena_mem_free(catena_mem_t *mem);
+/* Host <-> device copies (synchronous).  catena_mem_read replaces the raw
+ * host dereference of managed memory in Mem::to_f32_vec / to_u64_vec
+ * (catena-lang/src/runtime/mem.rs:44-70). */
+int catena_mem_write(catena_mem_t mem, uint64_t offset, const void *src, uint64_t len);
+int catena_mem_read(catena_mem_t mem, uint64_t offset, void *dst, uint64_t len);
+int catena_pool_stats(uint64_t *bytes_live, uint64_t *bytes_cached, uint64_t *device_allocs);
+/* Release every cached (free) block back to the device. */
+int catena_pool_trim(void);
+
+/* ------------------------------------------------------------------ */
+/* kernel ABI (device pointers; stream-ordered)                         */
+
+/* C[n x m] = A[n x k] * B[k x m], f32, row-major, each cell the
+ * k-ascending fold acc = acc + A*B from +0.0 with no FMA: bitwise the
+ * reference's f32.matmul.row-major.materialize
+ * (catena-lang/stdlib/matrix.hex:236-327, lowered by
+ * catena-lang/src/codegen/ops/materializec.rs:36-82 and
+ * catena-lang/src/codegen/ops/reducec.rs:73-130). */
+int catena_mi355x_gemm_f32_exact(const float *a, const float *b, float *c, uint64_t n,
+                                 uint64_t m, uint64_t k);
+
+/* C[n x m] = A[n x k] * B[k x m] on bf16 inputs (raw bf16 bits), f32
+ * accumulation on MFMA in a fixed order, output bf16 (RNE) or f32 when
+ * out_f32 != 0.  Same contraction as above, extended to bf16 (no reference
+ * counterpart: catena has no bf16, catena-lang/src/codegen/lower_types.rs:13-22).
+ * n <= 16 (decode shape) uses the weight-streaming kernel. */
+int catena_mi355x_gemm_bf16(const uint16_t *a, const uint16_t *b, void *c, uint64_t n,
+                            uint64_t m, uint64_t k, int out_f32);
+
+/* Decode attention, one query per (batch, head): q[B][H][D], k/v[B][H][L][D]
+ * bf16, lens[B] (device u32, each <= L), o[B][H][D] f32.  Bitwise the
+ * sequential composition of cell-dot, nn.softmax and cell-dot
+ * (catena-lang/stdlib/matrix.hex:236-256, catena-lang/stdlib/nn.hex:93-122,
+ * catena-lang/stdlib/math.hex:148-199).  No reference counterpart (catena
+ * has no attention primitive).  head_dim must be 128. */
+int catena_mi355x_attn_decode_bf16(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                                   const uint32_t *lens, float *o, uint32_t batch,
+                                   uint32_t heads, uint32_t max_len, uint32_t head_dim,
+                                   float scale);
+
+/* nn.softmax over `rows` contiguous vectors of length n (bitwise the
+ * reference's fold order; catena-lang/stdlib/nn.hex:93-122).  y may equal x. */
+int catena_mi355x_softmax_f32(const float *x, float *y, uint64_t rows, uint64_t n);
+
+/* math.exp-approx elementwise (catena-lang/stdlib/math.hex:185-199). */
+int catena_mi355x_exp_approx_f32(const float *x, float *y, uint64_t n);
+
+/* Seeded synthetic inputs (counter-based splitmix64; see fill.hip). */
+int catena_mi355x_fill_normal_bf16(uint16_t *out, uint64_t n, uint64_t seed, uint64_t stream,
+                                   float scale);
+int catena_mi355x_fill_uniform_f32(float *out, uint64_t n, uint64_t seed, uint64_t stream);
+
+/* ------------------------------------------------------------------ */
+/* program ABI (generated-module symbols; synchronous; fail-stop)        */
+
+/* tests/cases/matrix/matmul.hex:1-63 "matmul-2x2-via-mem":
+ * (mem A, mem B, n, m, k, nk, km, nm) -> (mem C).  Asserts nk == len(A)/4 and
+ * km == len(B)/4 like the reference, and additionally n*k == nk, k*m == km,
+ * n*m == nm (the reference leaves those to its type checker). */
+void program_matmul_2x2_via_mem(catena_mem_t a, catena_mem_t b, uint64_t n, uint64_t m,
+                                uint64_t k, uint64_t nk, uint64_t km, uint64_t nm,
+                                catena_mem_t *out);
+/* tests/cases/matrix/matmul.hex:65-106 / :108-147: A * I and I * A. */
+void program_matmul_right_identity_2x2_via_mem(catena_mem_t a, uint64_t n, uint64_t nn,
+                                               catena_mem_t *out);
+void program_matmul_left_identity_2x2_via_mem(catena_mem_t a, uint64_t n, uint64_t nn,
+                                              catena_mem_t *out);
+/* catena-lang/stdlib/nn.hex:93-122 "nn.softmax": (mem) -> (mem). */
+void program_nn_softmax(catena_mem_t x, catena_mem_t *out);
+/* catena-lang/stdlib/math.hex:185-199 "math.exp-approx": (f32) -> (f32). */
+void program_math_exp_approx(float x, float *out);
+/* bf16 analogue of matmul-2x2-via-mem (no reference counterpart):
+ * (mem A bf16, mem B bf16, n, m, k, nk, km, nm) -> (mem C bf16). */
+void program_bf16_matmul_via_mem(catena_mem_t a, catena_mem_t b, uint64_t n, uint64_t m,
+                                 uint64_t k, uint64_t nk, uint64_t km, uint64_t nm,
+                                 catena_mem_t *out);
+/* Decode attention as a program (no reference counterpart):
+ * (mem q, mem k, mem v, mem lens u32, batch, heads, max_len, head_dim, f32 scale)
+ * -> (mem o f32). */
+void program_attn_decode_via_mem(catena_mem_t q, catena_mem_t k, catena_mem_t v,
+                                 catena_mem_t lens, uint64_t batch, uint64_t heads,
+                                 uint64_t max_len, uint64_t head_dim, float scale,
+                                 catena_mem_t *out);
+
+/* ------------------------------------------------------------------ */
+/* runtime mirror                                                         */
+
+/* ValueKind, catena-lang/src/runtime/value.rs:15-21 */
+typedef enum catena_value_kind {
+  CATENA_VALUE_BOOL = 0,
+  CATENA_VALUE_U32 = 1,
+  CATENA_VALUE_U64 = 2,
+  CATENA_VALUE_F32 = 3,
+  CATENA_VALUE_MEM = 4
+} catena_value_kind_t;
+
+/* Value, catena-lang/src/runtime/value.rs:5-12 */
+typedef struct catena_value {
+  catena_value_kind_t kind;
+  union {
+    uint8_t b;
+    uint32_t u32;
+    uint64_t u64;
+    float f32;
+    catena_mem_t mem;
+  } as;
+} catena_value_t;
+
+/* ExecError / InitError kinds, catena-lang/src/runtime/runtime.rs:36-102 */
+typedef enum catena_exec_status {
+  CATENA_EXEC_OK = 0,
+  CATENA_EXEC_UNKNOWN_SOURCE_FUNCTION = 1,
+  CATENA_EXEC_INPUT_ARITY_MISMATCH = 2,
+  CATENA_EXEC_OUTPUT_ARITY_MISMATCH = 3,
+  CATENA_EXEC_TYPE_MISMATCH = 4,
+  CATENA_INIT_PARSE = 10,
+  CATENA_INIT_NO_LOWERING = 11,
+  CATENA_INIT_SIGNATURE_MISMATCH = 12,
+  CATENA_INIT_DIALECT = 13,
+  CATENA_INIT_DEVICE = 14
+} catena_exec_status_t;
+
+typedef struct catena_runtime catena_runtime_t;
+
+/* Runtime::from_sources (catena-lang/src/runtime/runtime.rs:115-121).
+ * `dialect` is "hip" (the only accepted GpuDialect here).  Sources are
+ * scanned for `(def program NAME : TYPE = ...)` forms; every declared
+ * program with a native lowering becomes executable, its signature taken
+ * from the declared type. */
+int catena_runtime_from_sources(const char *const *sources, size_t n_sources,
+                                const char *dialect, catena_runtime_t **out);
+void catena_runtime_destroy(catena_runtime_t *rt);
+/* Runtime::exec (catena-lang/src/runtime/runtime.rs:175-236): validation in
+ * the reference's order (unknown name, input arity, output arity, kinds);
+ * outputs are written to outs[0..n_outs). */
+int catena_runtime_exec(catena_runtime_t *rt, const char *name, const catena_value_t *args,
+                        size_t n_args, catena_value_t *outs, size_t n_outs);
+/* Details of the last runtime error on this thread (index / expected /
+ * actual for TypeMismatch, expected / actual counts for arity errors). */
+int catena_runtime_last_error_detail(int64_t *index, int64_t *expected, int64_t *actual);
+/* Number of executable programs and their names (for listing). */
+size_t catena_runtime_program_count(const catena_runtime_t *rt);
+const char *catena_runtime_program_name(const catena_runtime_t *rt, size_t i);
+/* Runtime::mem_u64 / mem_f32 (catena-lang/src/runtime/runtime.rs:166-172). */
+int catena_runtime_mem_u64(catena_runtime_t *rt, const uint64_t *values, size_t n,
+                           catena_value_t *out);
+int catena_runtime_mem_f32(catena_runtime_t *rt, const float *values, size_t n,
+                           catena_value_t *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

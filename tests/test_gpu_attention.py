@@ -1,0 +1,112 @@
+"""GPU parity of KV-cache decode attention: bitwise against the oracle.
+
+The kernel reproduces every fold of the oracle in the same order (scores:
+d ascending per position; max: exact parallel form of the sequential fold;
+denominator and output: t ascending), so outputs must match bit for bit,
+including ragged lengths, empty and single-position sequences, NaN scores,
+and the full benchmark shape.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import catena_amd as ca
+import oracle
+from gpu_util import dev_normal_bf16, hash_bits, say
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _init():
+    say("init device 0")
+    ca.init(0)
+
+
+def _run(q, k, v, lens, B, H, L, scale):
+    lb = ca.Buffer.from_array(np.asarray(lens, np.uint32))
+    o = ca.Buffer(B * H * D * 4)
+    ca.attn_decode_bf16(q, k, v, lb, o, B, H, L, D, scale)
+    return o.read(np.float32, (B, H, D))
+
+
+def _bitwise(got, want):
+    gn, wn = np.isnan(got), np.isnan(want)
+    assert np.array_equal(gn, wn)
+    assert np.array_equal(got[~gn].view(np.uint32), want[~wn].view(np.uint32))
+
+
+@pytest.mark.parametrize("B,H,L,lens", [
+    (2, 3, 100, [100, 37]),
+    (4, 2, 257, [0, 1, 64, 257]),
+    (3, 1, 1000, [65, 999, 128]),
+    (1, 4, 4096, [4096]),
+])
+def test_attention_bitwise_small(B, H, L, lens):
+    say(f"attention B={B} H={H} L={L} lens={lens}")
+    seed = B * 1000 + H * 100 + L
+    q = dev_normal_bf16(B * H * D, seed, 0)
+    k = dev_normal_bf16(B * H * L * D, seed, 1)
+    v = dev_normal_bf16(B * H * L * D, seed, 2)
+    scale = 1.0 / math.sqrt(D)
+    got = _run(q, k, v, lens, B, H, L, scale)
+    want = oracle.attn_decode(q.read(np.uint16, (B, H, D)), k.read(np.uint16, (B, H, L, D)),
+                              v.read(np.uint16, (B, H, L, D)), np.array(lens, np.uint32), scale)
+    _bitwise(got, want)
+
+
+def test_attention_nan_and_inf_scores():
+    B, H, L = 1, 4, 70
+    rng = np.random.default_rng(8)
+    q16 = oracle.f32_to_bf16_bits_np(rng.normal(0, 1, (B, H, D)).astype(np.float32))
+    k32 = rng.normal(0, 1, (B, H, L, D)).astype(np.float32)
+    k32[0, 0, 10, 5] = np.nan          # NaN in the middle: fold restarts after it
+    k32[0, 1, L - 1, 0] = np.nan       # NaN at the last position: max is NaN
+    k32[0, 2, 3, :] = 1e30             # +inf score
+    k32[0, 3, :, :] = 0.0              # all scores equal (+0): ties
+    k16 = oracle.f32_to_bf16_bits_np(k32)
+    v16 = oracle.f32_to_bf16_bits_np(rng.normal(0, 1, (B, H, L, D)).astype(np.float32))
+    say("attention NaN / inf / tie scores")
+    qb, kb, vb = ca.Buffer.from_array(q16), ca.Buffer.from_array(k16), ca.Buffer.from_array(v16)
+    got = _run(qb, kb, vb, [L], B, H, L, 0.088388)
+    want = oracle.attn_decode(q16, k16, v16, np.array([L], np.uint32), 0.088388)
+    _bitwise(got, want)
+
+
+def test_attention_full_shape_bitwise_and_run_to_run():
+    B, H, L = 32, 32, 4096
+    say("attention full shape B=32 H=32 L=4096")
+    q = dev_normal_bf16(B * H * D, 41, 0)
+    k = dev_normal_bf16(B * H * L * D, 41, 1)
+    v = dev_normal_bf16(B * H * L * D, 41, 2)
+    scale = float(np.float32(1.0 / math.sqrt(D)))
+    lens = [L] * B
+    got = _run(q, k, v, lens, B, H, L, scale)
+    h = hash_bits(got)
+    say("attention full shape run-to-run x3")
+    for _ in range(3):
+        assert hash_bits(_run(q, k, v, lens, B, H, L, scale)) == h
+    say("attention full shape oracle compare")
+    want = oracle.attn_decode(q.read(np.uint16, (B, H, D)), k.read(np.uint16, (B, H, L, D)),
+                              v.read(np.uint16, (B, H, L, D)), np.array(lens, np.uint32), scale)
+    _bitwise(got, want)
+
+
+def test_attention_program_abi():
+    rt = ca.Runtime([])
+    B, H, L = 2, 2, 50
+    rng = np.random.default_rng(2)
+    q16 = oracle.f32_to_bf16_bits_np(rng.normal(0, 1, (B, H, D)).astype(np.float32))
+    k16 = oracle.f32_to_bf16_bits_np(rng.normal(0, 1, (B, H, L, D)).astype(np.float32))
+    v16 = oracle.f32_to_bf16_bits_np(rng.normal(0, 1, (B, H, L, D)).astype(np.float32))
+    lens = np.array([50, 7], np.uint32)
+    bufs = [ca.Buffer.from_array(x) for x in (q16, k16, v16, lens)]
+    say("runtime exec attn.decode.via-mem")
+    [res] = rt.exec("attn.decode.via-mem", [ca.Value.mem(b.mem) for b in bufs] +
+                    [ca.Value.u64(x) for x in (B, H, L, D)] + [ca.Value.f32(0.125)], 1)
+    got = ca.mem_to_array(res.get(), np.float32).reshape(B, H, D)
+    _bitwise(got, oracle.attn_decode(q16, k16, v16, lens, 0.125))
+    ca.mem_free(res.get())

@@ -1,0 +1,144 @@
+"""GPU parity of the bf16 MFMA GEMM (tile, edge and decode kernels).
+
+The MFMA datapath sums in its own order, so against the reference-order
+sequential oracle the check is an error bound, stated here:
+
+  f32 output:  |C_gpu - C_exact| <= 8 * (K/32 + 1) * u * sum_k |A_ik B_kj|
+               (K/32 dependent MFMA accumulation steps, each rounding to f32
+               a bounded number of times; u = 2^-24; C_exact in float64);
+  bf16 output: |C16_gpu - C16_oracle| <= delta + 1 ulp_bf16, with delta the
+               f32-level distance bound above plus the oracle's own sequential
+               bound K * u * sum|A B|.
+
+Alongside it, the bf16 output must be bitwise RNE(f32 output) of the same
+kernel (same accumulation order), and results are bitwise identical from run
+to run (fixed tile->workgroup map, fixed K order, no atomics).
+"""
+import numpy as np
+import pytest
+
+import catena_amd as ca
+import oracle
+from gpu_util import U, as_f32, bf16_ulp_diff, bf16_ulp_of, dev_normal_bf16, hash_bits, say
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _init():
+    say("init device 0")
+    ca.init(0)
+
+
+def _inputs(n, m, k, seed, wscale=1.0):
+    a = dev_normal_bf16(n * k, seed, 0, 1.0)
+    b = dev_normal_bf16(k * m, seed, 1, wscale)
+    return a, b, a.read(np.uint16, (n, k)), b.read(np.uint16, (k, m))
+
+
+def _check(a16, b16, got32, got16, rows=None):
+    af = as_f32(a16).astype(np.float64)
+    bf = as_f32(b16).astype(np.float64)
+    if rows is not None:
+        af = af[rows]
+    k = a16.shape[1]
+    exact = af @ bf
+    absprod = np.abs(af) @ np.abs(bf)
+    mfma_bound = 8 * (k / 32 + 1) * U * absprod
+    seq32, seq16 = oracle.matmul_bf16(a16, b16, rows=rows)
+    stats = {}
+    if got32 is not None:
+        err = np.abs(got32.astype(np.float64) - exact)
+        assert np.all(err <= mfma_bound), float((err / np.maximum(mfma_bound, 1e-300)).max())
+        stats["f32_max_err_over_u_absprod"] = float((err / (U * np.maximum(absprod, 1e-300))).max())
+        stats["f32_bitwise_equal_to_sequential_frac"] = float(np.mean(got32 == seq32))
+    if got16 is not None:
+        delta = mfma_bound + k * U * absprod
+        g = as_f32(got16).astype(np.float64)
+        s = as_f32(seq16).astype(np.float64)
+        tol = delta + bf16_ulp_of(np.maximum(np.abs(g), np.abs(s)))
+        assert np.all(np.abs(g - s) <= tol)
+        ulps = bf16_ulp_diff(got16, seq16)
+        stats["bf16_max_ulp_vs_sequential"] = int(ulps.max())
+        stats["bf16_equal_frac"] = float(np.mean(ulps == 0))
+        stats["bf16_le1ulp_frac"] = float(np.mean(ulps <= 1))
+    print("[bf16-gemm-stats]", stats, flush=True)
+    return stats
+
+
+@pytest.mark.parametrize("n,m,k", [(256, 256, 64), (512, 256, 1024), (256, 768, 320)])
+def test_tile_kernel_full_compare(n, m, k):
+    say(f"bf16 gemm tile {n}x{m}x{k}")
+    a, b, a16, b16 = _inputs(n, m, k, seed=100 + n + m + k)
+    c32, c16 = ca.Buffer(n * m * 4), ca.Buffer(n * m * 2)
+    ca.gemm_bf16(a, b, c32, n, m, k, out_f32=True)
+    ca.gemm_bf16(a, b, c16, n, m, k, out_f32=False)
+    g32, g16 = c32.read(np.float32, (n, m)), c16.read(np.uint16, (n, m))
+    assert np.array_equal(g16, oracle.f32_to_bf16_bits_np(g32))
+    _check(a16, b16, g32, g16)
+
+
+@pytest.mark.parametrize("n,m,k", [(1, 1, 1), (17, 9, 5), (300, 200, 100), (257, 513, 72),
+                                   (64, 64, 63)])
+def test_edge_kernel_full_compare(n, m, k):
+    say(f"bf16 gemm edge {n}x{m}x{k}")
+    a, b, a16, b16 = _inputs(n, m, k, seed=200 + n + m + k)
+    c32, c16 = ca.Buffer(n * m * 4), ca.Buffer(n * m * 2)
+    ca.gemm_bf16(a, b, c32, n, m, k, out_f32=True)
+    ca.gemm_bf16(a, b, c16, n, m, k, out_f32=False)
+    g32, g16 = c32.read(np.float32, (n, m)), c16.read(np.uint16, (n, m))
+    assert np.array_equal(g16, oracle.f32_to_bf16_bits_np(g32))
+    _check(a16, b16, g32, g16)
+
+
+def test_gemm_4096_sampled_rows_and_run_to_run():
+    n = m = k = 4096
+    say("bf16 gemm 4096^3")
+    a, b, a16, b16 = _inputs(n, m, k, seed=3)
+    c16 = ca.Buffer(n * m * 2)
+    c32 = ca.Buffer(n * m * 4)
+    ca.gemm_bf16(a, b, c16, n, m, k)
+    first = c16.read(np.uint16, (n, m))
+    say("bf16 gemm 4096^3 run-to-run x5")
+    for _ in range(5):
+        ca.gemm_bf16(a, b, c16, n, m, k)
+        assert hash_bits(c16.read(np.uint16)) == hash_bits(first)
+    ca.gemm_bf16(a, b, c32, n, m, k, out_f32=True)
+    g32 = c32.read(np.float32, (n, m))
+    assert np.array_equal(first, oracle.f32_to_bf16_bits_np(g32))
+    rows = np.random.default_rng(0).choice(n, 48, replace=False).astype(np.uint64)
+    rows.sort()
+    ri = rows.astype(np.int64)
+    _check(a16, b16, g32[ri], first[ri], rows=rows)
+
+
+@pytest.mark.parametrize("mrows,n,k", [(16, 11008, 4096), (16, 4096, 11008), (1, 4096, 4096),
+                                       (7, 1024, 960), (16, 128, 32), (5, 136, 8)])
+def test_decode_kernel_full_compare(mrows, n, k):
+    say(f"bf16 decode gemm M={mrows} N={n} K={k}")
+    a, b, a16, b16 = _inputs(mrows, n, k, seed=300 + mrows + n + k, wscale=0.02)
+    c16 = ca.Buffer(mrows * n * 2)
+    ca.gemm_bf16(a, b, c16, mrows, n, k)
+    g16 = c16.read(np.uint16, (mrows, n))
+    _check(a16, b16, None, g16)
+    h = hash_bits(g16)
+    for _ in range(3):
+        ca.gemm_bf16(a, b, c16, mrows, n, k)
+        assert hash_bits(c16.read(np.uint16)) == h
+
+
+def test_program_bf16_matmul():
+    rt = ca.Runtime([])
+    n, m, k = 32, 40, 24
+    rng = np.random.default_rng(4)
+    a16 = oracle.f32_to_bf16_bits_np(rng.integers(-4, 5, (n, k)).astype(np.float32))
+    b16 = oracle.f32_to_bf16_bits_np(rng.integers(-4, 5, (k, m)).astype(np.float32))
+    abuf, bbuf = ca.Buffer.from_array(a16), ca.Buffer.from_array(b16)
+    say("runtime exec bf16.matmul.row-major.via-mem")
+    [res] = rt.exec("bf16.matmul.row-major.via-mem",
+                    [ca.Value.mem(abuf.mem), ca.Value.mem(bbuf.mem)] +
+                    [ca.Value.u64(x) for x in (n, m, k, n * k, k * m, n * m)], 1)
+    got = ca.mem_to_array(res.get(), np.uint16).reshape(n, m)
+    # small integers: every partial sum is exact, so any order gives the oracle's bits
+    assert np.array_equal(got, oracle.matmul_bf16(a16, b16)[1])
+    ca.mem_free(res.get())

@@ -1,0 +1,181 @@
+"""GPU parity of the exact-order paths against the pinned oracle: bitwise.
+
+math.exp-approx, nn.softmax and the f32 matmul contraction reproduce the
+reference's operation order exactly, so every output bit must match the CPU
+oracle on the same inputs (NaN payloads excepted: only NaN-ness is compared).
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import catena_amd as ca
+import oracle
+from gpu_util import hash_bits, say
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
+                                     "reference_known_answers.json")))
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _init():
+    say("init device 0")
+    ca.init(0)
+
+
+def _bits_equal_nan_aware(x: np.ndarray, y: np.ndarray) -> bool:
+    xn, yn = np.isnan(x), np.isnan(y)
+    if not np.array_equal(xn, yn):
+        return False
+    return np.array_equal(x[~xn].view(np.uint32), y[~yn].view(np.uint32))
+
+
+def test_exp_approx_bitwise_sweep():
+    rng = np.random.default_rng(21)
+    x = np.concatenate([
+        np.linspace(-100, 100, 400001).astype(np.float32),
+        rng.integers(0, 2 ** 32, 600000, dtype=np.uint64).astype(np.uint32).view(np.float32),
+        np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 88.5, -88.5, 89.5, -89.5, 1e-40, -1e-40],
+                 np.float32),
+    ]).astype(np.float32)
+    say(f"exp-approx sweep n={x.size}")
+    xb, yb = ca.Buffer.from_array(x), ca.Buffer(x.nbytes)
+    ca.exp_approx_f32(xb, yb, x.size)
+    got = yb.read(np.float32)
+    L = oracle.lib()
+    want = np.array([L.or_exp_approx(float(v)) for v in x], np.float32)
+    assert _bits_equal_nan_aware(got, want)
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 255, 256, 257, 4096, 100003])
+def test_softmax_bitwise(n):
+    rng = np.random.default_rng(n)
+    x = (rng.normal(0, 4, n)).astype(np.float32)
+    say(f"softmax n={n}")
+    xb, yb = ca.Buffer.from_array(x), ca.Buffer(x.nbytes)
+    ca.softmax_f32(xb, yb, 1, n)
+    assert np.array_equal(yb.read(np.float32).view(np.uint32), oracle.softmax_f32(x).view(np.uint32))
+
+
+def test_softmax_rows_in_place_and_specials():
+    rows = [
+        np.array([1.0, 2.0, 4.0], np.float32),
+        np.array([0.0, -0.0, -0.0, 0.0], np.float32),           # max tie: first (+0) wins
+        np.array([-0.0, 0.0, 0.0, -0.0], np.float32),           # first (-0) wins
+        np.array([5.0, np.nan, 1.0, 2.0], np.float32),          # NaN resets the max fold
+        np.array([1.0, 2.0, 3.0, np.nan], np.float32),          # trailing NaN is the max
+        np.array([-np.inf, -np.inf, -np.inf, -np.inf], np.float32),
+        np.array([3.0, 3.0, 3.0, 3.0], np.float32),
+        np.array([100.0, -100.0, 50.0, 89.0], np.float32),      # exp~ wrap region
+    ]
+    x = np.stack(rows)
+    say("softmax rows specials (in place)")
+    buf = ca.Buffer.from_array(x)
+    ca.softmax_f32(buf, buf, x.shape[0], x.shape[1])
+    got = buf.read(np.float32, x.shape)
+    for i, r in enumerate(rows):
+        assert _bits_equal_nan_aware(got[i], oracle.softmax_f32(r)), i
+
+
+@pytest.mark.parametrize("n,m,k", [(256, 256, 256), (1, 1, 1), (65, 33, 17), (130, 70, 300),
+                                   (64, 64, 0), (3, 200, 5), (257, 129, 64)])
+def test_gemm_f32_exact_bitwise(n, m, k):
+    rng = np.random.default_rng(n + m + k)
+    a = rng.uniform(-1, 1, (n, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (k, m)).astype(np.float32)
+    say(f"gemm f32 exact {n}x{m}x{k}")
+    ab, bb, cb = ca.Buffer.from_array(a), ca.Buffer.from_array(b), ca.Buffer(n * m * 4)
+    ca.gemm_f32_exact(ab, bb, cb, n, m, k)
+    got = cb.read(np.float32, (n, m))
+    want = oracle.matmul_f32(a, b) if k else np.zeros((n, m), np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_gemm_f32_exact_run_to_run():
+    n = m = k = 256
+    a = ca.Buffer(n * k * 4)
+    b = ca.Buffer(k * m * 4)
+    ca.fill_uniform_f32(a, n * k, 1, 0)
+    ca.fill_uniform_f32(b, k * m, 2, 0)
+    c = ca.Buffer(n * m * 4)
+    say("gemm f32 exact run-to-run x10")
+    hashes = set()
+    for _ in range(10):
+        ca.gemm_f32_exact(a, b, c, n, m, k)
+        hashes.add(hash_bits(c.read(np.uint32)))
+    assert len(hashes) == 1
+    # and against the oracle on the device-generated inputs
+    want = oracle.matmul_f32(a.read(np.float32, (n, k)), b.read(np.float32, (k, m)))
+    assert np.array_equal(c.read(np.uint32, (n, m)), want.view(np.uint32))
+
+
+# ---------------------------------------------------------------- runtime / programs
+MATMUL_DECLS = """
+(def program matmul-2x2-via-mem :
+  ([n m k.] {(cap.ref mem) (cap.ref mem) ({[.n] u64} :) ({[.m] u64} :) ({[.k] u64} :)
+             ({({[.n] [.k]} *) u64} :) ({({[.k] [.m]} *) u64} :) ({({[.n] [.m]} *) u64} :)})
+  -> ([n m k.] (cap.own mem)) = native)
+(def program matmul-right-identity-2x2-via-mem :
+  ([n.] {(cap.ref mem) ({[.n] u64} :) ({({[.n] [.n]} *) u64} :)}) -> ([n.] (cap.own mem)) = native)
+(def program matmul-left-identity-2x2-via-mem :
+  ([n.] {(cap.ref mem) ({[.n] u64} :) ({({[.n] [.n]} *) u64} :)}) -> ([n.] (cap.own mem)) = native)
+"""
+
+
+def test_runtime_matmul_reference_known_answer():
+    g = GOLDEN["matmul_2x2_via_mem"]
+    rt = ca.Runtime([MATMUL_DECLS])
+    a, b = rt.mem_f32(g["a"]), rt.mem_f32(g["b"])
+    say("runtime exec matmul-2x2-via-mem")
+    [res] = rt.exec("matmul-2x2-via-mem",
+                    [a, b] + [ca.Value.u64(g[x]) for x in ("n", "m", "k", "nk", "km", "nm")], 1)
+    assert res.kind == ca.KIND_MEM
+    vals = ca.mem_to_array(res.get(), np.float32)
+    assert np.abs(vals - np.array(g["expected"], np.float32)).max() < g["tolerance"]
+    assert vals.tolist() == g["expected"]
+    for v in (a, b, res):
+        ca.mem_free(v.get())
+
+
+def test_runtime_identity_programs_exact():
+    g = GOLDEN["matmul_identity"]
+    rt = ca.Runtime([MATMUL_DECLS])
+    for name in ("matmul-right-identity-2x2-via-mem", "matmul-left-identity-2x2-via-mem"):
+        a = rt.mem_f32(g["a"])
+        say(f"runtime exec {name}")
+        [res] = rt.exec(name, [a, ca.Value.u64(g["n"]), ca.Value.u64(g["nn"])], 1)
+        assert ca.mem_to_array(res.get(), np.float32).tolist() == g["expected"]
+        ca.mem_free(a.get())
+        ca.mem_free(res.get())
+
+
+def test_runtime_softmax_and_exp_reference_tests():
+    rt = ca.Runtime([])
+    g = GOLDEN["softmax"]
+    x = rt.mem_f32(g["input"])
+    say("runtime exec nn.softmax")
+    [res] = rt.exec("nn.softmax", [x], 1)
+    vals = ca.mem_to_array(res.get(), np.float32)
+    xin = np.array(g["input"], np.float64)
+    e = np.exp(xin - xin.max())
+    assert np.abs(vals - e / e.sum()).max() < g["absolute_tolerance"]
+    assert abs(vals.astype(np.float64).sum() - 1.0) < g["sum_tolerance"]
+    assert np.array_equal(vals, oracle.softmax_f32(np.array(g["input"], np.float32)))
+    ge = GOLDEN["exp_approx"]
+    for v in ge["inputs"]:
+        say(f"runtime exec math.exp-approx({v})")
+        [r] = rt.exec("math.exp-approx", [ca.Value.f32(v)], 1)
+        assert r.kind == ca.KIND_F32
+        assert np.float32(r.get()).view(np.uint32) == np.float32(oracle.exp_approx(v)).view(np.uint32)
+        assert abs(r.get() - np.exp(v)) / max(np.exp(v), 1.0) < ge["relative_tolerance"]
+
+
+def test_pool_reuses_blocks():
+    before = ca.pool_stats()["device_allocs"]
+    for _ in range(50):
+        b = ca.Buffer(1 << 20)
+        b.close()
+    assert ca.pool_stats()["device_allocs"] - before <= 1
