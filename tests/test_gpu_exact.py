@@ -62,7 +62,7 @@ def test_softmax_bitwise(n):
 
 def test_softmax_rows_in_place_and_specials():
     rows = [
-        np.array([1.0, 2.0, 4.0], np.float32),
+        np.array([1.0, 2.0, 4.0, 0.5], np.float32),
         np.array([0.0, -0.0, -0.0, 0.0], np.float32),           # max tie: first (+0) wins
         np.array([-0.0, 0.0, 0.0, -0.0], np.float32),           # first (-0) wins
         np.array([5.0, np.nan, 1.0, 2.0], np.float32),          # NaN resets the max fold
