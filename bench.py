@@ -191,6 +191,9 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["gemm", "all"], default="all")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also launch the plain copy kernel on 1 GiB (known traffic) three "
+                         "times, for scaling FETCH_SIZE / WRITE_SIZE counter readings")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
@@ -217,15 +220,24 @@ def main(argv=None) -> int:
                 "bytes_per_launch": at["bytes_per_launch"]},
             "decode_gemm_m16": dg,
         }
+    if args.copy_calibration:
+        nbytes = 1 << 30
+        src, dst = ca.Buffer(nbytes), ca.Buffer(nbytes)
+        ca.fill_uniform_f32(src, nbytes // 4, 5, 0)
+        for _ in range(3):
+            ca.copy_bytes(dst, src, nbytes)
+        ca.synchronize()
+        print(f"[bench] copy calibration: 3 x catena_copy_16b over {nbytes} B", file=sys.stderr,
+              flush=True)
     cpu = None
     if not args.no_cpu_baseline:
         threads = max(1, min(16, len(os.sched_getaffinity(0))))
         print(f"[bench] cpu baseline ({threads} threads)", file=sys.stderr, flush=True)
         a, b = g["inputs"]
-        cpu = cpu_baseline_gemm(a, b, rows=96, threads=threads)
+        cpu = cpu_baseline_gemm(a, b, rows=4096, threads=threads)
         if args.only == "all":
             q, k, v = at["inputs"]
-            extra["decode_attention"]["cpu_baseline"] = cpu_baseline_attention(q, k, v, 64, threads)
+            extra["decode_attention"]["cpu_baseline"] = cpu_baseline_attention(q, k, v, 1024, threads)
 
     tflops = g["tflops"]
     line = {

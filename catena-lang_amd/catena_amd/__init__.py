@@ -123,6 +123,7 @@ SIGNATURES = {
     "catena_mi355x_exp_approx_f32": (_int, [_vp, _vp, _u64]),
     "catena_mi355x_fill_normal_bf16": (_int, [_vp, _u64, _u64, _u64, _f32]),
     "catena_mi355x_fill_uniform_f32": (_int, [_vp, _u64, _u64, _u64]),
+    "catena_mi355x_copy_bytes": (_int, [_vp, _vp, _u64]),
     "program_matmul_2x2_via_mem": (None, [Mem, Mem] + [_u64] * 6 + [ctypes.POINTER(Mem)]),
     "program_matmul_right_identity_2x2_via_mem": (None, [Mem, _u64, _u64, ctypes.POINTER(Mem)]),
     "program_matmul_left_identity_2x2_via_mem": (None, [Mem, _u64, _u64, ctypes.POINTER(Mem)]),
@@ -269,6 +270,10 @@ def fill_normal_bf16(out, n: int, seed: int, stream_id: int, scale: float = 1.0)
 
 def fill_uniform_f32(out, n: int, seed: int, stream_id: int) -> None:
     check(lib().catena_mi355x_fill_uniform_f32(_p(out), n, seed, stream_id))
+
+
+def copy_bytes(dst, src, n: int) -> None:
+    check(lib().catena_mi355x_copy_bytes(_p(dst), _p(src), n))
 
 
 # ------------------------------------------------------------------ runtime

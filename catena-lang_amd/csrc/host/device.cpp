@@ -56,6 +56,8 @@ const KernelSpec kKernels[] = {
     {KernelId::GemmBf16TileF32, "gemm_bf16", "catena_gemm_bf16_tile_f32out"},
     {KernelId::GemmBf16EdgeBf16, "gemm_bf16", "catena_gemm_bf16_edge_bf16out"},
     {KernelId::GemmBf16EdgeF32, "gemm_bf16", "catena_gemm_bf16_edge_f32out"},
+    {KernelId::GemmBf16LdsBf16, "gemm_bf16_lds", "catena_gemm_bf16_lds_bf16out"},
+    {KernelId::GemmBf16LdsF32, "gemm_bf16_lds", "catena_gemm_bf16_lds_f32out"},
     {KernelId::GemmBf16Decode, "gemm_bf16_decode", "catena_gemm_bf16_decode"},
     {KernelId::GemmBf16DecodeReduce, "gemm_bf16_decode", "catena_gemm_bf16_decode_reduce"},
     {KernelId::AttnDecodeD128, "attn_decode", "catena_attn_decode_bf16_d128"},
@@ -63,6 +65,7 @@ const KernelSpec kKernels[] = {
     {KernelId::ExpApprox, "softmax", "catena_exp_approx_f32"},
     {KernelId::FillNormalBf16, "fill", "catena_fill_normal_bf16"},
     {KernelId::FillUniformF32, "fill", "catena_fill_uniform_f32"},
+    {KernelId::Copy16, "fill", "catena_copy_16b"},
 };
 
 std::string library_dir() {

@@ -16,6 +16,8 @@ enum class KernelId : int {
   GemmBf16TileF32,
   GemmBf16EdgeBf16,
   GemmBf16EdgeF32,
+  GemmBf16LdsBf16,
+  GemmBf16LdsF32,
   GemmBf16Decode,
   GemmBf16DecodeReduce,
   AttnDecodeD128,
@@ -23,6 +25,7 @@ enum class KernelId : int {
   ExpApprox,
   FillNormalBf16,
   FillUniformF32,
+  Copy16,
   Count
 };
 

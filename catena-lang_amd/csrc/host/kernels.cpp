@@ -1,6 +1,7 @@
 // Kernel ABI: shape checks, variant selection and launches.
 #include <cstdint>
 #include <cstdlib>
+#include <cstring>
 
 #include "internal.h"
 
@@ -84,14 +85,25 @@ int catena_mi355x_gemm_bf16(const uint16_t* a, const uint16_t* b, void* c, uint6
   }
 
   const bool tile_ok = n % 256 == 0 && m % 256 == 0 && k % 64 == 0 && k > 0 && aligned16(a) &&
-                       aligned16(b);
-  const size_t lds = 2ull * 2 * 256 * 72 * sizeof(uint16_t);  // 147456 B
-  if (lds > d.max_lds) return fail(CATENA_ERR_UNSUPPORTED, "device LDS %zu < %zu", d.max_lds, lds);
+                       aligned16(b) && aligned16(c);
   const uint64_t tiles = ceil_div(n, 256) * ceil_div(m, 256);
   if (tiles > 0x7FFFFFFFu) return fail(CATENA_ERR_UNSUPPORTED, "matrix too large");
+  void* args[] = {&a, &b, &c, &n, &m, &k};
+  // Aligned shapes: direct-to-LDS kernel (8 waves, 128 KiB LDS).  The older
+  // register-staged tile kernel stays selectable with CATENA_GEMM_TILE=regs
+  // for comparison; it computes in the same order per output tile.
+  const char* sel = getenv("CATENA_GEMM_TILE");
+  const bool use_regs = sel && strcmp(sel, "regs") == 0;
+  if (tile_ok && !use_regs) {
+    const size_t lds = 2ull * (256 * 64 + 64 * 256) * sizeof(uint16_t);  // 131072 B
+    if (lds > d.max_lds) return fail(CATENA_ERR_UNSUPPORTED, "device LDS %zu < %zu", d.max_lds, lds);
+    return launch(out_f32 ? KernelId::GemmBf16LdsF32 : KernelId::GemmBf16LdsBf16,
+                  dim3((unsigned)tiles), dim3(512), lds, args);
+  }
+  const size_t lds = 2ull * 2 * 256 * 72 * sizeof(uint16_t);  // 147456 B
+  if (lds > d.max_lds) return fail(CATENA_ERR_UNSUPPORTED, "device LDS %zu < %zu", d.max_lds, lds);
   KernelId id = tile_ok ? (out_f32 ? KernelId::GemmBf16TileF32 : KernelId::GemmBf16TileBf16)
                         : (out_f32 ? KernelId::GemmBf16EdgeF32 : KernelId::GemmBf16EdgeBf16);
-  void* args[] = {&a, &b, &c, &n, &m, &k};
   return launch(id, dim3((unsigned)tiles), dim3(256), lds, args);
 }
 
@@ -161,6 +173,19 @@ int catena_mi355x_fill_uniform_f32(float* out, uint64_t n, uint64_t seed, uint64
   if (g > 0x7FFFFFFFull) return fail(CATENA_ERR_UNSUPPORTED, "too many elements");
   void* args[] = {&out, &n, &seed, &stream};
   return launch(KernelId::FillUniformF32, dim3((unsigned)g), dim3(256), 0, args);
+}
+
+int catena_mi355x_copy_bytes(void* dst, const void* src, uint64_t n) {
+  int st = ensure_init();
+  if (st) return st;
+  if (n == 0) return CATENA_OK;
+  if (!dst || !src) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
+  if (n % 16 != 0 || !aligned16(dst) || !aligned16(src))
+    return fail(CATENA_ERR_INVALID_ARGUMENT, "copy needs 16-byte aligned pointers and size");
+  uint64_t n16 = n / 16;
+  const uint64_t g = ceil_div(n16, 256) < 8192 ? ceil_div(n16, 256) : 8192;
+  void* args[] = {&dst, &src, &n16};
+  return launch(KernelId::Copy16, dim3((unsigned)g), dim3(256), 0, args);
 }
 
 }  // extern "C"

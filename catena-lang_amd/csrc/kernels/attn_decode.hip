@@ -17,16 +17,17 @@
 // moved in four 32-wide d segments: a coalesced 16-byte-per-lane global load
 // (4 lanes per 64-byte row segment), a write into the wave's private LDS
 // slice, and a read back in which lane l owns row l, so every score is one
-// lane's d-ascending chain of v_mul_f32 + v_add_f32.  The next segment's
-// loads are issued before the current one is folded.
+// lane's d-ascending chain of v_mul_f32 + v_add_f32.  Two register sets keep
+// the next two segments' loads in flight while one is folded.
 // Softmax: the max is the exact parallel form of the sequential fold (see
 // FirstMax in common.h); exp~ is elementwise; the denominator is the one
 // truly sequential fold and runs in one lane over LDS; p_t is one correctly
 // rounded division per element.
 // V pass: waves 0 and 1 own 64 output columns each (lane = column) and walk
-// t ascending through 64-row batches staged in LDS, with the next batch's
-// loads in flight while the current one is folded.  Every K and V byte is
-// read from HBM once.
+// t ascending through 64-row batches staged in LDS, with the next two
+// batches' loads in flight while one is folded; the first batch is requested
+// before the softmax phase so HBM stays busy through it.  Every K and V byte
+// is read from HBM once.
 #include "common.h"
 
 namespace {
@@ -62,7 +63,8 @@ CATENA_DEV FirstMax wave_first_max(FirstMax a) {
 }
 }  // namespace
 
-extern "C" __global__ __launch_bounds__(256) void catena_attn_decode_bf16_d128(
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void
+catena_attn_decode_bf16_d128(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint32_t* __restrict__ lens, float* __restrict__ o,
     uint32_t H, uint32_t L, float scale) {
@@ -106,17 +108,19 @@ extern "C" __global__ __launch_bounds__(256) void catena_attn_decode_bf16_d128(
           r[i] = u32x4_t{0u, 0u, 0u, 0u};
       }
     };
-    u32x4_t cur[4], nxt[4];
-    if (steps) gload(0, cur);
+    // Two register sets: while segment `step` is folded, segments step+1 and
+    // step+2 are in flight.  steps is a multiple of 4, so the pair loop is exact.
+    u32x4_t ra[4], rb[4];
+    if (steps > 0) gload(0, ra);
+    if (steps > 1) gload(1, rb);
     float acc = __uint_as_float(0u);
-    for (uint32_t step = 0; step < steps; ++step) {
+    auto process = [&](uint32_t step, u32x4_t* r) {
       const uint32_t seg = step & 3;
-      const bool more = step + 1 < steps;
-      if (more) gload(step + 1, nxt);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        *reinterpret_cast<u32x4_t*>(st + (lrow + 16 * i) * KSTAGE_ROW + lchunk * 16) = cur[i];
+        *reinterpret_cast<u32x4_t*>(st + (lrow + 16 * i) * KSTAGE_ROW + lchunk * 16) = r[i];
       wave_sync();
+      if (step + 2 < steps) gload(step + 2, r);
       if (seg == 0) acc = __uint_as_float(0u);
       const unsigned char* myrow = st + lane * KSTAGE_ROW;
 #pragma unroll
@@ -139,12 +143,31 @@ extern "C" __global__ __launch_bounds__(256) void catena_attn_decode_bf16_d128(
         if (t < len) sp[t] = acc * scale;
       }
       wave_sync();
-      if (more) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) cur[i] = nxt[i];
-      }
+    };
+    for (uint32_t step = 0; step < steps; step += 2) {
+      process(step, ra);
+      process(step + 1, rb);
     }
   }
+  // V prefetch: waves 0 and 1 start streaming their first V batch now, so
+  // HBM stays busy through the softmax phase.  (The V pass itself is below.)
+  unsigned char* vst = stage + (wave & 1) * 8192;  // [64 rows][64 cols] bf16
+  const int vrow = lane >> 3, vchunk = lane & 7;
+  const uint64_t vcolbase = (uint64_t)(wave & 1) * 64;
+  const uint32_t vnb = (len + 63) / 64;
+  auto vload = [&](uint32_t bt, u32x4_t* r) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t t = bt * 64 + vrow + 8 * i;
+      if (t < len)
+        r[i] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4_t*>(vb + (uint64_t)t * D + vcolbase + vchunk * 8));
+      else
+        r[i] = u32x4_t{0u, 0u, 0u, 0u};
+    }
+  };
+  u32x4_t va[8], vbuf[8];
+  if (wave < 2 && vnb > 0) vload(0, va);
   __syncthreads();
 
   // ---------------------------------------------------------------- max
@@ -184,10 +207,39 @@ extern "C" __global__ __launch_bounds__(256) void catena_attn_decode_bf16_d128(
   }
   __syncthreads();
   if (tid == 0) {
+    // The one sequential fold: den = (((0 + e_0) + e_1) + ...) in ascending t.
+    // The next 32 values are read from LDS before the current 32 are added.
     float den = __uint_as_float(0u);
     const uint32_t n4 = len / 4;
     const f32x4_t* s4 = reinterpret_cast<const f32x4_t*>(sp);
-    for (uint32_t i = 0; i < n4; ++i) {
+    uint32_t i = 0;
+    if (n4 >= 8) {
+      f32x4_t cur[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) cur[u] = s4[u];
+      for (i = 8; i + 8 <= n4; i += 8) {
+        f32x4_t nxt[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) nxt[u] = s4[i + u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          den = den + cur[u][0];
+          den = den + cur[u][1];
+          den = den + cur[u][2];
+          den = den + cur[u][3];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        den = den + cur[u][0];
+        den = den + cur[u][1];
+        den = den + cur[u][2];
+        den = den + cur[u][3];
+      }
+    }
+    for (; i < n4; ++i) {
       const f32x4_t e = s4[i];
       den = den + e[0];
       den = den + e[1];
@@ -205,48 +257,36 @@ extern "C" __global__ __launch_bounds__(256) void catena_attn_decode_bf16_d128(
   // ---------------------------------------------------------------- V pass
   if (wave >= 2) return;
   {
-    unsigned char* st = stage + wave * 8192;  // [64 rows][64 cols] bf16
-    const int vrow = lane >> 3, vchunk = lane & 7;
-    const uint64_t colbase = (uint64_t)wave * 64;
-    const uint32_t nb = (len + 63) / 64;
-    auto gload = [&](uint32_t bt, u32x4_t r[8]) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t t = bt * 64 + vrow + 8 * i;
-        if (t < len)
-          r[i] = __builtin_nontemporal_load(
-              reinterpret_cast<const u32x4_t*>(vb + (uint64_t)t * D + colbase + vchunk * 8));
-        else
-          r[i] = u32x4_t{0u, 0u, 0u, 0u};
-      }
-    };
-    u32x4_t rv[8];
-    if (nb) gload(0, rv);
+    if (vnb > 1) vload(1, vbuf);
     float acc = __uint_as_float(0u);
-    const uint16_t* st16 = reinterpret_cast<const uint16_t*>(st);
-    for (uint32_t bt = 0; bt < nb; ++bt) {
+    const uint16_t* st16 = reinterpret_cast<const uint16_t*>(vst);
+    auto process = [&](uint32_t bt, u32x4_t* r) {
 #pragma unroll
       for (int i = 0; i < 8; ++i)
-        *reinterpret_cast<u32x4_t*>(st + (vrow + 8 * i) * 128 + vchunk * 16) = rv[i];
+        *reinterpret_cast<u32x4_t*>(vst + (vrow + 8 * i) * 128 + vchunk * 16) = r[i];
       wave_sync();
-      if (bt + 1 < nb) gload(bt + 1, rv);
+      if (bt + 2 < vnb) vload(bt + 2, r);
       const uint32_t t0 = bt * 64;
       const uint32_t rows = (len - t0) < 64u ? (len - t0) : 64u;
       if (rows == 64) {
 #pragma unroll 16
-        for (uint32_t r = 0; r < 64; ++r) {
-          const float pv = sp[t0 + r];
-          const float prod = pv * bf16_to_f32(st16[r * 64 + lane]);
+        for (uint32_t rr = 0; rr < 64; ++rr) {
+          const float pv = sp[t0 + rr];
+          const float prod = pv * bf16_to_f32(st16[rr * 64 + lane]);
           acc = acc + prod;
         }
       } else {
-        for (uint32_t r = 0; r < rows; ++r) {
-          const float prod = sp[t0 + r] * bf16_to_f32(st16[r * 64 + lane]);
+        for (uint32_t rr = 0; rr < rows; ++rr) {
+          const float prod = sp[t0 + rr] * bf16_to_f32(st16[rr * 64 + lane]);
           acc = acc + prod;
         }
       }
       wave_sync();
+    };
+    for (uint32_t bt = 0; bt < vnb; bt += 2) {
+      process(bt, va);
+      if (bt + 1 < vnb) process(bt + 1, vbuf);
     }
-    o[bh * D + colbase + lane] = acc;
+    o[bh * D + vcolbase + lane] = acc;
   }
 }

@@ -44,11 +44,12 @@ CATENA_DEV uint32_t pack_bf16x2(float lo, float hi) {
 // gpu.rs:642-655), with the device conversion's defined behaviour spelled
 // out: NaN and values <= 0 give 0, values >= 2^32 saturate.
 CATENA_DEV uint32_t round_to_u32(float x) {
-  float r = __builtin_rintf(x);
-  if (r != r) return 0u;
-  if (r <= 0.0f) return 0u;
-  if (r >= 4294967296.0f) return 0xFFFFFFFFu;
-  return (uint32_t)r;
+  const float r = __builtin_rintf(x);
+  // branch-free: max(NaN, 0) = 0 and max(negative, 0) = 0; below 2^32 the
+  // conversion is exact; at or above 2^32 the result saturates.
+  const float c = __builtin_fminf(__builtin_fmaxf(r, 0.0f), 4294967040.0f);
+  const uint32_t k = (uint32_t)c;
+  return (r >= 4294967296.0f) ? 0xFFFFFFFFu : k;
 }
 
 // math.exp-approx-nonneg (catena-lang/stdlib/math.hex:148-183); one IEEE

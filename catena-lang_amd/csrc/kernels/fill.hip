@@ -41,3 +41,12 @@ extern "C" __global__ __launch_bounds__(256) void catena_fill_normal_bf16(
   const float z = r * cosf(6.283185307179586f * u2);
   out[i] = (uint16_t)f32_to_bf16_bits(z * scale);
 }
+
+// Plain device-to-device copy in 16-byte units (n16 = bytes / 16): the
+// reference kernel for calibrating HBM traffic counters, and a utility.
+extern "C" __global__ __launch_bounds__(256) void catena_copy_16b(
+    u32x4_t* __restrict__ dst, const u32x4_t* __restrict__ src, uint64_t n16) {
+  const uint64_t stride = (uint64_t)gridDim.x * 256;
+  for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride)
+    dst[i] = __builtin_nontemporal_load(src + i);
+}

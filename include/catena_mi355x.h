@@ -131,6 +131,9 @@ int catena_mi355x_exp_approx_f32(const float *x, float *y, uint64_t n);
 int catena_mi355x_fill_normal_bf16(uint16_t *out, uint64_t n, uint64_t seed, uint64_t stream,
                                    float scale);
 int catena_mi355x_fill_uniform_f32(float *out, uint64_t n, uint64_t seed, uint64_t stream);
+/* Device-to-device copy kernel (16-byte aligned pointers, n % 16 == 0); also
+ * the known-size reference for calibrating HBM traffic counters. */
+int catena_mi355x_copy_bytes(void *dst, const void *src, uint64_t n);
 
 /* ------------------------------------------------------------------ */
 /* program ABI (generated-module symbols; synchronous; fail-stop)        */

@@ -78,6 +78,20 @@ def test_tile_kernel_full_compare(n, m, k):
     _check(a16, b16, g32, g16)
 
 
+def test_register_staged_tile_kernel(monkeypatch):
+    """The older register-staged tile kernel (selectable for comparison)."""
+    monkeypatch.setenv("CATENA_GEMM_TILE", "regs")
+    n, m, k = 512, 256, 1024
+    say(f"bf16 gemm register-staged tile {n}x{m}x{k}")
+    a, b, a16, b16 = _inputs(n, m, k, seed=77)
+    c32, c16 = ca.Buffer(n * m * 4), ca.Buffer(n * m * 2)
+    ca.gemm_bf16(a, b, c32, n, m, k, out_f32=True)
+    ca.gemm_bf16(a, b, c16, n, m, k, out_f32=False)
+    g32, g16 = c32.read(np.float32, (n, m)), c16.read(np.uint16, (n, m))
+    assert np.array_equal(g16, oracle.f32_to_bf16_bits_np(g32))
+    _check(a16, b16, g32, g16)
+
+
 @pytest.mark.parametrize("n,m,k", [(1, 1, 1), (17, 9, 5), (300, 200, 100), (257, 513, 72),
                                    (64, 64, 63)])
 def test_edge_kernel_full_compare(n, m, k):

@@ -173,6 +173,14 @@ def test_runtime_softmax_and_exp_reference_tests():
         assert abs(r.get() - np.exp(v)) / max(np.exp(v), 1.0) < ge["relative_tolerance"]
 
 
+def test_copy_kernel():
+    x = np.random.default_rng(1).integers(0, 2 ** 32, 1 << 20, dtype=np.uint64).astype(np.uint32)
+    src, dst = ca.Buffer.from_array(x), ca.Buffer(x.nbytes)
+    say("copy kernel 4 MiB")
+    ca.copy_bytes(dst, src, x.nbytes)
+    assert np.array_equal(dst.read(np.uint32), x)
+
+
 def test_pool_reuses_blocks():
     before = ca.pool_stats()["device_allocs"]
     for _ in range(50):
