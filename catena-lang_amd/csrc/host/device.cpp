@@ -56,11 +56,18 @@ const KernelSpec kKernels[] = {
     {KernelId::GemmBf16TileF32, "gemm_bf16", "catena_gemm_bf16_tile_f32out"},
     {KernelId::GemmBf16EdgeBf16, "gemm_bf16", "catena_gemm_bf16_edge_bf16out"},
     {KernelId::GemmBf16EdgeF32, "gemm_bf16", "catena_gemm_bf16_edge_f32out"},
-    {KernelId::GemmBf16LdsBf16, "gemm_bf16_lds", "catena_gemm_bf16_lds_bf16out"},
-    {KernelId::GemmBf16LdsF32, "gemm_bf16_lds", "catena_gemm_bf16_lds_f32out"},
+    {KernelId::GemmBf16LdsBf16, "gemm_bf16_lds", "catena_gemm_bf16_lds_v0_bf16out"},
+    {KernelId::GemmBf16LdsBf16V1, "gemm_bf16_lds", "catena_gemm_bf16_lds_v1_bf16out"},
+    {KernelId::GemmBf16LdsBf16V2, "gemm_bf16_lds", "catena_gemm_bf16_lds_v2_bf16out"},
+    {KernelId::GemmBf16LdsBf16V3, "gemm_bf16_lds", "catena_gemm_bf16_lds_v3_bf16out"},
+    {KernelId::GemmBf16LdsF32, "gemm_bf16_lds", "catena_gemm_bf16_lds_v0_f32out"},
+    {KernelId::GemmBf16LdsF32V1, "gemm_bf16_lds", "catena_gemm_bf16_lds_v1_f32out"},
+    {KernelId::GemmBf16LdsF32V2, "gemm_bf16_lds", "catena_gemm_bf16_lds_v2_f32out"},
+    {KernelId::GemmBf16LdsF32V3, "gemm_bf16_lds", "catena_gemm_bf16_lds_v3_f32out"},
     {KernelId::GemmBf16Decode, "gemm_bf16_decode", "catena_gemm_bf16_decode"},
     {KernelId::GemmBf16DecodeReduce, "gemm_bf16_decode", "catena_gemm_bf16_decode_reduce"},
     {KernelId::AttnDecodeD128, "attn_decode", "catena_attn_decode_bf16_d128"},
+    {KernelId::AttnDecodeD128KC, "attn_decode", "catena_attn_decode_bf16_d128_kc"},
     {KernelId::SoftmaxRows, "softmax", "catena_softmax_rows_f32"},
     {KernelId::ExpApprox, "softmax", "catena_exp_approx_f32"},
     {KernelId::FillNormalBf16, "fill", "catena_fill_normal_bf16"},

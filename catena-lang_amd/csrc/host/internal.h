@@ -16,11 +16,18 @@ enum class KernelId : int {
   GemmBf16TileF32,
   GemmBf16EdgeBf16,
   GemmBf16EdgeF32,
-  GemmBf16LdsBf16,
-  GemmBf16LdsF32,
+  GemmBf16LdsBf16,  // + variant (0..3), see gemm_bf16_lds.hip
+  GemmBf16LdsBf16V1,
+  GemmBf16LdsBf16V2,
+  GemmBf16LdsBf16V3,
+  GemmBf16LdsF32,  // + variant
+  GemmBf16LdsF32V1,
+  GemmBf16LdsF32V2,
+  GemmBf16LdsF32V3,
   GemmBf16Decode,
   GemmBf16DecodeReduce,
   AttnDecodeD128,
+  AttnDecodeD128KC,
   SoftmaxRows,
   ExpApprox,
   FillNormalBf16,

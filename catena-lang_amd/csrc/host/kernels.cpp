@@ -12,6 +12,9 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 
+// Default scheduling variant of the direct-to-LDS GEMM (gemm_bf16_lds.hip).
+constexpr int kGemmLdsDefaultVariant = 0;
+
 // k per wave for the decode kernel: aim for ~1500 waves in flight (1024
 // SIMDs on MI355X), in whole 32-k MFMA steps.  CATENA_DECODE_KW overrides.
 uint32_t decode_kw(uint64_t n_cols, uint64_t k) {
@@ -97,8 +100,12 @@ int catena_mi355x_gemm_bf16(const uint16_t* a, const uint16_t* b, void* c, uint6
   if (tile_ok && !use_regs) {
     const size_t lds = 2ull * (256 * 64 + 64 * 256) * sizeof(uint16_t);  // 131072 B
     if (lds > d.max_lds) return fail(CATENA_ERR_UNSUPPORTED, "device LDS %zu < %zu", d.max_lds, lds);
-    return launch(out_f32 ? KernelId::GemmBf16LdsF32 : KernelId::GemmBf16LdsBf16,
-                  dim3((unsigned)tiles), dim3(512), lds, args);
+    // scheduling variant (identical arithmetic): CATENA_GEMM_VARIANT=0..3
+    int variant = kGemmLdsDefaultVariant;
+    const char* v = getenv("CATENA_GEMM_VARIANT");
+    if (v && v[0] >= '0' && v[0] <= '3' && v[1] == 0) variant = v[0] - '0';
+    const int base = static_cast<int>(out_f32 ? KernelId::GemmBf16LdsF32 : KernelId::GemmBf16LdsBf16);
+    return launch(static_cast<KernelId>(base + variant), dim3((unsigned)tiles), dim3(512), lds, args);
   }
   const size_t lds = 2ull * 2 * 256 * 72 * sizeof(uint16_t);  // 147456 B
   if (lds > d.max_lds) return fail(CATENA_ERR_UNSUPPORTED, "device LDS %zu < %zu", d.max_lds, lds);
@@ -127,7 +134,11 @@ int catena_mi355x_attn_decode_bf16(const uint16_t* q, const uint16_t* k, const u
     return fail(CATENA_ERR_UNSUPPORTED, "max_len %u needs %zu B of LDS (device has %zu)", max_len,
                 lds, d.max_lds);
   void* args[] = {&q, &k, &v, &lens, &o, &heads, &max_len, &scale};
-  return launch(KernelId::AttnDecodeD128, dim3((unsigned)bh), dim3(256), lds, args);
+  // K-pass cache policy: CATENA_ATTN_K=cached selects plain loads for K.
+  const char* kp = getenv("CATENA_ATTN_K");
+  const bool k_cached = kp && strcmp(kp, "cached") == 0;
+  return launch(k_cached ? KernelId::AttnDecodeD128KC : KernelId::AttnDecodeD128, dim3((unsigned)bh),
+                dim3(256), lds, args);
 }
 
 int catena_mi355x_softmax_f32(const float* x, float* y, uint64_t rows, uint64_t n) {

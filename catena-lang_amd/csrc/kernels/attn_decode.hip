@@ -63,11 +63,13 @@ CATENA_DEV FirstMax wave_first_max(FirstMax a) {
 }
 }  // namespace
 
-extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void
-catena_attn_decode_bf16_d128(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-    const uint16_t* __restrict__ v, const uint32_t* __restrict__ lens, float* __restrict__ o,
-    uint32_t H, uint32_t L, float scale) {
+// K_NT: K-pass loads carry the non-temporal hint.  Each 128-byte line of K
+// is read as two 64-byte halves by consecutive steps, so the hint can cost a
+// second fetch of the line; both forms are kept and the host picks one.
+template <bool K_NT>
+CATENA_DEV void attn_body(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                          const uint16_t* __restrict__ v, const uint32_t* __restrict__ lens,
+                          float* __restrict__ o, uint32_t H, uint32_t L, float scale) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   float* qf = reinterpret_cast<float*>(smem);                  // [128]
   unsigned char* stage = smem + D * 4;                         // [STAGE_BYTES]
@@ -101,9 +103,10 @@ catena_attn_decode_bf16_d128(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const uint32_t t = blk * 64 + lrow + 16 * i;
+        const u32x4_t* src =
+            reinterpret_cast<const u32x4_t*>(kb + (uint64_t)t * D + seg * 32 + lchunk * 8);
         if (t < len)
-          r[i] = __builtin_nontemporal_load(
-              reinterpret_cast<const u32x4_t*>(kb + (uint64_t)t * D + seg * 32 + lchunk * 8));
+          r[i] = K_NT ? __builtin_nontemporal_load(src) : *src;
         else
           r[i] = u32x4_t{0u, 0u, 0u, 0u};
       }
@@ -289,4 +292,18 @@ catena_attn_decode_bf16_d128(
     }
     o[bh * D + vcolbase + lane] = acc;
   }
+}
+
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void
+catena_attn_decode_bf16_d128(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                             const uint16_t* __restrict__ v, const uint32_t* __restrict__ lens,
+                             float* __restrict__ o, uint32_t H, uint32_t L, float scale) {
+  attn_body<true>(q, k, v, lens, o, H, L, scale);
+}
+
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void
+catena_attn_decode_bf16_d128_kc(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                                const uint16_t* __restrict__ v, const uint32_t* __restrict__ lens,
+                                float* __restrict__ o, uint32_t H, uint32_t L, float scale) {
+  attn_body<false>(q, k, v, lens, o, H, L, scale);
 }

@@ -72,7 +72,7 @@ CATENA_DEV void tile_of(uint32_t bid, uint32_t tiles_m, uint32_t tiles_n, uint32
 #define CATENA_WAIT_VMCNT(n) \
   __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | 0x0070 | 0x0F00)
 
-template <bool OUT_BF16>
+template <bool OUT_BF16, bool PIPE, bool PRIO>
 CATENA_DEV void gemm_lds_body(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                               void* __restrict__ C, uint64_t M, uint64_t N, uint64_t K) {
   extern __shared__ __attribute__((aligned(1024))) uint16_t smem[];
@@ -89,29 +89,33 @@ CATENA_DEV void gemm_lds_body(const uint16_t* __restrict__ A, const uint16_t* __
   tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const uint64_t m0 = (uint64_t)tm * BM, n0 = (uint64_t)tn * BN;
 
-  // Per-lane global sources of this wave's 4 A and 4 B load instructions
-  // (a slab is 32 + 32 one-KiB instructions spread over the 8 waves).
-  const uint16_t* asrc[4];
-  const uint16_t* bsrc[4];
+  // Per-lane byte offsets of this wave's 4 A and 4 B load instructions (a
+  // slab is 32 + 32 one-KiB instructions spread over the 8 waves), relative
+  // to the slab's uniform base; 32 bits suffice (256 rows of A, 64 of B).
+  uint32_t aoff[4], boff[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t r = 32 * wave + 8 * i + (lane >> 3);
     const uint32_t q = (uint32_t)(lane & 7) ^ hA(r);
-    asrc[i] = A + (m0 + r) * K + 8 * q;
+    aoff[i] = (uint32_t)((r * K + 8 * q) * 2);
     const uint32_t kr = 8 * wave + 2 * i + (lane >> 5);
     const uint32_t qb = (uint32_t)(lane & 31) ^ hB(kr);
-    bsrc[i] = B + (uint64_t)kr * N + n0 + 8 * qb;
+    boff[i] = (uint32_t)((kr * N + 8 * qb) * 2);
   }
+  const char* abase = reinterpret_cast<const char*>(A + m0 * K);
+  const char* bbase = reinterpret_cast<const char*>(B + n0);
   auto issue = [&](uint64_t slab, int stage) {
     const uint64_t k0 = slab * BK;
+    const char* ab = abase + k0 * 2;
+    const char* bb = bbase + k0 * N * 2;
     uint16_t* as = As + stage * A_STAGE + (32 * wave) * BK;
     uint16_t* bs = Bs + stage * B_STAGE + (8 * wave) * BN;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_global_load_lds(asrc[i] + k0, (lds_void*)(as + 8 * i * BK), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(ab + aoff[i], (lds_void*)(as + 8 * i * BK), 16, 0, 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_global_load_lds(bsrc[i] + k0 * N, (lds_void*)(bs + 2 * i * BN), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(bb + boff[i], (lds_void*)(bs + 2 * i * BN), 16, 0, 0);
   };
 
   f32x4_t acc[8][4];  // [row block i][col block j], transposed blocks
@@ -124,58 +128,111 @@ CATENA_DEV void gemm_lds_body(const uint16_t* __restrict__ A, const uint16_t* __
   issue(0, 0);
   if (nk > 1) issue(1, 1);
 
-  // fragment addressing (element offsets inside a stage)
+  // Fragment addressing (byte offsets inside a stage).  For A, hA(row) is
+  // the same for the 8 row blocks of a lane (16 rows apart), so one base
+  // plus immediates covers them.  For B, hB(row) is the same for both k32
+  // steps and both halves of a fragment, so 4 offsets (one per column block)
+  // cover every read.
   const int G = lane >> 4, s = lane & 15;
-  const uint32_t a_row0 = wm * 128 + s;  // + 16 i
-  const uint32_t b_col_chunk = 4 * (s & 3);
-  const uint32_t b_krow = 8 * G + (s >> 2);  // + kk + 4h
+  const uint32_t a_row0 = wm * 128 + s;
+  const uint32_t a_lds = a_row0 * BK * 2 + 16 * ((uint32_t)G ^ hA(a_row0));  // + 16*16*BK*i, ^(kk/8) below
+  const uint32_t b_krow = 8 * G + (s >> 2);
+  const uint32_t hb = hB(b_krow);
+  uint32_t b_lds[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t col = wn * 64 + 16 * j + 4 * (s & 3);
+    b_lds[j] = b_krow * BN * 2 + 16 * ((col >> 3) ^ hb) + 2 * (col & 7);
+  }
 
-  for (uint64_t it = 0; it < nk; ++it) {
-    const int stage = (int)(it & 1);
-    asm volatile("" ::: "memory");
-    if (it + 1 < nk) {
+  struct Frags {
+    bf16x8_t a[8];
+    bf16x8_t b[4];
+  };
+  // LDS -> registers for one k32 step of this wave's 128 x 64 block.
+  auto load_frags = [&](int stage, int kk, Frags& f) {
+    const char* as = reinterpret_cast<const char*>(As + stage * A_STAGE);
+    const char* bs = reinterpret_cast<const char*>(Bs + stage * B_STAGE);
+    // A chunk index for this kk is (kk/8 + G) ^ hA = (G ^ hA) ^ (kk/8): kk/8
+    // is 0 or 4 and hA < 8, so the XOR with kk/8 flips bit 2 of the chunk.
+    const uint32_t a_off = kk == 0 ? a_lds : (a_lds ^ (4u * 16u));
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      f.a[i] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(as + a_off + i * 16 * BK * 2));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const char* p = bs + b_lds[j] + kk * BN * 2;
+      i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+      i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 4 * BN * 2));
+      f.b[j] = cat_bf16(lo, hi);
+    }
+  };
+  auto mma = [&](const Frags& f) {
+    if (PRIO) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.b[j], f.a[i], acc[i][j], 0, 0, 0);
+    if (PRIO) __builtin_amdgcn_s_setprio(0);
+  };
+
+  if (!PIPE) {
+    // two barriers per slab: wait + barrier before reading, barrier before refill
+    for (uint64_t it = 0; it < nk; ++it) {
+      const int stage = (int)(it & 1);
+      asm volatile("" ::: "memory");
+      if (it + 1 < nk) {
+        CATENA_WAIT_VMCNT(8);
+      } else {
+        CATENA_WAIT_VMCNT(0);
+      }
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int kk = 0; kk < BK; kk += 32) {
+        Frags f;
+        load_frags(stage, kk, f);
+        mma(f);
+      }
+      if (it + 2 < nk) {
+        // every wave's reads of this stage have landed before it is refilled
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        issue(it + 2, stage);
+      }
+    }
+  } else {
+    // one barrier per slab; the fragments of the next k32 step are read from
+    // LDS while the current step's MFMAs run:
+    //   read F1 (2nd half of slab it) | MFMA F0 | wait: F1 landed, my slab it+1
+    //   loads landed | barrier | refill this stage with slab it+2 | read F0 (1st
+    //   half of slab it+1) | MFMA F1
+    if (nk > 1) {
       CATENA_WAIT_VMCNT(8);
     } else {
       CATENA_WAIT_VMCNT(0);
     }
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    const uint16_t* as = As + stage * A_STAGE;
-    const uint16_t* bs = Bs + stage * B_STAGE;
-#pragma unroll
-    for (int kk = 0; kk < BK; kk += 32) {
-      bf16x8_t af[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t r = a_row0 + 16 * i;
-        const uint32_t q = (uint32_t)(kk / 8 + G) ^ hA(r);
-        af[i] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(as + r * BK + 8 * q));
+    Frags f0, f1;
+    load_frags(0, 0, f0);
+    for (uint64_t it = 0; it < nk; ++it) {
+      const int stage = (int)(it & 1);
+      load_frags(stage, 32, f1);
+      mma(f0);
+      if (it + 1 < nk) {
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): f1 has landed
+        CATENA_WAIT_VMCNT(0);                // this wave's slab it+1 has landed
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (it + 2 < nk) issue(it + 2, stage);
+        load_frags(stage ^ 1, 0, f0);
       }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t col = wn * 64 + 16 * j + b_col_chunk;  // 4 columns, 8 bytes
-        bf16x8_t bfrag;
-        {
-          const uint32_t k0r = kk + b_krow, k1r = kk + b_krow + 4;
-          const uint32_t c16 = col >> 3, half = col & 7;  // 16-byte chunk, element within it
-          const uint32_t o0 = k0r * BN + 8 * (c16 ^ hB(k0r)) + half;
-          const uint32_t o1 = k1r * BN + 8 * (c16 ^ hB(k1r)) + half;
-          i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(bs + o0));
-          i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(bs + o1));
-          bfrag = cat_bf16(lo, hi);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfrag, af[i], acc[i][j], 0, 0, 0);
-      }
-    }
-    if (it + 2 < nk) {
-      // every wave's reads of this stage have landed before it is refilled
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-      asm volatile("" ::: "memory");
-      __builtin_amdgcn_s_barrier();
-      asm volatile("" ::: "memory");
-      issue(it + 2, stage);
+      mma(f1);
     }
   }
 
@@ -201,14 +258,21 @@ CATENA_DEV void gemm_lds_body(const uint16_t* __restrict__ A, const uint16_t* __
 }
 }  // namespace
 
-extern "C" __global__ __launch_bounds__(512) void catena_gemm_bf16_lds_bf16out(
-    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C,
-    uint64_t M, uint64_t N, uint64_t K) {
-  gemm_lds_body<true>(A, B, C, M, N, K);
-}
+#define CATENA_GEMM_LDS_KERNEL(NAME, OUTB, PIPE, PRIO)                                    \
+  extern "C" __global__ __launch_bounds__(512) void NAME(                                 \
+      const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C, \
+      uint64_t M, uint64_t N, uint64_t K) {                                               \
+    gemm_lds_body<OUTB, PIPE, PRIO>(A, B, C, M, N, K);                                    \
+  }
 
-extern "C" __global__ __launch_bounds__(512) void catena_gemm_bf16_lds_f32out(
-    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C,
-    uint64_t M, uint64_t N, uint64_t K) {
-  gemm_lds_body<false>(A, B, C, M, N, K);
-}
+// Scheduling variants (same arithmetic and order; selected by the host):
+//   v0 two barriers per slab; v1 = v0 + MFMA priority; v2 one barrier per
+//   slab with fragment double-buffering; v3 = v2 + MFMA priority.
+CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v0_bf16out, true, false, false)
+CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v1_bf16out, true, false, true)
+CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v2_bf16out, true, true, false)
+CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v3_bf16out, true, true, true)
+CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v0_f32out, false, false, false)
+CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v1_f32out, false, false, true)
+CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v2_f32out, false, true, false)
+CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v3_f32out, false, true, true)
