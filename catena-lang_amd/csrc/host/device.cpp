@@ -56,14 +56,24 @@ const KernelSpec kKernels[] = {
     {KernelId::GemmBf16TileF32, "gemm_bf16", "catena_gemm_bf16_tile_f32out"},
     {KernelId::GemmBf16EdgeBf16, "gemm_bf16", "catena_gemm_bf16_edge_bf16out"},
     {KernelId::GemmBf16EdgeF32, "gemm_bf16", "catena_gemm_bf16_edge_f32out"},
-    {KernelId::GemmBf16LdsBf16, "gemm_bf16_lds", "catena_gemm_bf16_lds_v0_bf16out"},
-    {KernelId::GemmBf16LdsBf16V1, "gemm_bf16_lds", "catena_gemm_bf16_lds_v1_bf16out"},
-    {KernelId::GemmBf16LdsBf16V2, "gemm_bf16_lds", "catena_gemm_bf16_lds_v2_bf16out"},
-    {KernelId::GemmBf16LdsBf16V3, "gemm_bf16_lds", "catena_gemm_bf16_lds_v3_bf16out"},
-    {KernelId::GemmBf16LdsF32, "gemm_bf16_lds", "catena_gemm_bf16_lds_v0_f32out"},
-    {KernelId::GemmBf16LdsF32V1, "gemm_bf16_lds", "catena_gemm_bf16_lds_v1_f32out"},
-    {KernelId::GemmBf16LdsF32V2, "gemm_bf16_lds", "catena_gemm_bf16_lds_v2_f32out"},
-    {KernelId::GemmBf16LdsF32V3, "gemm_bf16_lds", "catena_gemm_bf16_lds_v3_f32out"},
+    {KernelId::GemmBf16LdsV0Bf16, "gemm_bf16_lds", "catena_gemm_bf16_lds_v0_bf16out"},
+    {KernelId::GemmBf16LdsV1Bf16, "gemm_bf16_lds", "catena_gemm_bf16_lds_v1_bf16out"},
+    {KernelId::GemmBf16LdsV2Bf16, "gemm_bf16_lds", "catena_gemm_bf16_lds_v2_bf16out"},
+    {KernelId::GemmBf16LdsV3Bf16, "gemm_bf16_lds", "catena_gemm_bf16_lds_v3_bf16out"},
+    {KernelId::GemmBf16LdsV4Bf16, "gemm_bf16_lds", "catena_gemm_bf16_lds_v4_bf16out"},
+    {KernelId::GemmBf16LdsV5Bf16, "gemm_bf16_lds", "catena_gemm_bf16_lds_v5_bf16out"},
+    {KernelId::GemmBf16LdsV7Bf16, "gemm_bf16_lds", "catena_gemm_bf16_lds_v7_bf16out"},
+    {KernelId::GemmBf16LdsV0F32, "gemm_bf16_lds", "catena_gemm_bf16_lds_v0_f32out"},
+    {KernelId::GemmBf16LdsV1F32, "gemm_bf16_lds", "catena_gemm_bf16_lds_v1_f32out"},
+    {KernelId::GemmBf16LdsV2F32, "gemm_bf16_lds", "catena_gemm_bf16_lds_v2_f32out"},
+    {KernelId::GemmBf16LdsV3F32, "gemm_bf16_lds", "catena_gemm_bf16_lds_v3_f32out"},
+    {KernelId::GemmBf16LdsV4F32, "gemm_bf16_lds", "catena_gemm_bf16_lds_v4_f32out"},
+    {KernelId::GemmBf16LdsV5F32, "gemm_bf16_lds", "catena_gemm_bf16_lds_v5_f32out"},
+    {KernelId::GemmBf16LdsV7F32, "gemm_bf16_lds", "catena_gemm_bf16_lds_v7_f32out"},
+    {KernelId::GemmBf16DeepBf16, "gemm_bf16_deep", "catena_gemm_bf16_deep4_bf16out"},
+    {KernelId::GemmBf16DeepF32, "gemm_bf16_deep", "catena_gemm_bf16_deep4_f32out"},
+    {KernelId::GemmBf16DeepFrontBf16, "gemm_bf16_deep", "catena_gemm_bf16_deep4f_bf16out"},
+    {KernelId::GemmBf16DeepFrontF32, "gemm_bf16_deep", "catena_gemm_bf16_deep4f_f32out"},
     {KernelId::GemmBf16Decode, "gemm_bf16_decode", "catena_gemm_bf16_decode"},
     {KernelId::GemmBf16DecodeReduce, "gemm_bf16_decode", "catena_gemm_bf16_decode_reduce"},
     {KernelId::AttnDecodeD128, "attn_decode", "catena_attn_decode_bf16_d128"},

@@ -16,14 +16,24 @@ enum class KernelId : int {
   GemmBf16TileF32,
   GemmBf16EdgeBf16,
   GemmBf16EdgeF32,
-  GemmBf16LdsBf16,  // + variant (0..3), see gemm_bf16_lds.hip
-  GemmBf16LdsBf16V1,
-  GemmBf16LdsBf16V2,
-  GemmBf16LdsBf16V3,
-  GemmBf16LdsF32,  // + variant
-  GemmBf16LdsF32V1,
-  GemmBf16LdsF32V2,
-  GemmBf16LdsF32V3,
+  GemmBf16LdsV0Bf16,  // direct-to-LDS tile kernels, scheduling variants (see kernels.cpp)
+  GemmBf16LdsV1Bf16,
+  GemmBf16LdsV2Bf16,
+  GemmBf16LdsV3Bf16,
+  GemmBf16LdsV4Bf16,
+  GemmBf16LdsV5Bf16,
+  GemmBf16LdsV7Bf16,
+  GemmBf16LdsV0F32,
+  GemmBf16LdsV1F32,
+  GemmBf16LdsV2F32,
+  GemmBf16LdsV3F32,
+  GemmBf16LdsV4F32,
+  GemmBf16LdsV5F32,
+  GemmBf16LdsV7F32,
+  GemmBf16DeepBf16,
+  GemmBf16DeepF32,
+  GemmBf16DeepFrontBf16,
+  GemmBf16DeepFrontF32,
   GemmBf16Decode,
   GemmBf16DecodeReduce,
   AttnDecodeD128,

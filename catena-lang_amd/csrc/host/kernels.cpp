@@ -12,8 +12,35 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 
-// Default scheduling variant of the direct-to-LDS GEMM (gemm_bf16_lds.hip).
-constexpr int kGemmLdsDefaultVariant = 0;
+// Aligned-shape bf16 GEMM kernels.  All compute the same 256x256 tiles with
+// the same per-accumulator k32 order (bitwise identical outputs); they differ
+// in scheduling only.  CATENA_GEMM_VARIANT selects one for comparison.
+struct GemmVariant {
+  KernelId bf16, f32;
+  uint64_t min_k;  // K must be a multiple of 64 and at least this
+};
+const GemmVariant kGemmVariants[] = {
+    /* 0 two barriers per 64-k slab */
+    {KernelId::GemmBf16LdsV0Bf16, KernelId::GemmBf16LdsV0F32, 64},
+    /* 1 v0 + MFMA priority */
+    {KernelId::GemmBf16LdsV1Bf16, KernelId::GemmBf16LdsV1F32, 64},
+    /* 2 one barrier per slab, fragment double-buffering */
+    {KernelId::GemmBf16LdsV2Bf16, KernelId::GemmBf16LdsV2F32, 64},
+    /* 3 v2 + MFMA priority */
+    {KernelId::GemmBf16LdsV3Bf16, KernelId::GemmBf16LdsV3F32, 64},
+    /* 4 v2 with LDS reads interleaved 1:2 with MFMAs */
+    {KernelId::GemmBf16LdsV4Bf16, KernelId::GemmBf16LdsV4F32, 64},
+    /* 5 v4 + MFMA priority */
+    {KernelId::GemmBf16LdsV5Bf16, KernelId::GemmBf16LdsV5F32, 64},
+    /* 6 four 32-k stages, three slabs in flight (gemm_bf16_deep.hip) */
+    {KernelId::GemmBf16DeepBf16, KernelId::GemmBf16DeepF32, 128},
+    /* 7 v4 with reads front-loaded 1:1 */
+    {KernelId::GemmBf16LdsV7Bf16, KernelId::GemmBf16LdsV7F32, 64},
+    /* 8 v6 with reads front-loaded 1:1 */
+    {KernelId::GemmBf16DeepFrontBf16, KernelId::GemmBf16DeepFrontF32, 128},
+};
+constexpr int kGemmVariantCount = sizeof(kGemmVariants) / sizeof(kGemmVariants[0]);
+constexpr int kGemmDefaultVariant = 7;
 
 // k per wave for the decode kernel: aim for ~1500 waves in flight (1024
 // SIMDs on MI355X), in whole 32-k MFMA steps.  CATENA_DECODE_KW overrides.
@@ -100,12 +127,15 @@ int catena_mi355x_gemm_bf16(const uint16_t* a, const uint16_t* b, void* c, uint6
   if (tile_ok && !use_regs) {
     const size_t lds = 2ull * (256 * 64 + 64 * 256) * sizeof(uint16_t);  // 131072 B
     if (lds > d.max_lds) return fail(CATENA_ERR_UNSUPPORTED, "device LDS %zu < %zu", d.max_lds, lds);
-    // scheduling variant (identical arithmetic): CATENA_GEMM_VARIANT=0..3
-    int variant = kGemmLdsDefaultVariant;
+    int variant = kGemmDefaultVariant;
     const char* v = getenv("CATENA_GEMM_VARIANT");
-    if (v && v[0] >= '0' && v[0] <= '3' && v[1] == 0) variant = v[0] - '0';
-    const int base = static_cast<int>(out_f32 ? KernelId::GemmBf16LdsF32 : KernelId::GemmBf16LdsBf16);
-    return launch(static_cast<KernelId>(base + variant), dim3((unsigned)tiles), dim3(512), lds, args);
+    if (v && *v) {
+      const long x = strtol(v, nullptr, 10);
+      if (x >= 0 && x < kGemmVariantCount) variant = (int)x;
+    }
+    if (k < kGemmVariants[variant].min_k) variant = kGemmDefaultVariant;
+    const GemmVariant& gv = kGemmVariants[variant];
+    return launch(out_f32 ? gv.f32 : gv.bf16, dim3((unsigned)tiles), dim3(512), lds, args);
   }
   const size_t lds = 2ull * 2 * 256 * 72 * sizeof(uint16_t);  // 147456 B
   if (lds > d.max_lds) return fail(CATENA_ERR_UNSUPPORTED, "device LDS %zu < %zu", d.max_lds, lds);
@@ -134,9 +164,11 @@ int catena_mi355x_attn_decode_bf16(const uint16_t* q, const uint16_t* k, const u
     return fail(CATENA_ERR_UNSUPPORTED, "max_len %u needs %zu B of LDS (device has %zu)", max_len,
                 lds, d.max_lds);
   void* args[] = {&q, &k, &v, &lens, &o, &heads, &max_len, &scale};
-  // K-pass cache policy: CATENA_ATTN_K=cached selects plain loads for K.
+  // K-pass cache policy: plain loads by default (each 128-byte line of K is
+  // read as two halves by consecutive steps and must stay in L2 between
+  // them); CATENA_ATTN_K=nt selects the non-temporal form for comparison.
   const char* kp = getenv("CATENA_ATTN_K");
-  const bool k_cached = kp && strcmp(kp, "cached") == 0;
+  const bool k_cached = !(kp && strcmp(kp, "nt") == 0);
   return launch(k_cached ? KernelId::AttnDecodeD128KC : KernelId::AttnDecodeD128, dim3((unsigned)bh),
                 dim3(256), lds, args);
 }

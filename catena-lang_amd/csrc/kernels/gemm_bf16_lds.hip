@@ -72,7 +72,7 @@ CATENA_DEV void tile_of(uint32_t bid, uint32_t tiles_m, uint32_t tiles_n, uint32
 #define CATENA_WAIT_VMCNT(n) \
   __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | 0x0070 | 0x0F00)
 
-template <bool OUT_BF16, bool PIPE, bool PRIO>
+template <bool OUT_BF16, bool PIPE, bool PRIO, bool ILV, bool FRONT>
 CATENA_DEV void gemm_lds_body(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                               void* __restrict__ C, uint64_t M, uint64_t N, uint64_t K) {
   extern __shared__ __attribute__((aligned(1024))) uint16_t smem[];
@@ -177,6 +177,66 @@ CATENA_DEV void gemm_lds_body(const uint16_t* __restrict__ A, const uint16_t* __
     if (PRIO) __builtin_amdgcn_s_setprio(0);
   };
 
+  // LDS reads of `next` interleaved with the MFMAs of `cur`, pinned with
+  // scheduling barriers so that few reads are outstanding when an MFMA
+  // issues (the LDS counter tracks only 15 operations, so a block of 16
+  // reads ahead of the MFMAs forces a full wait).  FRONT: one read per MFMA
+  // over the first 16 MFMAs, then 16 MFMAs with no reads (the reads have
+  // landed by the next barrier); otherwise one read per two MFMAs.
+  auto load_mma = [&](int stage, int kk, Frags& next, const Frags& cur) {
+    const char* as = reinterpret_cast<const char*>(As + stage * A_STAGE);
+    const char* bs = reinterpret_cast<const char*>(Bs + stage * B_STAGE);
+    const uint32_t a_off = kk == 0 ? a_lds : (a_lds ^ (4u * 16u));
+    i16x4_t blo[4], bhi[4];
+    if (PRIO) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+      if (g < 8) {
+        next.a[g] = __builtin_bit_cast(
+            bf16x8_t, *reinterpret_cast<const u32x4_t*>(as + a_off + g * 16 * BK * 2));
+      } else {
+        const int j = (g - 8) >> 1;
+        const char* p = bs + b_lds[j] + kk * BN * 2;
+        if ((g & 1) == 0)
+          blo[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+        else
+          bhi[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 4 * BN * 2));
+      }
+      if (FRONT) {
+        const int j = g >> 3, i = g & 7;
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.b[j], cur.a[i], acc[i][j], 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int m = 2 * g + t, j = m >> 3, i = m & 7;
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.b[j], cur.a[i], acc[i][j], 0, 0, 0);
+        }
+      }
+    }
+    if (FRONT) {
+#pragma unroll
+      for (int m = 16; m < 32; ++m) {
+        const int j = m >> 3, i = m & 7;
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.b[j], cur.a[i], acc[i][j], 0, 0, 0);
+      }
+#pragma unroll
+      for (int g = 0; g < 16; ++g) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);   // sixteen MFMAs
+    } else {
+#pragma unroll
+      for (int g = 0; g < 16; ++g) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // two MFMAs
+      }
+    }
+    if (PRIO) __builtin_amdgcn_s_setprio(0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) next.b[j] = cat_bf16(blo[j], bhi[j]);
+  };
+
   if (!PIPE) {
     // two barriers per slab: wait + barrier before reading, barrier before refill
     for (uint64_t it = 0; it < nk; ++it) {
@@ -219,19 +279,35 @@ CATENA_DEV void gemm_lds_body(const uint16_t* __restrict__ A, const uint16_t* __
     asm volatile("" ::: "memory");
     Frags f0, f1;
     load_frags(0, 0, f0);
-    for (uint64_t it = 0; it < nk; ++it) {
-      const int stage = (int)(it & 1);
-      load_frags(stage, 32, f1);
-      mma(f0);
-      if (it + 1 < nk) {
+    if (!ILV) {
+      for (uint64_t it = 0; it < nk; ++it) {
+        const int stage = (int)(it & 1);
+        load_frags(stage, 32, f1);
+        mma(f0);
+        if (it + 1 < nk) {
+          __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): f1 has landed
+          CATENA_WAIT_VMCNT(0);                // this wave's slab it+1 has landed
+          asm volatile("" ::: "memory");
+          __builtin_amdgcn_s_barrier();
+          asm volatile("" ::: "memory");
+          if (it + 2 < nk) issue(it + 2, stage);
+          load_frags(stage ^ 1, 0, f0);
+        }
+        mma(f1);
+      }
+    } else {
+      for (uint64_t it = 0; it + 1 < nk; ++it) {
+        const int stage = (int)(it & 1);
+        load_mma(stage, 32, f1, f0);
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): f1 has landed
         CATENA_WAIT_VMCNT(0);                // this wave's slab it+1 has landed
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         if (it + 2 < nk) issue(it + 2, stage);
-        load_frags(stage ^ 1, 0, f0);
+        load_mma(stage ^ 1, 0, f0, f1);
       }
+      load_mma((int)((nk - 1) & 1), 32, f1, f0);
       mma(f1);
     }
   }
@@ -258,21 +334,29 @@ CATENA_DEV void gemm_lds_body(const uint16_t* __restrict__ A, const uint16_t* __
 }
 }  // namespace
 
-#define CATENA_GEMM_LDS_KERNEL(NAME, OUTB, PIPE, PRIO)                                    \
+#define CATENA_GEMM_LDS_KERNEL(NAME, OUTB, PIPE, PRIO, ILV, FRONT)                        \
   extern "C" __global__ __launch_bounds__(512) void NAME(                                 \
       const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C, \
       uint64_t M, uint64_t N, uint64_t K) {                                               \
-    gemm_lds_body<OUTB, PIPE, PRIO>(A, B, C, M, N, K);                                    \
+    gemm_lds_body<OUTB, PIPE, PRIO, ILV, FRONT>(A, B, C, M, N, K);                        \
   }
 
 // Scheduling variants (same arithmetic and order; selected by the host):
 //   v0 two barriers per slab; v1 = v0 + MFMA priority; v2 one barrier per
-//   slab with fragment double-buffering; v3 = v2 + MFMA priority.
-CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v0_bf16out, true, false, false)
-CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v1_bf16out, true, false, true)
-CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v2_bf16out, true, true, false)
-CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v3_bf16out, true, true, true)
-CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v0_f32out, false, false, false)
-CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v1_f32out, false, false, true)
-CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v2_f32out, false, true, false)
-CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v3_f32out, false, true, true)
+//   slab with fragment double-buffering; v3 = v2 + MFMA priority; v4 = v2
+//   with LDS reads interleaved 1:2 with MFMAs; v5 = v4 + MFMA priority;
+//   v7 = v4 with the reads front-loaded 1:1 into the first 16 MFMAs.
+CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v0_bf16out, true, false, false, false, false)
+CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v1_bf16out, true, false, true, false, false)
+CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v2_bf16out, true, true, false, false, false)
+CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v3_bf16out, true, true, true, false, false)
+CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v4_bf16out, true, true, false, true, false)
+CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v5_bf16out, true, true, true, true, false)
+CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v7_bf16out, true, true, false, true, true)
+CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v0_f32out, false, false, false, false, false)
+CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v1_f32out, false, false, true, false, false)
+CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v2_f32out, false, true, false, false, false)
+CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v3_f32out, false, true, true, false, false)
+CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v4_f32out, false, true, false, true, false)
+CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v5_f32out, false, true, true, true, false)
+CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v7_f32out, false, true, false, true, true)
