@@ -38,6 +38,19 @@ import catena_amd as ca  # noqa: E402
 METRIC = "det. bf16 GEMM TFLOP/s (%MFMA peak); KV-cache decode attention HBM GB/s"
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (copy-kernel calibrated), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            d = json.load(f)
+        k = d["kernels"][kernel]
+        return int(k["fetch_kib_raw"] * 1024 * d["fetch_factor"] + k["write_kib_raw"] * 1024 * d["write_factor"])
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 class HipEvents:
@@ -216,7 +229,8 @@ def main(argv=None) -> int:
                 "workload": "B=32 H=32 D=128 L=4096 bf16 KV, f32 softmax/out, bitwise vs sequential oracle",
                 "us_per_launch": at["us"], "GB/s": at["GB/s"], "bitwise_run_to_run": at["bitwise_run_to_run"],
                 "roofline": {"bound": "hbm", "achieved": at["GB/s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                             "frac": at["frac_hbm"], "traffic": None},
+                             "frac": at["frac_hbm"],
+                             "traffic": measured_traffic("catena_attn_decode_bf16_d128_kc")},
                 "bytes_per_launch": at["bytes_per_launch"]},
             "decode_gemm_m16": dg,
         }
@@ -258,7 +272,8 @@ def main(argv=None) -> int:
                    "M": 4096, "N": 4096, "K": 4096, "parallelism": "single GPU"},
         "bitwise_run_to_run": g["bitwise_run_to_run"],
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None},
+                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": measured_traffic("catena_gemm_bf16_lds_v7_bf16out")},
         "cpu_baseline": cpu,
         "extra": extra,
     }
