@@ -72,6 +72,18 @@ def lib():
                                      ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                      ctypes.c_float, _u32p, ctypes.c_uint32, ctypes.c_int]
         L.or_attn_decode.restype = None
+        for name in ("or_sqrt_newton", "or_sigmoid", "or_silu", "or_sin_approx", "or_cos_approx",
+                     "or_sin_full", "or_cos_full"):
+            getattr(L, name).argtypes = [ctypes.c_float]
+            getattr(L, name).restype = ctypes.c_float
+        L.or_rmsnorm_f32.argtypes = [_f32p, _f32p, ctypes.c_uint64]
+        L.or_rmsnorm_f32.restype = None
+        L.or_argmax_f32.argtypes = [_f32p, ctypes.c_uint64]
+        L.or_argmax_f32.restype = ctypes.c_uint64
+        L.or_rope_inv_freq.argtypes = [_f32p, ctypes.c_uint32, ctypes.c_double]
+        L.or_rope_inv_freq.restype = None
+        L.or_rope_f32.argtypes = [_f32p, ctypes.c_uint32, _f32p, ctypes.c_uint32]
+        L.or_rope_f32.restype = None
         _lib = L
     return _lib
 
@@ -180,3 +192,43 @@ def attn_decode(q, k, v, lens, scale: float, heads=None, threads: int | None = N
                          _p(o, _f32p), B, H, L, D, float(scale), _p(hl, _u32p),
                          0 if hl is None else hl.size, threads or default_threads())
     return o
+
+
+# ---------------------------------------------------------------- decoder-block pieces
+def scalar(name: str, x: float) -> float:
+    return getattr(lib(), "or_" + name)(float(x))
+
+
+def scalar_vec(name: str, x: np.ndarray) -> np.ndarray:
+    f = getattr(lib(), "or_" + name)
+    return np.array([f(float(v)) for v in np.asarray(x, np.float32).ravel()], np.float32)
+
+
+def rmsnorm_f32(x: np.ndarray) -> np.ndarray:
+    """nn.rmsnorm per row of a 1-D or 2-D array."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    rows = x.reshape(-1, x.shape[-1])
+    out = y.reshape(-1, x.shape[-1])
+    for r in range(rows.shape[0]):
+        lib().or_rmsnorm_f32(_p(rows[r], _f32p), _p(out[r], _f32p), rows.shape[1])
+    return y
+
+
+def argmax_f32(x: np.ndarray) -> int:
+    x = np.ascontiguousarray(x, np.float32)
+    return int(lib().or_argmax_f32(_p(x, _f32p), x.size))
+
+
+def rope_inv_freq(d: int, base: float) -> np.ndarray:
+    out = np.empty(d // 2, np.float32)
+    lib().or_rope_inv_freq(_p(out, _f32p), d, float(base))
+    return out
+
+
+def rope_f32(x: np.ndarray, pos: int, inv_freq: np.ndarray) -> np.ndarray:
+    """Rotate one head vector (copy)."""
+    y = np.ascontiguousarray(x, np.float32).copy()
+    f = np.ascontiguousarray(inv_freq, np.float32)
+    lib().or_rope_f32(_p(y, _f32p), int(pos), _p(f, _f32p), y.size)
+    return y

@@ -28,6 +28,16 @@
  *   or_attn_decode        pinned: float64 attention within the softmax
  *                         tolerance, brute-force composition of the pinned
  *                         pieces on tiny shapes, uniform-V / one-hot cases.
+ *   or_sqrt_newton        pinned: closed forms (1, 4, 0, negatives), libm on
+ *                         the converging range, the reference's divergence
+ *                         for large inputs (guess0 = x).
+ *   or_sigmoid/or_silu    pinned: closed form at 0, libm within exp~'s error.
+ *   or_sin/cos_full       pinned: libm within the Taylor remainder bound,
+ *                         exact 0/1 at 0, odd/even symmetry.
+ *   or_rmsnorm_f32        pinned: reference test (tests/runtime.rs:1011-1044).
+ *   or_argmax_f32         pinned: reference cases (tests/runtime.rs:1176-1197).
+ *   or_rope_f32           pinned: identity at pos 0, norm preservation,
+ *                         float64 rotation with libm cos/sin.
  */
 #ifndef CATENA_ORACLE_H
 #define CATENA_ORACLE_H
@@ -72,6 +82,19 @@ void or_attn_decode(const uint16_t *q, const uint16_t *k, const uint16_t *v,
                     const uint32_t *lens, float *o, uint32_t B, uint32_t H,
                     uint32_t L, uint32_t D, float scale,
                     const uint32_t *bh_list, uint32_t nbh, int threads);
+
+/* ---- decoder-block pieces (catena_oracle_block.c) ---- */
+float or_sqrt_newton(float x);   /* math.sqrt */
+float or_sigmoid(float x);       /* nn.sigmoid */
+float or_silu(float x);          /* nn.silu */
+float or_sin_approx(float x);    /* math.sin-approx */
+float or_cos_approx(float x);    /* math.cos-approx */
+float or_sin_full(float x);      /* math.sin-approx-full */
+float or_cos_full(float x);      /* this build's full-range cosine */
+void or_rmsnorm_f32(const float *x, float *y, uint64_t n);   /* nn.rmsnorm */
+uint64_t or_argmax_f32(const float *x, uint64_t n);           /* tensor.argmax-f32 */
+void or_rope_inv_freq(float *inv_freq, uint32_t d, double base);
+void or_rope_f32(float *x, uint32_t pos, const float *inv_freq, uint32_t d);
 
 #ifdef __cplusplus
 }
