@@ -8,6 +8,8 @@ no Python or CPU fallback; if the library or its code objects are missing,
 Layout mirrors the C header:
   * device/pool:   init, Buffer (catena_mem_t), synchronize, stream
   * kernel ABI:    gemm_f32_exact, gemm_bf16, attn_decode_bf16, softmax_f32, ...
+                   and the decoder-block pieces (rmsnorm, rope, silu_mul, argmax, ...)
+  * decoder:       Decoder (catena_mi355x_decoder_*)
   * program ABI:   program_* functions (fail-stop: they trap on bad input)
   * runtime:       Runtime (catena_runtime_*), mirrors Runtime::from_sources /
                    exec / mem_* of catena-lang/src/runtime/runtime.rs:104-247
@@ -124,6 +126,22 @@ SIGNATURES = {
     "catena_mi355x_fill_normal_bf16": (_int, [_vp, _u64, _u64, _u64, _f32]),
     "catena_mi355x_fill_uniform_f32": (_int, [_vp, _u64, _u64, _u64]),
     "catena_mi355x_copy_bytes": (_int, [_vp, _vp, _u64]),
+    "catena_mi355x_attn_causal_bf16": (_int, [_vp] * 5 + [_u32] * 5 + [_f32, _int]),
+    "catena_mi355x_rmsnorm_f32": (_int, [_vp, _vp, _u64, _u64]),
+    "catena_mi355x_residual_rmsnorm_bf16": (_int, [_vp] * 5 + [_u64, _u64]),
+    "catena_mi355x_embed_bf16": (_int, [_vp, _vp, _vp, _u64, _u32, _u32]),
+    "catena_mi355x_rope_inv_freq": (_int, [ctypes.POINTER(_f32), _u32, ctypes.c_double]),
+    "catena_mi355x_rope_qkv_bf16": (_int, [_vp] * 6 + [_u32] * 5),
+    "catena_mi355x_silu_mul_bf16": (_int, [_vp, _vp, _u64, _u32]),
+    "catena_mi355x_argmax_f32": (_int, [_vp, _vp, _u64, _u64]),
+    "program_nn_rmsnorm": (None, [Mem, ctypes.POINTER(Mem)]),
+    "program_tensor_argmax_f32": (None, [Mem, ctypes.POINTER(_u64)]),
+    "catena_mi355x_decoder_create": (_int, [_vp, ctypes.POINTER(_vp)]),
+    "catena_mi355x_decoder_destroy": (None, [_vp]),
+    "catena_mi355x_decoder_tensor": (_int, [_vp, _u32, _u32, ctypes.POINTER(Mem)]),
+    "catena_mi355x_decoder_init_weights": (_int, [_vp, _u64, _f32]),
+    "catena_mi355x_decoder_prefill": (_int, [_vp, _vp, _u32, _u32, _vp]),
+    "catena_mi355x_decoder_generate": (_int, [_vp, _u32, _vp]),
     "program_matmul_2x2_via_mem": (None, [Mem, Mem] + [_u64] * 6 + [ctypes.POINTER(Mem)]),
     "program_matmul_right_identity_2x2_via_mem": (None, [Mem, _u64, _u64, ctypes.POINTER(Mem)]),
     "program_matmul_left_identity_2x2_via_mem": (None, [Mem, _u64, _u64, ctypes.POINTER(Mem)]),
@@ -274,6 +292,103 @@ def fill_uniform_f32(out, n: int, seed: int, stream_id: int) -> None:
 
 def copy_bytes(dst, src, n: int) -> None:
     check(lib().catena_mi355x_copy_bytes(_p(dst), _p(src), n))
+
+
+def attn_causal_bf16(q, k, v, lens, o, batch: int, tq: int, heads: int, max_len: int,
+                     head_dim: int, scale: float, out_f32: bool = False) -> None:
+    check(lib().catena_mi355x_attn_causal_bf16(_p(q), _p(k), _p(v), _p(lens), _p(o), batch, tq,
+                                               heads, max_len, head_dim, scale,
+                                               1 if out_f32 else 0))
+
+
+def rmsnorm_f32(x, y, rows: int, n: int) -> None:
+    check(lib().catena_mi355x_rmsnorm_f32(_p(x), _p(y), rows, n))
+
+
+def residual_rmsnorm_bf16(x, resid, row_index, h_out, y, rows: int, n: int) -> None:
+    opt = lambda b: None if b is None else _p(b)  # noqa: E731
+    check(lib().catena_mi355x_residual_rmsnorm_bf16(_p(x), opt(resid), opt(row_index), opt(h_out),
+                                                    _p(y), rows, n))
+
+
+def embed_bf16(tokens, table, x, rows: int, vocab: int, d: int) -> None:
+    check(lib().catena_mi355x_embed_bf16(_p(tokens), _p(table), _p(x), rows, vocab, d))
+
+
+def rope_inv_freq(head_dim: int, base: float) -> np.ndarray:
+    out = np.empty(head_dim // 2, np.float32)
+    check(lib().catena_mi355x_rope_inv_freq(out.ctypes.data_as(ctypes.POINTER(_f32)), head_dim,
+                                            float(base)))
+    return out
+
+
+def rope_qkv_bf16(qkv, inv_freq, lens, q, k_cache, v_cache, batch: int, tq: int, heads: int,
+                  head_dim: int, max_len: int) -> None:
+    check(lib().catena_mi355x_rope_qkv_bf16(_p(qkv), _p(inv_freq), _p(lens), _p(q), _p(k_cache),
+                                            _p(v_cache), batch, tq, heads, head_dim, max_len))
+
+
+def silu_mul_bf16(gu, out, rows: int, ffn: int) -> None:
+    check(lib().catena_mi355x_silu_mul_bf16(_p(gu), _p(out), rows, ffn))
+
+
+def argmax_f32(x, idx, rows: int, n: int) -> None:
+    check(lib().catena_mi355x_argmax_f32(_p(x), _p(idx), rows, n))
+
+
+# ------------------------------------------------------------------ decoder
+class DecoderConfig(ctypes.Structure):
+    """catena_decoder_config_t."""
+    _fields_ = [("d_model", _u32), ("n_heads", _u32), ("head_dim", _u32), ("ffn_dim", _u32),
+                ("n_layers", _u32), ("vocab", _u32), ("max_batch", _u32), ("max_len", _u32),
+                ("rope_base", _f32)]
+
+
+# catena_decoder_tensor_t
+(DEC_EMBED, DEC_W_QKV, DEC_W_O, DEC_W_GU, DEC_W_DOWN, DEC_W_LM, DEC_K_CACHE, DEC_V_CACHE,
+ DEC_INV_FREQ, DEC_X, DEC_XN, DEC_QKV, DEC_Q, DEC_ATTN, DEC_ATTN_PROJ, DEC_H, DEC_HN, DEC_GU,
+ DEC_ACT, DEC_FFN_OUT, DEC_FINAL_H, DEC_FINAL_XN, DEC_LOGITS, DEC_LENS) = range(24)
+
+
+class Decoder:
+    """Handle of a catena_decoder_t (device-resident weights, caches and
+    activations; prefill / generate enqueue on the library stream)."""
+
+    def __init__(self, d_model: int, n_heads: int, ffn_dim: int, n_layers: int, vocab: int,
+                 max_batch: int, max_len: int, head_dim: int = 128, rope_base: float = 10000.0):
+        self.cfg = DecoderConfig(d_model, n_heads, head_dim, ffn_dim, n_layers, vocab, max_batch,
+                                 max_len, rope_base)
+        h = _vp()
+        check(lib().catena_mi355x_decoder_create(ctypes.byref(self.cfg), ctypes.byref(h)))
+        self._h = h
+
+    def tensor(self, which: int, layer: int = 0) -> Mem:
+        m = Mem()
+        check(lib().catena_mi355x_decoder_tensor(self._h, which, layer, ctypes.byref(m)))
+        return m
+
+    def read(self, which: int, dtype, layer: int = 0) -> np.ndarray:
+        return mem_to_array(self.tensor(which, layer), dtype)
+
+    def init_weights(self, seed: int, std: float = 0.02) -> None:
+        check(lib().catena_mi355x_decoder_init_weights(self._h, seed, std))
+
+    def prefill(self, tokens, batch: int, t: int, next_tokens) -> None:
+        check(lib().catena_mi355x_decoder_prefill(self._h, _p(tokens), batch, t, _p(next_tokens)))
+
+    def generate(self, steps: int, out) -> None:
+        check(lib().catena_mi355x_decoder_generate(self._h, steps, _p(out)))
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().catena_mi355x_decoder_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 # ------------------------------------------------------------------ runtime

@@ -1,0 +1,349 @@
+// Llama-style decoder built from the library's kernels: the model the two
+// hot contractions (bf16 GEMM, KV-cache attention) serve.  No reference
+// counterpart; its pieces mirror the reference's stdlib ops (nn.rmsnorm,
+// nn.silu, math.sin-approx-full, tensor.argmax-f32) bit for bit, and the
+// GEMMs follow the bf16 contraction contract of catena_mi355x_gemm_bf16.
+//
+// Everything after create() is stream-ordered on the library stream with no
+// host synchronisation: prefill and the greedy generate loop enqueue their
+// kernels and return; the argmax of step s feeds the embedding gather of
+// step s + 1 on the device.  Sequence lengths are uniform across the batch,
+// so the per-sequence lengths a step needs are rows of a table uploaded once
+// (lens_table[t][b] = t).
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "internal.h"
+
+using namespace catena;
+
+struct catena_decoder {
+  catena_decoder_config_t cfg{};
+  uint64_t d = 0, f = 0;
+  // weights and caches
+  void* embed = nullptr;
+  void* w_lm = nullptr;
+  void* inv_freq = nullptr;
+  void* lens_table = nullptr;  // [(max_len + 1)][max_batch] u32
+  std::vector<void*> w_qkv, w_o, w_gu, w_down, kc, vc;
+  // activations (capacity rows_cap rows) and per-sequence buffers
+  uint64_t rows_cap = 0;
+  void* act[CATENA_DEC_TENSOR_COUNT] = {};
+  void* final_rows = nullptr;  // [max_batch] u32: index of each sequence's last row
+  void* cur_tok = nullptr;     // [max_batch] u32: next input token per sequence
+  uint32_t batch = 0, cur_len = 0, last_rows = 0;
+};
+
+namespace {
+
+uint64_t kv_elems(const catena_decoder& m) {
+  return (uint64_t)m.cfg.max_batch * m.cfg.n_heads * m.cfg.max_len * m.cfg.head_dim;
+}
+
+// bytes per row of each activation tensor
+uint64_t act_row_bytes(const catena_decoder& m, int which) {
+  switch (which) {
+    case CATENA_DEC_X: case CATENA_DEC_ATTN_PROJ: case CATENA_DEC_H: case CATENA_DEC_FFN_OUT:
+      return m.d * 4;
+    case CATENA_DEC_XN: case CATENA_DEC_Q: case CATENA_DEC_ATTN: case CATENA_DEC_HN:
+      return m.d * 2;
+    case CATENA_DEC_QKV: return 3 * m.d * 4;
+    case CATENA_DEC_GU: return 2 * m.f * 4;
+    case CATENA_DEC_ACT: return m.f * 2;
+    default: return 0;
+  }
+}
+
+// per-batch-row tensors, sized for max_batch
+uint64_t batch_tensor_bytes(const catena_decoder& m, int which) {
+  switch (which) {
+    case CATENA_DEC_FINAL_H: return m.cfg.max_batch * m.d * 4;
+    case CATENA_DEC_FINAL_XN: return m.cfg.max_batch * m.d * 2;
+    case CATENA_DEC_LOGITS: return (uint64_t)m.cfg.max_batch * m.cfg.vocab * 4;
+    default: return 0;
+  }
+}
+
+int alloc(uint64_t bytes, void** p) { return pool_alloc(bytes, p); }
+
+int ensure_rows(catena_decoder& m, uint64_t rows) {
+  if (rows <= m.rows_cap) return CATENA_OK;
+  // queued kernels may still use the old buffers
+  int st = hip_check(hipStreamSynchronize(device().stream), "hipStreamSynchronize");
+  if (st) return st;
+  for (int w = CATENA_DEC_X; w <= CATENA_DEC_FFN_OUT; ++w) {
+    pool_free(m.act[w]);
+    m.act[w] = nullptr;
+  }
+  m.rows_cap = 0;
+  for (int w = CATENA_DEC_X; w <= CATENA_DEC_FFN_OUT; ++w) {
+    st = alloc(rows * act_row_bytes(m, w), &m.act[w]);
+    if (st) return st;
+  }
+  m.rows_cap = rows;
+  return CATENA_OK;
+}
+
+void release(catena_decoder* m) {
+  pool_free(m->embed);
+  pool_free(m->w_lm);
+  pool_free(m->inv_freq);
+  pool_free(m->lens_table);
+  for (auto* v : {&m->w_qkv, &m->w_o, &m->w_gu, &m->w_down, &m->kc, &m->vc})
+    for (void* p : *v) pool_free(p);
+  for (void*& p : m->act) {
+    if (p) pool_free(p);
+    p = nullptr;
+  }
+  pool_free(m->final_rows);
+  pool_free(m->cur_tok);
+}
+
+#define TRY(expr)              \
+  do {                         \
+    int st_ = (expr);          \
+    if (st_) return st_;       \
+  } while (0)
+
+// One forward pass over rows = batch * tq tokens (tq per sequence), caches
+// already holding the earlier positions; lens = positions after the append;
+// final_rows selects each sequence's last row (NULL when tq == 1); next
+// receives the greedy tokens.
+int forward(catena_decoder& m, const uint32_t* tokens, uint32_t batch, uint32_t tq,
+            const uint32_t* lens, const uint32_t* final_rows, uint32_t* next) {
+  const catena_decoder_config_t& c = m.cfg;
+  const uint64_t rows = (uint64_t)batch * tq, d = m.d, f = m.f;
+  TRY(ensure_rows(m, rows));
+  auto A = [&](int w) { return m.act[w]; };
+  float* X = static_cast<float*>(A(CATENA_DEC_X));
+  uint16_t* XN = static_cast<uint16_t*>(A(CATENA_DEC_XN));
+  float* QKV = static_cast<float*>(A(CATENA_DEC_QKV));
+  uint16_t* Q = static_cast<uint16_t*>(A(CATENA_DEC_Q));
+  uint16_t* ATT = static_cast<uint16_t*>(A(CATENA_DEC_ATTN));
+  float* AP = static_cast<float*>(A(CATENA_DEC_ATTN_PROJ));
+  float* H = static_cast<float*>(A(CATENA_DEC_H));
+  uint16_t* HN = static_cast<uint16_t*>(A(CATENA_DEC_HN));
+  float* GU = static_cast<float*>(A(CATENA_DEC_GU));
+  uint16_t* ACT = static_cast<uint16_t*>(A(CATENA_DEC_ACT));
+  float* FO = static_cast<float*>(A(CATENA_DEC_FFN_OUT));
+  const float scale = (float)(1.0 / std::sqrt((double)c.head_dim));
+
+  TRY(catena_mi355x_embed_bf16(tokens, static_cast<const uint16_t*>(m.embed), X, rows, c.vocab,
+                               (uint32_t)d));
+  for (uint32_t l = 0; l < c.n_layers; ++l) {
+    // x_l = h_{l-1} + ffn_{l-1} (layer 0: the embedding), xn = bf16(rmsnorm(x_l))
+    if (l == 0)
+      TRY(catena_mi355x_residual_rmsnorm_bf16(X, nullptr, nullptr, nullptr, XN, rows, d));
+    else
+      TRY(catena_mi355x_residual_rmsnorm_bf16(H, FO, nullptr, X, XN, rows, d));
+    TRY(catena_mi355x_gemm_bf16(XN, static_cast<const uint16_t*>(m.w_qkv[l]), QKV, rows, 3 * d, d, 1));
+    uint16_t* kc = static_cast<uint16_t*>(m.kc[l]);
+    uint16_t* vc = static_cast<uint16_t*>(m.vc[l]);
+    TRY(catena_mi355x_rope_qkv_bf16(QKV, static_cast<const float*>(m.inv_freq), lens, Q, kc, vc,
+                                    batch, tq, c.n_heads, c.head_dim, c.max_len));
+    TRY(catena_mi355x_attn_causal_bf16(Q, kc, vc, lens, ATT, batch, tq, c.n_heads, c.max_len,
+                                       c.head_dim, scale, 0));
+    TRY(catena_mi355x_gemm_bf16(ATT, static_cast<const uint16_t*>(m.w_o[l]), AP, rows, d, d, 1));
+    TRY(catena_mi355x_residual_rmsnorm_bf16(X, AP, nullptr, H, HN, rows, d));
+    TRY(catena_mi355x_gemm_bf16(HN, static_cast<const uint16_t*>(m.w_gu[l]), GU, rows, 2 * f, d, 1));
+    TRY(catena_mi355x_silu_mul_bf16(GU, ACT, rows, (uint32_t)f));
+    TRY(catena_mi355x_gemm_bf16(ACT, static_cast<const uint16_t*>(m.w_down[l]), FO, rows, d, f, 1));
+  }
+  float* FH = static_cast<float*>(A(CATENA_DEC_FINAL_H));
+  uint16_t* FXN = static_cast<uint16_t*>(A(CATENA_DEC_FINAL_XN));
+  float* LG = static_cast<float*>(A(CATENA_DEC_LOGITS));
+  TRY(catena_mi355x_residual_rmsnorm_bf16(H, FO, final_rows, FH, FXN, batch, d));
+  TRY(catena_mi355x_gemm_bf16(FXN, static_cast<const uint16_t*>(m.w_lm), LG, batch, c.vocab, d, 1));
+  TRY(catena_mi355x_argmax_f32(LG, next, batch, c.vocab));
+  return CATENA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int catena_mi355x_decoder_create(const catena_decoder_config_t* cfg, catena_decoder_t** out) {
+  if (!out || !cfg) return fail(CATENA_ERR_INVALID_ARGUMENT, "null argument");
+  *out = nullptr;
+  int st = ensure_init();
+  if (st) return st;
+  const catena_decoder_config_t& c = *cfg;
+  if (c.head_dim != 128) return fail(CATENA_ERR_UNSUPPORTED, "decoder head_dim must be 128");
+  if (c.n_heads == 0 || c.n_layers == 0 || c.vocab == 0 || c.max_batch == 0 || c.max_len == 0 ||
+      c.ffn_dim == 0)
+    return fail(CATENA_ERR_INVALID_ARGUMENT, "decoder sizes must be non-zero");
+  if ((uint64_t)c.n_heads * c.head_dim != c.d_model)
+    return fail(CATENA_ERR_INVALID_ARGUMENT, "d_model must equal n_heads * head_dim");
+  if (c.ffn_dim % 8 != 0 || c.vocab % 8 != 0)
+    return fail(CATENA_ERR_INVALID_ARGUMENT, "ffn_dim and vocab must be multiples of 8");
+  if (!(c.rope_base > 1.0f)) return fail(CATENA_ERR_INVALID_ARGUMENT, "rope_base must exceed 1");
+
+  catena_decoder* m = new (std::nothrow) catena_decoder();
+  if (!m) return fail(CATENA_ERR_OUT_OF_MEMORY, "decoder allocation");
+  m->cfg = c;
+  m->d = c.d_model;
+  m->f = c.ffn_dim;
+  const uint64_t d = m->d, f = m->f;
+  auto fail_out = [&](int s) {
+    release(m);
+    delete m;
+    return s;
+  };
+  if ((st = alloc((uint64_t)c.vocab * d * 2, &m->embed))) return fail_out(st);
+  if ((st = alloc(d * c.vocab * 2, &m->w_lm))) return fail_out(st);
+  for (uint32_t l = 0; l < c.n_layers; ++l) {
+    void *a = nullptr, *b = nullptr, *g = nullptr, *dn = nullptr, *k = nullptr, *v = nullptr;
+    if ((st = alloc(d * 3 * d * 2, &a))) return fail_out(st);
+    m->w_qkv.push_back(a);
+    if ((st = alloc(d * d * 2, &b))) return fail_out(st);
+    m->w_o.push_back(b);
+    if ((st = alloc(d * 2 * f * 2, &g))) return fail_out(st);
+    m->w_gu.push_back(g);
+    if ((st = alloc(f * d * 2, &dn))) return fail_out(st);
+    m->w_down.push_back(dn);
+    if ((st = alloc(kv_elems(*m) * 2, &k))) return fail_out(st);
+    m->kc.push_back(k);
+    if ((st = alloc(kv_elems(*m) * 2, &v))) return fail_out(st);
+    m->vc.push_back(v);
+  }
+  for (int w = CATENA_DEC_FINAL_H; w <= CATENA_DEC_LOGITS; ++w)
+    if ((st = alloc(batch_tensor_bytes(*m, w), &m->act[w]))) return fail_out(st);
+  if ((st = alloc(c.max_batch * 4, &m->act[CATENA_DEC_LENS]))) return fail_out(st);
+  if ((st = alloc(c.max_batch * 4, &m->final_rows))) return fail_out(st);
+  if ((st = alloc(c.max_batch * 4, &m->cur_tok))) return fail_out(st);
+
+  // host-computed tables: RoPE frequencies and the uniform-length lens rows
+  std::vector<float> inv(c.head_dim / 2);
+  if ((st = catena_mi355x_rope_inv_freq(inv.data(), c.head_dim, (double)c.rope_base)))
+    return fail_out(st);
+  if ((st = alloc(inv.size() * 4, &m->inv_freq))) return fail_out(st);
+  std::vector<uint32_t> lt((uint64_t)(c.max_len + 1) * c.max_batch);
+  for (uint64_t t = 0; t <= c.max_len; ++t)
+    for (uint32_t b = 0; b < c.max_batch; ++b) lt[t * c.max_batch + b] = (uint32_t)t;
+  if ((st = alloc(lt.size() * 4, &m->lens_table))) return fail_out(st);
+  if ((st = catena_mem_write(catena_mem_t{m->inv_freq, inv.size() * 4}, 0, inv.data(), inv.size() * 4)))
+    return fail_out(st);
+  if ((st = catena_mem_write(catena_mem_t{m->lens_table, lt.size() * 4}, 0, lt.data(), lt.size() * 4)))
+    return fail_out(st);
+  *out = m;
+  return CATENA_OK;
+}
+
+void catena_mi355x_decoder_destroy(catena_decoder_t* dec) {
+  if (!dec) return;
+  hipStreamSynchronize(device().stream);
+  release(dec);
+  delete dec;
+}
+
+int catena_mi355x_decoder_tensor(catena_decoder_t* dec, uint32_t which, uint32_t layer,
+                                 catena_mem_t* out) {
+  if (!dec || !out) return fail(CATENA_ERR_INVALID_ARGUMENT, "null argument");
+  catena_decoder& m = *dec;
+  const catena_decoder_config_t& c = m.cfg;
+  const bool per_layer = which == CATENA_DEC_W_QKV || which == CATENA_DEC_W_O ||
+                         which == CATENA_DEC_W_GU || which == CATENA_DEC_W_DOWN ||
+                         which == CATENA_DEC_K_CACHE || which == CATENA_DEC_V_CACHE;
+  if (per_layer && layer >= c.n_layers)
+    return fail(CATENA_ERR_INVALID_ARGUMENT, "layer %u out of range", layer);
+  const uint64_t d = m.d, f = m.f;
+  switch (which) {
+    case CATENA_DEC_EMBED: *out = {m.embed, (uint64_t)c.vocab * d * 2}; break;
+    case CATENA_DEC_W_QKV: *out = {m.w_qkv[layer], d * 3 * d * 2}; break;
+    case CATENA_DEC_W_O: *out = {m.w_o[layer], d * d * 2}; break;
+    case CATENA_DEC_W_GU: *out = {m.w_gu[layer], d * 2 * f * 2}; break;
+    case CATENA_DEC_W_DOWN: *out = {m.w_down[layer], f * d * 2}; break;
+    case CATENA_DEC_W_LM: *out = {m.w_lm, d * c.vocab * 2}; break;
+    case CATENA_DEC_K_CACHE: *out = {m.kc[layer], kv_elems(m) * 2}; break;
+    case CATENA_DEC_V_CACHE: *out = {m.vc[layer], kv_elems(m) * 2}; break;
+    case CATENA_DEC_INV_FREQ: *out = {m.inv_freq, (uint64_t)c.head_dim / 2 * 4}; break;
+    case CATENA_DEC_FINAL_H: case CATENA_DEC_FINAL_XN: case CATENA_DEC_LOGITS:
+      *out = {m.act[which], batch_tensor_bytes(m, (int)which) / c.max_batch * m.batch};
+      break;
+    case CATENA_DEC_LENS: *out = {m.act[which], (uint64_t)m.batch * 4}; break;
+    default:
+      if (which >= CATENA_DEC_X && which <= CATENA_DEC_FFN_OUT) {
+        *out = {m.act[which], m.act[which] ? m.last_rows * act_row_bytes(m, (int)which) : 0};
+        break;
+      }
+      return fail(CATENA_ERR_INVALID_ARGUMENT, "unknown decoder tensor %u", which);
+  }
+  return CATENA_OK;
+}
+
+int catena_mi355x_decoder_init_weights(catena_decoder_t* dec, uint64_t seed, float std) {
+  if (!dec) return fail(CATENA_ERR_INVALID_ARGUMENT, "null decoder");
+  catena_decoder& m = *dec;
+  const uint64_t d = m.d, f = m.f, V = m.cfg.vocab;
+  TRY(catena_mi355x_fill_normal_bf16(static_cast<uint16_t*>(m.embed), V * d, seed, 0, std));
+  TRY(catena_mi355x_fill_normal_bf16(static_cast<uint16_t*>(m.w_lm), d * V, seed, 1, std));
+  for (uint32_t l = 0; l < m.cfg.n_layers; ++l) {
+    const uint64_t s = 16 + 4ull * l;
+    TRY(catena_mi355x_fill_normal_bf16(static_cast<uint16_t*>(m.w_qkv[l]), d * 3 * d, seed, s, std));
+    TRY(catena_mi355x_fill_normal_bf16(static_cast<uint16_t*>(m.w_o[l]), d * d, seed, s + 1, std));
+    TRY(catena_mi355x_fill_normal_bf16(static_cast<uint16_t*>(m.w_gu[l]), d * 2 * f, seed, s + 2, std));
+    TRY(catena_mi355x_fill_normal_bf16(static_cast<uint16_t*>(m.w_down[l]), f * d, seed, s + 3, std));
+  }
+  return CATENA_OK;
+}
+
+int catena_mi355x_decoder_prefill(catena_decoder_t* dec, const uint32_t* tokens, uint32_t batch,
+                                  uint32_t t, uint32_t* next) {
+  if (!dec || !tokens || !next) return fail(CATENA_ERR_INVALID_ARGUMENT, "null argument");
+  catena_decoder& m = *dec;
+  const catena_decoder_config_t& c = m.cfg;
+  if (batch == 0 || batch > c.max_batch)
+    return fail(CATENA_ERR_INVALID_ARGUMENT, "batch %u outside 1..%u", batch, c.max_batch);
+  if (t == 0 || t > c.max_len)
+    return fail(CATENA_ERR_INVALID_ARGUMENT, "prefill length %u outside 1..%u", t, c.max_len);
+  std::vector<uint32_t> rows(batch);
+  for (uint32_t b = 0; b < batch; ++b) rows[b] = b * t + (t - 1);
+  Device& dv = device();
+  // pageable source: HIP stages it before the call returns
+  TRY(hip_check(hipMemcpyAsync(m.final_rows, rows.data(), batch * 4, hipMemcpyHostToDevice,
+                               dv.stream),
+                "hipMemcpyAsync(final rows)"));
+  const uint32_t* lens = static_cast<const uint32_t*>(m.lens_table) + (uint64_t)t * c.max_batch;
+  m.batch = batch;
+  m.last_rows = batch * t;
+  TRY(forward(m, tokens, batch, t, lens, static_cast<const uint32_t*>(m.final_rows),
+              static_cast<uint32_t*>(m.cur_tok)));
+  m.cur_len = t;
+  TRY(hip_check(hipMemcpyAsync(m.act[CATENA_DEC_LENS], lens, batch * 4, hipMemcpyDeviceToDevice,
+                               dv.stream),
+                "hipMemcpyAsync(lens)"));
+  return hip_check(hipMemcpyAsync(next, m.cur_tok, batch * 4, hipMemcpyDeviceToDevice, dv.stream),
+                   "hipMemcpyAsync(next)");
+}
+
+int catena_mi355x_decoder_generate(catena_decoder_t* dec, uint32_t steps, uint32_t* out) {
+  if (!dec || (steps > 0 && !out)) return fail(CATENA_ERR_INVALID_ARGUMENT, "null argument");
+  catena_decoder& m = *dec;
+  const catena_decoder_config_t& c = m.cfg;
+  if (m.batch == 0) return fail(CATENA_ERR_INVALID_ARGUMENT, "generate before prefill");
+  if ((uint64_t)m.cur_len + steps > c.max_len)
+    return fail(CATENA_ERR_INVALID_ARGUMENT, "%u steps after %u positions overflow the %u-position cache",
+                steps, m.cur_len, c.max_len);
+  if (steps == 0) return CATENA_OK;
+  const uint32_t B = m.batch;
+  for (uint32_t s = 0; s < steps; ++s) {
+    const uint32_t* in = s == 0 ? static_cast<const uint32_t*>(m.cur_tok) : out + (uint64_t)(s - 1) * B;
+    const uint32_t* lens =
+        static_cast<const uint32_t*>(m.lens_table) + (uint64_t)(m.cur_len + 1) * c.max_batch;
+    m.last_rows = B;
+    TRY(forward(m, in, B, 1, lens, nullptr, out + (uint64_t)s * B));
+    m.cur_len += 1;
+  }
+  Device& dv = device();
+  const uint32_t* lens = static_cast<const uint32_t*>(m.lens_table) + (uint64_t)m.cur_len * c.max_batch;
+  TRY(hip_check(hipMemcpyAsync(m.act[CATENA_DEC_LENS], lens, B * 4, hipMemcpyDeviceToDevice, dv.stream),
+                "hipMemcpyAsync(lens)"));
+  return hip_check(hipMemcpyAsync(m.cur_tok, out + (uint64_t)(steps - 1) * B, B * 4,
+                                  hipMemcpyDeviceToDevice, dv.stream),
+                   "hipMemcpyAsync(cur_tok)");
+}
+
+}  // extern "C"

@@ -78,6 +78,13 @@ const KernelSpec kKernels[] = {
     {KernelId::GemmBf16DecodeReduce, "gemm_bf16_decode", "catena_gemm_bf16_decode_reduce"},
     {KernelId::AttnDecodeD128, "attn_decode", "catena_attn_decode_bf16_d128"},
     {KernelId::AttnDecodeD128KC, "attn_decode", "catena_attn_decode_bf16_d128_kc"},
+    {KernelId::AttnCausalD128F32, "attn_decode", "catena_attn_causal_bf16_d128_f32out"},
+    {KernelId::AttnCausalD128Bf16, "attn_decode", "catena_attn_causal_bf16_d128_bf16out"},
+    {KernelId::EmbedRowsBf16, "block", "catena_embed_rows_bf16"},
+    {KernelId::RmsnormRows, "block", "catena_rmsnorm_rows"},
+    {KernelId::RopeQkvStore, "block", "catena_rope_qkv_store"},
+    {KernelId::SiluMulBf16, "block", "catena_silu_mul_bf16"},
+    {KernelId::ArgmaxRowsF32, "block", "catena_argmax_rows_f32"},
     {KernelId::SoftmaxRows, "softmax", "catena_softmax_rows_f32"},
     {KernelId::ExpApprox, "softmax", "catena_exp_approx_f32"},
     {KernelId::FillNormalBf16, "fill", "catena_fill_normal_bf16"},

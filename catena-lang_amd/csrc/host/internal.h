@@ -38,6 +38,13 @@ enum class KernelId : int {
   GemmBf16DecodeReduce,
   AttnDecodeD128,
   AttnDecodeD128KC,
+  AttnCausalD128F32,
+  AttnCausalD128Bf16,
+  EmbedRowsBf16,
+  RmsnormRows,
+  RopeQkvStore,
+  SiluMulBf16,
+  ArgmaxRowsF32,
   SoftmaxRows,
   ExpApprox,
   FillNormalBf16,

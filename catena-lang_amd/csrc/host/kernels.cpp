@@ -90,28 +90,27 @@ int catena_mi355x_gemm_bf16(const uint16_t* a, const uint16_t* b, void* c, uint6
     const uint64_t S = ceil_div(chunks, 4);
     const uint64_t gx = ceil_div(m, 128);
     if (S > 65535 || gx > 0x7FFFFFFFu) return fail(CATENA_ERR_UNSUPPORTED, "decode grid too large");
-    if (out_f32 == 0) {
-      float* P = nullptr;
-      if (S > 1) {
-        void* ws = nullptr;
-        st = workspace(S * M * m * sizeof(float), &ws);
-        if (st) return st;
-        P = static_cast<float*>(ws);
-      }
-      const uint16_t* X = a;
-      const uint16_t* W = b;
-      uint16_t* Y = static_cast<uint16_t*>(c);
-      uint64_t N = m, K = k;
-      void* args[] = {&X, &W, &Y, &P, (void*)&M, &N, &K, (void*)&kw};
-      st = launch(KernelId::GemmBf16Decode, dim3((unsigned)gx, (unsigned)S), dim3(256), 0, args);
-      if (st || S == 1) return st;
-      uint32_t S32 = (uint32_t)S;
-      const uint64_t total4 = (uint64_t)M * m / 4;
-      const float* Pc = P;
-      void* rargs[] = {&Pc, &Y, (void*)&M, &N, &S32};
-      return launch(KernelId::GemmBf16DecodeReduce, dim3((unsigned)ceil_div(total4, 256)), dim3(256),
-                    0, rargs);
+    float* P = nullptr;
+    if (S > 1) {
+      void* ws = nullptr;
+      st = workspace(S * M * m * sizeof(float), &ws);
+      if (st) return st;
+      P = static_cast<float*>(ws);
     }
+    const uint16_t* X = a;
+    const uint16_t* W = b;
+    void* Y = c;
+    uint64_t N = m, K = k;
+    uint32_t of32 = out_f32 ? 1u : 0u;
+    void* args[] = {&X, &W, &Y, &P, (void*)&M, &N, &K, (void*)&kw, &of32};
+    st = launch(KernelId::GemmBf16Decode, dim3((unsigned)gx, (unsigned)S), dim3(256), 0, args);
+    if (st || S == 1) return st;
+    uint32_t S32 = (uint32_t)S;
+    const uint64_t total4 = (uint64_t)M * m / 4;
+    const float* Pc = P;
+    void* rargs[] = {&Pc, &Y, (void*)&M, &N, &S32, &of32};
+    return launch(KernelId::GemmBf16DecodeReduce, dim3((unsigned)ceil_div(total4, 256)), dim3(256),
+                  0, rargs);
   }
 
   const bool tile_ok = n % 256 == 0 && m % 256 == 0 && k % 64 == 0 && k > 0 && aligned16(a) &&

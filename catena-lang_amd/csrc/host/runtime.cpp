@@ -8,8 +8,9 @@
 // has no front end (out of scope) and instead binds source programs BY NAME
 // to native lowerings, checking the kinds of the declared type against the
 // lowering's signature.  The hot-path stdlib programs (nn.softmax,
-// math.exp-approx) and this build's new programs are built in; user
-// sources declare the rest (e.g. matmul-2x2-via-mem).
+// math.exp-approx, nn.rmsnorm, tensor.argmax-f32) and this build's new
+// programs are built in; user sources declare the rest (e.g.
+// matmul-2x2-via-mem).
 #include <cctype>
 #include <cstring>
 #include <memory>
@@ -81,6 +82,18 @@ void inv_attn(const catena_value_t* in, catena_value_t* out) {
   out[0] = mem_value(r);
 }
 
+void inv_rmsnorm(const catena_value_t* in, catena_value_t* out) {
+  catena_mem_t r;
+  program_nn_rmsnorm(in[0].as.mem, &r);
+  out[0] = mem_value(r);
+}
+void inv_argmax(const catena_value_t* in, catena_value_t* out) {
+  uint64_t r;
+  program_tensor_argmax_f32(in[0].as.mem, &r);
+  out[0].kind = kU64;
+  out[0].as.u64 = r;
+}
+
 const std::vector<Lowering>& lowerings() {
   static const std::vector<Lowering> t = {
       {"matmul-2x2-via-mem", false, {kMem, kMem, kU64, kU64, kU64, kU64, kU64, kU64}, {kMem},
@@ -89,6 +102,8 @@ const std::vector<Lowering>& lowerings() {
       {"matmul-left-identity-2x2-via-mem", false, {kMem, kU64, kU64}, {kMem}, inv_left_id},
       {"nn.softmax", true, {kMem}, {kMem}, inv_softmax},
       {"math.exp-approx", true, {kF32}, {kF32}, inv_exp},
+      {"nn.rmsnorm", true, {kMem}, {kMem}, inv_rmsnorm},
+      {"tensor.argmax-f32", true, {kMem}, {kU64}, inv_argmax},
       {"bf16.matmul.row-major.via-mem", true,
        {kMem, kMem, kU64, kU64, kU64, kU64, kU64, kU64}, {kMem}, inv_bf16_matmul},
       {"attn.decode.via-mem", true, {kMem, kMem, kMem, kMem, kU64, kU64, kU64, kU64, kF32}, {kMem},

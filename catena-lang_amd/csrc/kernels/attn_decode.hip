@@ -1,6 +1,6 @@
-// KV-cache decode attention (one query token per sequence), bf16 cache,
-// f32 softmax, f32 output, bitwise equal to the sequential composition of
-// the reference's own pieces:
+// KV-cache attention over a bf16 cache (decode: one query per sequence;
+// causal: its last Tq positions), f32 scores and softmax, bitwise equal to
+// the sequential composition of the reference's own pieces:
 //   s_t = (fold_{d asc} from +0 of q_d * k_{t,d}) * scale
 //         -- f32.matmul.cell-dot order, catena-lang/stdlib/matrix.hex:236-256
 //   m   = f32.max-env fold from -inf        (catena-lang/stdlib/sum.hex:73-84)
@@ -9,9 +9,12 @@
 //   o_d = fold_{t asc} from +0 of p_t * v_{t,d}
 // exp~ is math.exp-approx (catena-lang/stdlib/math.hex:148-199).
 //
-// One workgroup (4 waves) per (batch, head); layouts q[B][H][128],
+// One workgroup (4 waves) per (batch, query, head); layouts q[B][Tq][H][128],
 // k/v[B][H][L][128] (bf16, head-major, one 256-byte row per position),
-// lens[B] (positions used per sequence, clamped to L), o[B][H][128] f32.
+// lens[B] (positions in the cache per sequence, clamped to L),
+// o[B][Tq][H][128] (f32, or bf16 RNE).  The Tq queries of a sequence are
+// its last Tq positions (causal): query tq attends to the first
+// lens[b] - (Tq - 1 - tq) positions.  Tq = 1 is the decode step.
 //
 // K pass: each wave takes 64-row blocks (blocks w, w+4, ...).  A block is
 // moved in four 32-wide d segments: a coalesced 16-byte-per-lane global load
@@ -66,10 +69,11 @@ CATENA_DEV FirstMax wave_first_max(FirstMax a) {
 // K_NT: K-pass loads carry the non-temporal hint.  Each 128-byte line of K
 // is read as two 64-byte halves by consecutive steps, so the hint can cost a
 // second fetch of the line; both forms are kept and the host picks one.
-template <bool K_NT>
+template <bool K_NT, bool OUT_BF16>
 CATENA_DEV void attn_body(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                           const uint16_t* __restrict__ v, const uint32_t* __restrict__ lens,
-                          float* __restrict__ o, uint32_t H, uint32_t L, float scale) {
+                          void* __restrict__ o, uint32_t H, uint32_t L, uint32_t Tq,
+                          float scale) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   float* qf = reinterpret_cast<float*>(smem);                  // [128]
   unsigned char* stage = smem + D * 4;                         // [STAGE_BYTES]
@@ -80,14 +84,18 @@ CATENA_DEV void attn_body(const uint16_t* __restrict__ q, const uint16_t* __rest
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const uint64_t bh = blockIdx.x;
-  const uint32_t b = (uint32_t)(bh / H);
+  const uint64_t qi = blockIdx.x;  // (b * Tq + tq) * H + h
+  const uint32_t row = (uint32_t)(qi / H), h = (uint32_t)(qi % H);
+  const uint32_t b = row / Tq, tq = row % Tq;
+  const uint64_t bh = (uint64_t)b * H + h;
   uint32_t len = lens[b];
   if (len > L) len = L;
+  const uint32_t later = Tq - 1 - tq;  // queries after this one in the sequence
+  len = len > later ? len - later : 0;
 
   const uint16_t* kb = k + bh * (uint64_t)L * D;
   const uint16_t* vb = v + bh * (uint64_t)L * D;
-  if (tid < D) qf[tid] = bf16_to_f32(q[bh * D + tid]);
+  if (tid < D) qf[tid] = bf16_to_f32(q[qi * D + tid]);
   __syncthreads();
 
   // ---------------------------------------------------------------- K pass
@@ -290,7 +298,10 @@ CATENA_DEV void attn_body(const uint16_t* __restrict__ q, const uint16_t* __rest
       process(bt, va);
       if (bt + 1 < vnb) process(bt + 1, vbuf);
     }
-    o[bh * D + vcolbase + lane] = acc;
+    if (OUT_BF16)
+      static_cast<uint16_t*>(o)[qi * D + vcolbase + lane] = (uint16_t)f32_to_bf16_bits(acc);
+    else
+      static_cast<float*>(o)[qi * D + vcolbase + lane] = acc;
   }
 }
 
@@ -298,12 +309,29 @@ extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
 catena_attn_decode_bf16_d128(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                              const uint16_t* __restrict__ v, const uint32_t* __restrict__ lens,
                              float* __restrict__ o, uint32_t H, uint32_t L, float scale) {
-  attn_body<true>(q, k, v, lens, o, H, L, scale);
+  attn_body<true, false>(q, k, v, lens, o, H, L, 1u, scale);
 }
 
 extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void
 catena_attn_decode_bf16_d128_kc(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                 const uint16_t* __restrict__ v, const uint32_t* __restrict__ lens,
                                 float* __restrict__ o, uint32_t H, uint32_t L, float scale) {
-  attn_body<false>(q, k, v, lens, o, H, L, scale);
+  attn_body<false, false>(q, k, v, lens, o, H, L, 1u, scale);
+}
+
+// Tq causal queries per sequence (prefill and multi-token steps).
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void
+catena_attn_causal_bf16_d128_f32out(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                                    const uint16_t* __restrict__ v,
+                                    const uint32_t* __restrict__ lens, float* __restrict__ o,
+                                    uint32_t H, uint32_t L, uint32_t Tq, float scale) {
+  attn_body<false, false>(q, k, v, lens, o, H, L, Tq, scale);
+}
+
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void
+catena_attn_causal_bf16_d128_bf16out(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                                     const uint16_t* __restrict__ v,
+                                     const uint32_t* __restrict__ lens, uint16_t* __restrict__ o,
+                                     uint32_t H, uint32_t L, uint32_t Tq, float scale) {
+  attn_body<false, true>(q, k, v, lens, o, H, L, Tq, scale);
 }

@@ -92,6 +92,133 @@ CATENA_DEV float exp_approx(float x) {
   return is_negative ? reciprocal : base;
 }
 
+// math.sqrt (catena-lang/stdlib/math.hex:235-272): six Newton steps from
+// guess0 = (x < 1) ? 1 : x; non-positive inputs give +0.
+CATENA_DEV float sqrt_newton(float x) {
+  const float zero = (float)0u;
+  const float one = u32_as_f32(0x3F800000u);
+  const float half = u32_as_f32(0x3F000000u);
+  const bool lt_one = x < one;
+  float g = lt_one ? one : x;
+#pragma unroll
+  for (int it = 0; it < 6; ++it) {
+    const float ratio = x / g;
+    const float sum = g + ratio;
+    g = sum * half;
+  }
+  const bool is_nonpositive = x <= zero;
+  return is_nonpositive ? zero : g;
+}
+
+// nn.sigmoid / nn.silu (catena-lang/stdlib/nn.hex:1-21)
+CATENA_DEV float sigmoid_approx(float x) {
+  const float one = 1.0f;
+  const float neg_x = -x;
+  const float e = exp_approx(neg_x);
+  const float den = one + e;
+  return one / den;
+}
+CATENA_DEV float silu_approx(float x) {
+  const float gate = sigmoid_approx(x);
+  return x * gate;
+}
+
+// math.sin-approx / math.cos-approx (catena-lang/stdlib/math.hex:1-47)
+CATENA_DEV float sin_taylor(float x) {
+  const float x2 = x * x, x3 = x2 * x, x5 = x3 * x2, x7 = x5 * x2;
+  const float a = x3 / (float)6u, b = x5 / (float)120u, c = x7 / (float)5040u;
+  const float p1 = x - a;
+  const float p2 = p1 + b;
+  return p2 - c;
+}
+CATENA_DEV float cos_taylor(float x) {
+  const float x2 = x * x, x4 = x2 * x2, x6 = x4 * x2;
+  const float a = x2 / (float)2u, b = x4 / (float)24u, c = x6 / (float)720u;
+  const float p1 = (float)1u - a;
+  const float p2 = p1 + b;
+  return p2 - c;
+}
+// Cody-Waite quadrant evaluation of math.sin-approx-full-nonneg
+// (catena-lang/stdlib/math.hex:52-88); shift = 1 gives the cosine this
+// build defines (the quadrant advanced by one: cos x = sin(x + pi/2)).
+CATENA_DEV float quadrant_eval(float x, uint32_t shift) {
+  const float inv_pio2 = u32_as_f32(0x3F22F983u);
+  const float pio2_hi = u32_as_f32(0x3FC90FDAu);
+  const float pio2_lo = u32_as_f32(0x33A22168u);
+  const float scaled = x * inv_pio2;
+  const uint32_t n_u32 = round_to_u32(scaled);
+  const float n_f = (float)n_u32;
+  const float n_hi = n_f * pio2_hi;
+  const float n_lo = n_f * pio2_lo;
+  const float r1 = x - n_hi;
+  const float r = r1 - n_lo;
+  const float sin_r = sin_taylor(r);
+  const float cos_r = cos_taylor(r);
+  const float neg_sin = -sin_r, neg_cos = -cos_r;
+  const uint32_t quadrant = (n_u32 + shift) & 3u;
+  const float q23 = quadrant == 2u ? neg_sin : neg_cos;
+  const float q123 = quadrant == 1u ? cos_r : q23;
+  return quadrant == 0u ? sin_r : q123;
+}
+// math.sin-approx-full (catena-lang/stdlib/math.hex:90-103)
+CATENA_DEV float sin_full(float x) {
+  const bool is_negative = x < (float)0u;
+  const float magnitude = is_negative ? -x : x;
+  const float base = quadrant_eval(magnitude, 0u);
+  return is_negative ? -base : base;
+}
+CATENA_DEV float cos_full(float x) {
+  const bool is_negative = x < (float)0u;
+  const float magnitude = is_negative ? -x : x;
+  return quadrant_eval(magnitude, 1u);
+}
+
+// The sequential left fold ((0 + s[0]) + s[1]) + ... over n floats in LDS
+// (16-byte aligned), by one lane: the next 32 values are read before the
+// current 32 are added, so LDS latency stays off the dependency chain.
+CATENA_DEV float serial_sum_lds(const float* s, uint32_t n) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  float acc = __uint_as_float(0u);
+  const uint32_t n4 = n / 4;
+  const f4* s4 = reinterpret_cast<const f4*>(s);
+  uint32_t i = 0;
+  if (n4 >= 8) {
+    f4 cur[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) cur[u] = s4[u];
+    for (i = 8; i + 8 <= n4; i += 8) {
+      f4 nxt[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) nxt[u] = s4[i + u];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        acc = acc + cur[u][0];
+        acc = acc + cur[u][1];
+        acc = acc + cur[u][2];
+        acc = acc + cur[u][3];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      acc = acc + cur[u][0];
+      acc = acc + cur[u][1];
+      acc = acc + cur[u][2];
+      acc = acc + cur[u][3];
+    }
+  }
+  for (; i < n4; ++i) {
+    const f4 e = s4[i];
+    acc = acc + e[0];
+    acc = acc + e[1];
+    acc = acc + e[2];
+    acc = acc + e[3];
+  }
+  for (uint32_t t = n4 * 4; t < n; ++t) acc = acc + s[t];
+  return acc;
+}
+
 // Exact parallel form of the f32.max-env fold (catena-lang/stdlib/
 // sum.hex:73-84: acc = (acc >= x) ? acc : x from acc = -inf, ascending).
 // Without NaNs the fold returns the FIRST element that compares equal to the

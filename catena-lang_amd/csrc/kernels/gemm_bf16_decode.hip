@@ -10,9 +10,9 @@
 //   * a wave owns 128 consecutive columns and a contiguous chunk of KW k;
 //   * a workgroup holds 4 waves on 4 consecutive k chunks and adds their
 //     partials in ascending chunk order through LDS;
-//   * grid.y = number of such k groups (S).  S == 1 writes bf16 directly;
-//     otherwise each workgroup writes an f32 partial P[s][m][n] and
-//     catena_gemm_bf16_decode_reduce adds them in ascending s.
+//   * grid.y = number of such k groups (S).  S == 1 writes Y (bf16 or f32)
+//     directly; otherwise each workgroup writes an f32 partial P[s][m][n]
+//     and catena_gemm_bf16_decode_reduce adds them in ascending s.
 // No atomics; the addition order depends only on the shape, so results are
 // bitwise identical run to run.
 //
@@ -58,8 +58,8 @@ CATENA_DEV void load_w(const uint16_t* __restrict__ W, uint64_t K, uint64_t N, u
 
 // grid = (ceil(N/128), S), block = 256.  KW = k per wave (multiple of 32).
 extern "C" __global__ __launch_bounds__(256) void catena_gemm_bf16_decode(
-    const uint16_t* __restrict__ X, const uint16_t* __restrict__ W, uint16_t* __restrict__ Y,
-    float* __restrict__ P, uint32_t M, uint64_t N, uint64_t K, uint32_t KW) {
+    const uint16_t* __restrict__ X, const uint16_t* __restrict__ W, void* __restrict__ Y,
+    float* __restrict__ P, uint32_t M, uint64_t N, uint64_t K, uint32_t KW, uint32_t out_f32) {
   __shared__ f32x4_t red[3][8][64];  // partials of waves 1..3
 
   const int tid = threadIdx.x;
@@ -120,21 +120,25 @@ extern "C" __global__ __launch_bounds__(256) void catena_gemm_bf16_decode(
   for (int q = 0; q < 4; ++q) {
     const uint32_t row = 4 * g + q;
     if (row >= M) continue;
-    if (gridDim.y == 1) {
+    if (gridDim.y == 1 && !out_f32) {
       u32x4_t packed = u32x4_t{pack_bf16x2(acc[0][q], acc[1][q]), pack_bf16x2(acc[2][q], acc[3][q]),
                                pack_bf16x2(acc[4][q], acc[5][q]), pack_bf16x2(acc[6][q], acc[7][q])};
-      *reinterpret_cast<u32x4_t*>(Y + (uint64_t)row * N + col) = packed;
+      *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(Y) + (uint64_t)row * N + col) = packed;
     } else {
-      float* dst = P + ((uint64_t)blockIdx.y * M + row) * N + col;
+      // S == 1 with f32 output writes Y itself; otherwise partial s of P
+      float* dst = gridDim.y == 1 ? static_cast<float*>(Y) + (uint64_t)row * N + col
+                                  : P + ((uint64_t)blockIdx.y * M + row) * N + col;
       *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{acc[0][q], acc[1][q], acc[2][q], acc[3][q]};
       *reinterpret_cast<f32x4_t*>(dst + 4) = f32x4_t{acc[4][q], acc[5][q], acc[6][q], acc[7][q]};
     }
   }
 }
 
-// Y[m][n] = bf16( P[0][m][n] + P[1][m][n] + ... + P[S-1][m][n] ), ascending s.
+// Y[m][n] = P[0][m][n] + P[1][m][n] + ... + P[S-1][m][n], ascending s, then
+// bf16 (RNE) unless out_f32.
 extern "C" __global__ __launch_bounds__(256) void catena_gemm_bf16_decode_reduce(
-    const float* __restrict__ P, uint16_t* __restrict__ Y, uint32_t M, uint64_t N, uint32_t S) {
+    const float* __restrict__ P, void* __restrict__ Y, uint32_t M, uint64_t N, uint32_t S,
+    uint32_t out_f32) {
   const uint64_t idx = (uint64_t)blockIdx.x * 256 + threadIdx.x;  // over M*N/4
   const uint64_t total = (uint64_t)M * N / 4;
   if (idx >= total) return;
@@ -144,6 +148,10 @@ extern "C" __global__ __launch_bounds__(256) void catena_gemm_bf16_decode_reduce
     f32x4_t v = p4[(uint64_t)s * total + idx];
 #pragma unroll
     for (int q = 0; q < 4; ++q) acc[q] = acc[q] + v[q];
+  }
+  if (out_f32) {
+    reinterpret_cast<f32x4_t*>(Y)[idx] = acc;
+    return;
   }
   uint2 out;
   out.x = pack_bf16x2(acc[0], acc[1]);

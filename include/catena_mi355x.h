@@ -105,7 +105,7 @@ int catena_mi355x_gemm_f32_exact(const float *a, const float *b, float *c, uint6
  * accumulation on MFMA in a fixed order, output bf16 (RNE) or f32 when
  * out_f32 != 0.  Same contraction as above, extended to bf16 (no reference
  * counterpart: catena has no bf16, catena-lang/src/codegen/lower_types.rs:13-22).
- * n <= 16 (decode shape) uses the weight-streaming kernel. */
+ * n <= 16 (decode shape) uses the weight-streaming kernel (both outputs). */
 int catena_mi355x_gemm_bf16(const uint16_t *a, const uint16_t *b, void *c, uint64_t n,
                             uint64_t m, uint64_t k, int out_f32);
 
@@ -134,6 +134,66 @@ int catena_mi355x_fill_uniform_f32(float *out, uint64_t n, uint64_t seed, uint64
 /* Device-to-device copy kernel (16-byte aligned pointers, n % 16 == 0); also
  * the known-size reference for calibrating HBM traffic counters. */
 int catena_mi355x_copy_bytes(void *dst, const void *src, uint64_t n);
+
+/* -- decoder-block pieces (the callers on either side of the two hot ops) -- */
+
+/* Causal KV-cache attention for Tq queries per sequence (prefill, or
+ * several tokens per step): q[B][Tq][H][D], k/v[B][H][L][D] bf16,
+ * lens[B] (device u32: positions in the cache after the append, <= L),
+ * o[B][Tq][H][D] f32 (out_f32 != 0) or bf16 RNE.  Query tq of sequence b
+ * attends to the first lens[b] - (Tq - 1 - tq) positions, each exactly as
+ * catena_mi355x_attn_decode_bf16 (Tq = 1 is that call).  No reference
+ * counterpart.  head_dim must be 128. */
+int catena_mi355x_attn_causal_bf16(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                                   const uint32_t *lens, void *o, uint32_t batch, uint32_t tq,
+                                   uint32_t heads, uint32_t max_len, uint32_t head_dim,
+                                   float scale, int out_f32);
+
+/* nn.rmsnorm over `rows` contiguous vectors of length n
+ * (catena-lang/stdlib/nn.hex:154-182 with math.sqrt,
+ * catena-lang/stdlib/math.hex:235-272): bitwise the reference's fold order.
+ * n % 4 == 0; y may not alias x. */
+int catena_mi355x_rmsnorm_f32(const float *x, float *y, uint64_t rows, uint64_t n);
+
+/* Residual add in front of nn.rmsnorm, bf16 output: for output row i with
+ * src = row_index ? row_index[i] : i, h = x[src] + resid[src] (h = x[src]
+ * when resid is NULL), written to h_out[i] when h_out is not NULL; then
+ * y[i] = bf16(nn.rmsnorm(h)).  No reference counterpart (the decoder's fused
+ * form of f32.add and nn.rmsnorm).  n % 4 == 0. */
+int catena_mi355x_residual_rmsnorm_bf16(const float *x, const float *resid,
+                                        const uint32_t *row_index, float *h_out, uint16_t *y,
+                                        uint64_t rows, uint64_t n);
+
+/* Token embedding: x[r][:] = widen(table[tokens[r]][:]) for r < rows;
+ * table[vocab][d] bf16, x f32; a token >= vocab gives a row of NaN.
+ * d % 8 == 0.  No reference counterpart. */
+int catena_mi355x_embed_bf16(const uint32_t *tokens, const uint16_t *table, float *x,
+                             uint64_t rows, uint32_t vocab, uint32_t d);
+
+/* RoPE inverse frequencies on the host: out[i] = (float)(1 / base^(2i/d))
+ * in double precision, i < head_dim / 2.  No reference counterpart. */
+int catena_mi355x_rope_inv_freq(float *out_host, uint32_t head_dim, double base);
+
+/* RoPE + KV-cache append on a fused projection qkv[B*Tq][3*H*D] f32
+ * (columns: q heads | k heads | v heads; row b*Tq + tq at position
+ * lens[b] - Tq + tq).  Pairs (i, i + D/2) rotate by theta = pos *
+ * inv_freq[i] with sin = math.sin-approx-full
+ * (catena-lang/stdlib/math.hex:52-103) and cos the same reduction with the
+ * quadrant advanced by one.  Writes q[B*Tq][H*D] bf16 and the bf16 rotated
+ * k and v rows into k_cache/v_cache[B][H][L][D].  No reference counterpart. */
+int catena_mi355x_rope_qkv_bf16(const float *qkv, const float *inv_freq, const uint32_t *lens,
+                                uint16_t *q, uint16_t *k_cache, uint16_t *v_cache,
+                                uint32_t batch, uint32_t tq, uint32_t heads, uint32_t head_dim,
+                                uint32_t max_len);
+
+/* SwiGLU gate: gu[rows][2F] f32 (gate | up) -> out[rows][F] =
+ * bf16(nn.silu(gate) * up) (catena-lang/stdlib/nn.hex:1-21).  F % 4 == 0. */
+int catena_mi355x_silu_mul_bf16(const float *gu, uint16_t *out, uint64_t rows, uint32_t ffn);
+
+/* tensor.argmax-f32 per row (catena-lang/stdlib/tensor.hex:204-227):
+ * idx[r] = first index of the maximum with the reference's NaN behaviour;
+ * n = 0 gives 0xFFFFFFFF (the reference asserts n != 0). */
+int catena_mi355x_argmax_f32(const float *x, uint32_t *idx, uint64_t rows, uint64_t n);
 
 /* ------------------------------------------------------------------ */
 /* program ABI (generated-module symbols; synchronous; fail-stop)        */
@@ -166,6 +226,83 @@ void program_attn_decode_via_mem(catena_mem_t q, catena_mem_t k, catena_mem_t v,
                                  catena_mem_t lens, uint64_t batch, uint64_t heads,
                                  uint64_t max_len, uint64_t head_dim, float scale,
                                  catena_mem_t *out);
+
+/* catena-lang/stdlib/nn.hex:154-182 "nn.rmsnorm": (mem) -> (mem). */
+void program_nn_rmsnorm(catena_mem_t x, catena_mem_t *out);
+/* catena-lang/stdlib/tensor.hex:204-227 "tensor.argmax-f32": (mem) -> (u64);
+ * traps on an empty input like the reference's u64.assert-nz. */
+void program_tensor_argmax_f32(catena_mem_t x, uint64_t *out);
+
+/* ------------------------------------------------------------------ */
+/* decoder (Llama-style blocks composed from the ops above)              */
+
+/* No reference counterpart: the model the two hot contractions serve.
+ * Per layer, rows r of the residual stream x (f32):
+ *   xn  = bf16(rmsnorm(x));  qkv = xn * W_qkv (f32);  RoPE + cache append;
+ *   o   = bf16(attention);   h = x + o * W_o;  hn = bf16(rmsnorm(h));
+ *   gu  = hn * W_gu (f32);   a = bf16(silu(gate) * up);  x' = h + a * W_down.
+ * Then bf16(rmsnorm(x)) of each sequence's last row times W_lm gives f32
+ * logits and greedy argmax the next token.  Weights bf16, row-major NN:
+ * W_qkv[d][3d], W_o[d][d], W_gu[d][2F], W_down[F][d], W_lm[d][vocab];
+ * embedding[vocab][d]. */
+typedef struct catena_decoder catena_decoder_t;
+typedef struct catena_decoder_config {
+  uint32_t d_model;  /* = n_heads * head_dim */
+  uint32_t n_heads;
+  uint32_t head_dim; /* 128 */
+  uint32_t ffn_dim;  /* SwiGLU width F */
+  uint32_t n_layers;
+  uint32_t vocab;
+  uint32_t max_batch;
+  uint32_t max_len; /* cache positions per sequence */
+  float rope_base;
+} catena_decoder_config_t;
+
+typedef enum catena_decoder_tensor {
+  CATENA_DEC_EMBED = 0, /* [vocab][d] bf16 */
+  CATENA_DEC_W_QKV,     /* per layer [d][3d] bf16 */
+  CATENA_DEC_W_O,       /* per layer [d][d] bf16 */
+  CATENA_DEC_W_GU,      /* per layer [d][2F] bf16 */
+  CATENA_DEC_W_DOWN,    /* per layer [F][d] bf16 */
+  CATENA_DEC_W_LM,      /* [d][vocab] bf16 */
+  CATENA_DEC_K_CACHE,   /* per layer [max_batch][H][max_len][D] bf16 */
+  CATENA_DEC_V_CACHE,   /* per layer, same */
+  CATENA_DEC_INV_FREQ,  /* [D/2] f32 */
+  /* activations of the last forward call (rows = batch * tokens per
+   * sequence; the last layer's values when n_layers > 1) */
+  CATENA_DEC_X,         /* [rows][d] f32: residual stream into the last layer */
+  CATENA_DEC_XN,        /* [rows][d] bf16 */
+  CATENA_DEC_QKV,       /* [rows][3d] f32 */
+  CATENA_DEC_Q,         /* [rows][d] bf16 (rotated) */
+  CATENA_DEC_ATTN,      /* [rows][d] bf16 */
+  CATENA_DEC_ATTN_PROJ, /* [rows][d] f32 */
+  CATENA_DEC_H,         /* [rows][d] f32 */
+  CATENA_DEC_HN,        /* [rows][d] bf16 */
+  CATENA_DEC_GU,        /* [rows][2F] f32 */
+  CATENA_DEC_ACT,       /* [rows][F] bf16 */
+  CATENA_DEC_FFN_OUT,   /* [rows][d] f32 */
+  CATENA_DEC_FINAL_H,   /* [batch][d] f32: residual stream at the last rows */
+  CATENA_DEC_FINAL_XN,  /* [batch][d] bf16 */
+  CATENA_DEC_LOGITS,    /* [batch][vocab] f32 */
+  CATENA_DEC_LENS,      /* [batch] u32: cache positions per sequence */
+  CATENA_DEC_TENSOR_COUNT
+} catena_decoder_tensor_t;
+
+int catena_mi355x_decoder_create(const catena_decoder_config_t *cfg, catena_decoder_t **out);
+void catena_mi355x_decoder_destroy(catena_decoder_t *dec);
+/* Device memory owned by the decoder (weights can be written through it). */
+int catena_mi355x_decoder_tensor(catena_decoder_t *dec, uint32_t which, uint32_t layer,
+                                 catena_mem_t *out);
+/* Every weight ~ N(0, std) in bf16 from the seeded counter generator. */
+int catena_mi355x_decoder_init_weights(catena_decoder_t *dec, uint64_t seed, float std);
+/* Prefill `tokens` (device u32 [batch][t]) into an empty cache, then write
+ * each sequence's greedy next token to next (device u32 [batch]). */
+int catena_mi355x_decoder_prefill(catena_decoder_t *dec, const uint32_t *tokens,
+                                  uint32_t batch, uint32_t t, uint32_t *next);
+/* `steps` greedy decode steps after a prefill: step s appends tokens
+ * out[s-1] (out[-1] = the prefill's next) and writes out[s][batch].  out is
+ * device u32 [steps][batch].  Fails when the cache would overflow. */
+int catena_mi355x_decoder_generate(catena_decoder_t *dec, uint32_t steps, uint32_t *out);
 
 /* ------------------------------------------------------------------ */
 /* runtime mirror                                                         */

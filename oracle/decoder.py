@@ -1,0 +1,140 @@
+"""CPU oracle of the decoder built on the library's kernels (composition of
+the restated stdlib pieces in catena_oracle.c / catena_oracle_block.c).
+
+TEST INFRASTRUCTURE ONLY (imported by tests/, smoke() and bench.py's
+cpu_baseline leg).  Each stage takes numpy arrays (bf16 as uint16 bits) and
+returns what the corresponding GPU stage must produce: bitwise for the
+elementwise / fold stages, and the sequential-order reference value for the
+GEMMs (whose GPU order is MFMA's, checked under a bound).
+
+Stage definitions (one IEEE op per node, operands in this order):
+  residual_rmsnorm_bf16: h = x + r;  y = bf16(nn.rmsnorm(h))
+                         (catena-lang/stdlib/nn.hex:154-182)
+  rope_qkv:              pairs (i, i + D/2) of each q / k head rotate by
+                         theta = f32(pos) * inv_freq[i]:
+                         y1 = x1*c - x2*s, y2 = x2*c + x1*s with
+                         s = math.sin-approx-full(theta)
+                         (catena-lang/stdlib/math.hex:52-103) and c the same
+                         reduction with the quadrant advanced by one
+  attn_causal:           query tq of sequence b = decode attention over the
+                         first lens[b] - (Tq - 1 - tq) cache rows
+  silu_mul_bf16:         bf16(nn.silu(g) * u)   (catena-lang/stdlib/nn.hex:1-21)
+  argmax:                tensor.argmax-f32 (catena-lang/stdlib/tensor.hex:204-227)
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import (argmax_f32, attn_decode, bf16_bits_to_f32, f32_to_bf16_bits_np, lib,
+               matmul_bf16, rmsnorm_f32, rope_f32)
+
+
+def residual_rmsnorm_bf16(x, r=None):
+    """-> (h f32, y bf16 bits) per row."""
+    x = np.asarray(x, np.float32)
+    h = x if r is None else (x + np.asarray(r, np.float32)).astype(np.float32)
+    return h, f32_to_bf16_bits_np(rmsnorm_f32(h))
+
+
+def silu_mul_bf16(gu, ffn: int):
+    gu = np.ascontiguousarray(gu, np.float32)
+    g, u = gu[:, :ffn], gu[:, ffn:]
+    f = lib().or_silu
+    s = np.array([f(float(v)) for v in g.ravel()], np.float32).reshape(g.shape)
+    return f32_to_bf16_bits_np((s * u).astype(np.float32))
+
+
+def rope_qkv(qkv, inv_freq, lens, batch: int, tq: int, heads: int, head_dim: int):
+    """-> (q bf16 [R][H*D], k bf16 [R][H][D], v bf16 [R][H][D], pos [R])."""
+    qkv = np.ascontiguousarray(qkv, np.float32)
+    R = batch * tq
+    HD = heads * head_dim
+    q = np.empty((R, HD), np.uint16)
+    k = np.empty((R, heads, head_dim), np.uint16)
+    v = np.empty((R, heads, head_dim), np.uint16)
+    pos = np.empty(R, np.int64)
+    for r in range(R):
+        b, t = divmod(r, tq)
+        p = int(lens[b]) - tq + t
+        pos[r] = p
+        for h in range(heads):
+            qs = qkv[r, h * head_dim:(h + 1) * head_dim]
+            ks = qkv[r, HD + h * head_dim:HD + (h + 1) * head_dim]
+            q[r, h * head_dim:(h + 1) * head_dim] = f32_to_bf16_bits_np(rope_f32(qs, max(p, 0), inv_freq))
+            k[r, h] = f32_to_bf16_bits_np(rope_f32(ks, max(p, 0), inv_freq))
+            v[r, h] = f32_to_bf16_bits_np(qkv[r, 2 * HD + h * head_dim:2 * HD + (h + 1) * head_dim])
+    return q, k, v, pos
+
+
+def attn_causal(q, kc, vc, lens, batch: int, tq: int, heads: int, head_dim: int, scale: float):
+    """q bf16 [B*Tq][H*D], caches [B][H][L][D] -> o f32 [B*Tq][H*D]."""
+    q = np.asarray(q, np.uint16).reshape(batch, tq, heads, head_dim)
+    lens = np.asarray(lens, np.int64)
+    o = np.empty((batch, tq, heads, head_dim), np.float32)
+    for t in range(tq):
+        ln = np.maximum(lens - (tq - 1 - t), 0).astype(np.uint32)
+        o[:, t] = attn_decode(np.ascontiguousarray(q[:, t]), kc, vc, ln, scale)
+    return o.reshape(batch * tq, heads * head_dim)
+
+
+def gemm(a16, b16):
+    """Sequential-order bf16 GEMM: (f32, bf16 bits)."""
+    return matmul_bf16(a16, b16)
+
+
+class DecoderOracle:
+    """Whole-model sequential forward (all GEMMs in the reference's k order).
+    Weights are host arrays of bf16 bits laid out as the library's
+    (w_qkv [L][d][3d], w_o [L][d][d], w_gu [L][d][2F], w_down [L][F][d],
+    embed [V][d], w_lm [d][V])."""
+
+    def __init__(self, weights: dict, n_heads: int, head_dim: int, ffn: int, max_len: int,
+                 rope_base: float = 10000.0):
+        self.w = weights
+        self.H, self.D, self.F, self.L = n_heads, head_dim, ffn, max_len
+        self.d = n_heads * head_dim
+        self.layers = len(weights["w_qkv"])
+        from . import rope_inv_freq
+        self.inv = rope_inv_freq(head_dim, rope_base)
+        self.scale = float(np.float32(1.0 / np.sqrt(head_dim)))
+        self.kc = None
+        self.vc = None
+        self.len = 0
+
+    def _forward(self, tokens, batch: int, tq: int):
+        H, D, d, F = self.H, self.D, self.d, self.F
+        lens = np.full(batch, self.len + tq, np.int64)
+        x = bf16_bits_to_f32(self.w["embed"][np.asarray(tokens, np.int64).ravel()])
+        h = ffn_out = None
+        for l in range(self.layers):
+            if l == 0:
+                _, xn = residual_rmsnorm_bf16(x)
+            else:
+                x, xn = residual_rmsnorm_bf16(h, ffn_out)
+            qkv, _ = gemm(xn, self.w["w_qkv"][l])
+            q, k, v, pos = rope_qkv(qkv, self.inv, lens, batch, tq, H, D)
+            for r in range(batch * tq):
+                b = r // tq
+                self.kc[l][b, :, pos[r]] = k[r]
+                self.vc[l][b, :, pos[r]] = v[r]
+            o = attn_causal(q, self.kc[l], self.vc[l], lens, batch, tq, H, D, self.scale)
+            ap, _ = gemm(f32_to_bf16_bits_np(o), self.w["w_o"][l])
+            h, hn = residual_rmsnorm_bf16(x, ap)
+            gu, _ = gemm(hn, self.w["w_gu"][l])
+            act = silu_mul_bf16(gu, F)
+            ffn_out, _ = gemm(act, self.w["w_down"][l])
+        last = np.arange(batch) * tq + (tq - 1)
+        _, fxn = residual_rmsnorm_bf16(h[last], ffn_out[last])
+        logits, _ = gemm(fxn, self.w["w_lm"])
+        nxt = np.array([argmax_f32(logits[b]) for b in range(batch)], np.uint32)
+        self.len += tq
+        return logits, nxt
+
+    def prefill(self, tokens, batch: int, t: int):
+        self.kc = [np.zeros((batch, self.H, self.L, self.D), np.uint16) for _ in range(self.layers)]
+        self.vc = [np.zeros((batch, self.H, self.L, self.D), np.uint16) for _ in range(self.layers)]
+        self.len = 0
+        return self._forward(tokens, batch, t)
+
+    def step(self, tokens, batch: int):
+        return self._forward(tokens, batch, 1)

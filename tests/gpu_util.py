@@ -44,3 +44,16 @@ def hash_bits(arr: np.ndarray) -> int:
 
 def as_f32(bits16: np.ndarray) -> np.ndarray:
     return oracle.bf16_bits_to_f32(bits16)
+
+
+def gemm_within_bound(a16: np.ndarray, b16: np.ndarray, got32: np.ndarray) -> float:
+    """Assert the MFMA-order f32 GEMM bound |C - AB| <= 8 (K/32 + 1) u sum|A||B|
+    (A, B bf16 bits, C exact in float64); returns the worst ratio to the bound."""
+    af = as_f32(a16).astype(np.float64)
+    bf = as_f32(b16).astype(np.float64)
+    k = a16.shape[1]
+    bound = 8 * (k / 32 + 1) * U * (np.abs(af) @ np.abs(bf))
+    err = np.abs(got32.astype(np.float64) - af @ bf)
+    ratio = float((err / np.maximum(bound, 1e-300)).max())
+    assert np.all(err <= bound), ratio
+    return ratio

@@ -132,9 +132,13 @@ def test_decode_kernel_full_compare(mrows, n, k):
     say(f"bf16 decode gemm M={mrows} N={n} K={k}")
     a, b, a16, b16 = _inputs(mrows, n, k, seed=300 + mrows + n + k, wscale=0.02)
     c16 = ca.Buffer(mrows * n * 2)
+    c32 = ca.Buffer(mrows * n * 4)
     ca.gemm_bf16(a, b, c16, mrows, n, k)
+    ca.gemm_bf16(a, b, c32, mrows, n, k, out_f32=True)
     g16 = c16.read(np.uint16, (mrows, n))
-    _check(a16, b16, None, g16)
+    g32 = c32.read(np.float32, (mrows, n))
+    assert np.array_equal(g16, oracle.f32_to_bf16_bits_np(g32))
+    _check(a16, b16, g32, g16)
     h = hash_bits(g16)
     for _ in range(3):
         ca.gemm_bf16(a, b, c16, mrows, n, k)

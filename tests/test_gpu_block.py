@@ -1,0 +1,267 @@
+"""GPU parity of the decoder-block pieces: bitwise against the oracle.
+
+Each kernel reproduces its stdlib op's node order (nn.rmsnorm's serial
+square-sum fold and six-step Newton sqrt, nn.silu, math.sin-approx-full,
+tensor.argmax-f32's NaN and tie behaviour), so outputs must match bit for
+bit, including specials (zeros, NaN, inf, ties of +0/-0).  The causal
+attention's queries must each equal the decode attention over their prefix.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import catena_amd as ca
+import oracle
+from oracle import decoder as od
+from gpu_util import dev_normal_bf16, say
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _init():
+    say("init device 0")
+    ca.init(0)
+
+
+def _bitwise(got, want):
+    got = np.asarray(got)
+    want = np.asarray(want)
+    assert got.shape == want.shape
+    if got.dtype == np.float32:
+        gn, wn = np.isnan(got), np.isnan(want)
+        assert np.array_equal(gn, wn)
+        got, want = got[~gn].view(np.uint32), want[~wn].view(np.uint32)
+    assert np.array_equal(got, want), int(np.sum(got != want))
+
+
+def _rows(rows, n, seed, scale=1.0):
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal((rows, n)) * scale).astype(np.float32)
+
+
+@pytest.mark.parametrize("rows,n", [(1, 6), (3, 2048), (2, 4097), (5, 5632), (1, 1), (4, 12)])
+def test_rmsnorm_f32(rows, n):
+    say(f"rmsnorm rows={rows} n={n}")
+    x = _rows(rows, n, rows * 31 + n, scale=3.0)
+    if n == 6:
+        x[0] = [1.0, 2.0, 4.0, -1.0, -9.0, 13.29]  # catena-lang/tests/runtime.rs:1011-1044
+    xb, yb = ca.Buffer.from_array(x), ca.Buffer(x.nbytes)
+    ca.rmsnorm_f32(xb, yb, rows, n)
+    _bitwise(yb.read(np.float32, (rows, n)), oracle.rmsnorm_f32(x))
+
+
+def test_rmsnorm_specials():
+    n = 64
+    x = _rows(6, n, 5)
+    x[0] = 0.0                      # sum 0: rms = sqrt(eps)
+    x[1, 3] = np.nan                # NaN propagates through the fold
+    x[2, 7] = np.inf
+    x[3] = 3e19                     # squares overflow to inf
+    x[4] = 1e-30                    # squares underflow (subnormal/zero)
+    x[5, ::2] = -0.0
+    xb, yb = ca.Buffer.from_array(x), ca.Buffer(x.nbytes)
+    say("rmsnorm specials")
+    ca.rmsnorm_f32(xb, yb, 6, n)
+    _bitwise(yb.read(np.float32, (6, n)), oracle.rmsnorm_f32(x))
+
+
+@pytest.mark.parametrize("use_resid,use_index,n", [(True, False, 2048), (False, False, 256),
+                                                   (True, True, 2048), (True, True, 10)])
+def test_residual_rmsnorm_bf16(use_resid, use_index, n):
+    rows_in = 9
+    x = _rows(rows_in, n, n + 1)
+    r = _rows(rows_in, n, n + 2, scale=0.5)
+    idx = np.array([8, 0, 3], np.uint32) if use_index else None
+    rows_out = 3 if use_index else rows_in
+    xb, rb = ca.Buffer.from_array(x), ca.Buffer.from_array(r)
+    ib = ca.Buffer.from_array(idx) if use_index else None
+    hb, yb = ca.Buffer(rows_out * n * 4), ca.Buffer(rows_out * n * 2)
+    say(f"residual rmsnorm resid={use_resid} index={use_index} n={n}")
+    ca.residual_rmsnorm_bf16(xb, rb if use_resid else None, ib, hb, yb, rows_out, n)
+    src = idx.astype(np.int64) if use_index else np.arange(rows_in)
+    h, y = od.residual_rmsnorm_bf16(x[src], r[src] if use_resid else None)
+    _bitwise(hb.read(np.float32, (rows_out, n)), h)
+    _bitwise(yb.read(np.uint16, (rows_out, n)), y)
+
+
+def test_embed():
+    V, d = 40, 256
+    table = dev_normal_bf16(V * d, 7, 0)
+    tok = np.array([0, 39, 5, 5, 40, 1000000], np.uint32)  # last two out of range
+    tb = ca.Buffer.from_array(tok)
+    x = ca.Buffer(tok.size * d * 4)
+    say("embed")
+    ca.embed_bf16(tb, table, x, tok.size, V, d)
+    got = x.read(np.float32, (tok.size, d))
+    t = table.read(np.uint16, (V, d))
+    _bitwise(got[:4], oracle.bf16_bits_to_f32(t[tok[:4].astype(np.int64)]))
+    assert np.all(np.isnan(got[4:]))
+
+
+def test_rope_inv_freq_matches_oracle():
+    for D, base in [(128, 10000.0), (64, 500000.0)]:
+        assert np.array_equal(ca.rope_inv_freq(D, base).view(np.uint32),
+                              oracle.rope_inv_freq(D, base).view(np.uint32))
+
+
+@pytest.mark.parametrize("B,Tq,H,L,lens", [(2, 3, 2, 8, [5, 3]), (3, 1, 4, 640, [640, 1, 77]),
+                                           (2, 16, 3, 600, [600, 16])])
+def test_rope_qkv_store(B, Tq, H, L, lens):
+    D = 128
+    R = B * Tq
+    rng = np.random.default_rng(B * 100 + Tq)
+    qkv = (rng.standard_normal((R, 3 * H * D)) * 2).astype(np.float32)
+    inv = ca.rope_inv_freq(D, 10000.0)
+    kc = ca.Buffer(B * H * L * D * 2)
+    vc = ca.Buffer(B * H * L * D * 2)
+    sentinel = np.full(B * H * L * D, 0xABCD, np.uint16)
+    kc.write(sentinel)
+    vc.write(sentinel)
+    qb = ca.Buffer(R * H * D * 2)
+    say(f"rope qkv B={B} Tq={Tq} H={H} L={L} lens={lens}")
+    ca.rope_qkv_bf16(ca.Buffer.from_array(qkv), ca.Buffer.from_array(inv),
+                     ca.Buffer.from_array(np.array(lens, np.uint32)), qb, kc, vc, B, Tq, H, D, L)
+    q, k, v, pos = od.rope_qkv(qkv, inv, lens, B, Tq, H, D)
+    _bitwise(qb.read(np.uint16, (R, H * D)), q)
+    kg = kc.read(np.uint16, (B, H, L, D))
+    vg = vc.read(np.uint16, (B, H, L, D))
+    written = np.zeros((B, L), bool)
+    for r in range(R):
+        b = r // Tq
+        _bitwise(kg[b, :, pos[r]], k[r])
+        _bitwise(vg[b, :, pos[r]], v[r])
+        written[b, pos[r]] = True
+    untouched = ~written
+    assert np.all(kg.transpose(0, 2, 1, 3)[untouched] == 0xABCD)
+    assert np.all(vg.transpose(0, 2, 1, 3)[untouched] == 0xABCD)
+
+
+def test_rope_large_positions_against_libm():
+    """Rotation at position 4095 stays within 2e-4 (plus bf16 rounding) of the
+    libm value, so both the range reduction and the quadrant map hold."""
+    D, H, B, L = 128, 1, 1, 4096
+    lens = [4096]
+    qkv = np.random.default_rng(3).standard_normal((1, 3 * D)).astype(np.float32)
+    inv = ca.rope_inv_freq(D, 10000.0)
+    qb = ca.Buffer(D * 2)
+    kc, vc = ca.Buffer(B * H * L * D * 2), ca.Buffer(B * H * L * D * 2)
+    say("rope at position 4095")
+    ca.rope_qkv_bf16(ca.Buffer.from_array(qkv), ca.Buffer.from_array(inv),
+                     ca.Buffer.from_array(np.array(lens, np.uint32)), qb, kc, vc, 1, 1, H, D, L)
+    q = oracle.bf16_bits_to_f32(qb.read(np.uint16)).astype(np.float64)
+    th = 4095.0 * inv.astype(np.float64)
+    x1, x2 = qkv[0, :64].astype(np.float64), qkv[0, 64:128].astype(np.float64)
+    want = np.concatenate([x1 * np.cos(th) - x2 * np.sin(th), x2 * np.cos(th) + x1 * np.sin(th)])
+    assert np.abs(q - want).max() < 2e-4 + 2 ** -7 * np.abs(want).max()
+
+
+@pytest.mark.parametrize("rows,F", [(3, 1024), (8, 5632), (1, 4)])
+def test_silu_mul(rows, F):
+    rng = np.random.default_rng(F)
+    gu = (rng.standard_normal((rows, 2 * F)) * 4).astype(np.float32)
+    gu[0, :4] = [0.0, -0.0, 100.0, -100.0]
+    out = ca.Buffer(rows * F * 2)
+    say(f"silu_mul rows={rows} F={F}")
+    ca.silu_mul_bf16(ca.Buffer.from_array(gu), out, rows, F)
+    _bitwise(out.read(np.uint16, (rows, F)), od.silu_mul_bf16(gu, F))
+
+
+def _argmax_rows(rows):
+    n = max(len(r) for r in rows)
+    assert all(len(r) == n for r in rows)
+    x = np.array(rows, np.float32)
+    idx = ca.Buffer(len(rows) * 4)
+    ca.argmax_f32(ca.Buffer.from_array(x), idx, len(rows), n)
+    return idx.read(np.uint32)
+
+
+def test_argmax_special_rows():
+    nan, inf = np.nan, np.inf
+    rows = [
+        [1.0, 3.0, 3.0, 2.0, 0.0],
+        [nan, 1.0, 5.0, 5.0, 2.0],
+        [1.0, 9.0, nan, 0.5, 0.7],
+        [1.0, 2.0, 3.0, 4.0, nan],
+        [-inf, -inf, -inf, -inf, -inf],
+        [-0.0, 0.0, -0.0, 0.0, -1.0],
+        [0.0, -0.0, 0.0, -0.0, -1.0],
+        [nan, nan, nan, nan, nan],
+        [inf, 1.0, inf, nan, -inf],
+    ]
+    say("argmax special rows")
+    got = _argmax_rows(rows)
+    want = [oracle.argmax_f32(np.array(r, np.float32)) for r in rows]
+    assert list(got) == want
+
+
+def test_argmax_golden_and_large():
+    import json
+    import os
+    g = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
+                                    "reference_known_answers.json")))
+    for values, expect in g["argmax_first_index"]["cases"]:
+        say(f"argmax golden {values}")
+        assert int(_argmax_rows([values])[0]) == expect
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((8, 32000)).astype(np.float32)
+    x[3, 17] = x[3, 29999] = 50.0  # tie: first wins
+    x[5, 100] = np.nan
+    idx = ca.Buffer(8 * 4)
+    say("argmax 8 x 32000")
+    ca.argmax_f32(ca.Buffer.from_array(x), idx, 8, 32000)
+    assert list(idx.read(np.uint32)) == [oracle.argmax_f32(r) for r in x]
+
+
+def _attn_inputs(B, Tq, H, L, seed):
+    D = 128
+    q = dev_normal_bf16(B * Tq * H * D, seed, 0)
+    k = dev_normal_bf16(B * H * L * D, seed, 1)
+    v = dev_normal_bf16(B * H * L * D, seed, 2)
+    return q, k, v
+
+
+@pytest.mark.parametrize("B,Tq,H,L,lens", [(2, 4, 3, 64, [10, 4]), (1, 7, 2, 300, [300]),
+                                           (2, 64, 4, 512, [512, 100]), (3, 2, 1, 16, [1, 0, 16])])
+def test_attention_causal_matches_prefix_decode(B, Tq, H, L, lens):
+    D = 128
+    q, k, v = _attn_inputs(B, Tq, H, L, B * 10 + Tq)
+    lb = ca.Buffer.from_array(np.array(lens, np.uint32))
+    scale = 1.0 / math.sqrt(D)
+    o32 = ca.Buffer(B * Tq * H * D * 4)
+    o16 = ca.Buffer(B * Tq * H * D * 2)
+    say(f"causal attention B={B} Tq={Tq} H={H} L={L} lens={lens}")
+    ca.attn_causal_bf16(q, k, v, lb, o32, B, Tq, H, L, D, scale, out_f32=True)
+    ca.attn_causal_bf16(q, k, v, lb, o16, B, Tq, H, L, D, scale, out_f32=False)
+    want = od.attn_causal(q.read(np.uint16), k.read(np.uint16, (B, H, L, D)),
+                          v.read(np.uint16, (B, H, L, D)), lens, B, Tq, H, D, scale)
+    g32 = o32.read(np.float32, (B * Tq, H * D))
+    _bitwise(g32, want)
+    _bitwise(o16.read(np.uint16, (B * Tq, H * D)), oracle.f32_to_bf16_bits_np(want))
+
+
+def test_attention_causal_tq1_equals_decode_kernel():
+    B, H, L, D = 4, 8, 1024, 128
+    q, k, v = _attn_inputs(B, 1, H, L, 99)
+    lb = ca.Buffer.from_array(np.array([1024, 3, 700, 64], np.uint32))
+    a, b = ca.Buffer(B * H * D * 4), ca.Buffer(B * H * D * 4)
+    say("causal Tq=1 vs decode kernel")
+    ca.attn_causal_bf16(q, k, v, lb, a, B, 1, H, L, D, 1 / math.sqrt(D), out_f32=True)
+    ca.attn_decode_bf16(q, k, v, lb, b, B, H, L, D, 1 / math.sqrt(D))
+    assert np.array_equal(a.read(np.uint32), b.read(np.uint32))
+
+
+def test_programs_rmsnorm_and_argmax():
+    rt = ca.Runtime([])
+    x = [1.0, 2.0, 4.0, -1.0, -9.0, 13.29]  # catena-lang/tests/runtime.rs:1011-1044
+    say("runtime exec nn.rmsnorm")
+    [res] = rt.exec("nn.rmsnorm", [rt.mem_f32(x)], 1)
+    got = ca.mem_to_array(res.get(), np.float32)
+    _bitwise(got, oracle.rmsnorm_f32(np.array(x, np.float32)))
+    ms = sum(v * v for v in x) / len(x)
+    assert np.abs(got - np.array(x) / math.sqrt(ms + 1e-5)).max() < 3e-3
+    ca.mem_free(res.get())
+    say("runtime exec tensor.argmax-f32")
+    [res] = rt.exec("tensor.argmax-f32", [rt.mem_f32([1.0, 3.0, 3.0, 2.0])], 1)
+    assert res.get() == 1  # first index of the tie (catena-lang/tests/runtime.rs:1176-1197)
