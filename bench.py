@@ -6,7 +6,8 @@ one launch of that GEMM on inputs already resident in HBM.  The same JSON line
 carries, under "extra", the KV-cache decode attention (configs[3]: B=32,
 H=32, D=128, L=4096) and the decode-shape GEMMs, each with its
 own roofline, because BASELINE.json's metric names both GEMM TFLOP/s and
-attention HBM GB/s.
+attention HBM GB/s, and the decoder block of configs[4] (prefill and greedy
+decode timed separately).
 
 Timing: W untimed warmup launches, then K launches bracketed by stream
 synchronisation and HIP events recorded on the library's own stream (the
@@ -158,6 +159,56 @@ def bench_attention(steps, warmup, ev):
             "bitwise_run_to_run": output_hash(o) == h0, "inputs": (q, k, v)}
 
 
+def bench_decoder(reps: int, ev):
+    """configs[4] (C5): one Llama-style block, d=2048, 16 heads of 128, SwiGLU
+    5632, RMSNorm, RoPE; vocab 32000 embedding and LM head (bf16, N(0, 0.02));
+    batch 8: a 512-token prefill, then 128 greedy decode steps that feed each
+    argmax back on the device.  Times the prefill and the 128-step loop
+    separately (HIP events on the library stream), median over `reps`."""
+    d, H, F, layers, V, B, T, steps = 2048, 16, 5632, 1, 32000, 8, 512, 128
+    dec = ca.Decoder(d, H, F, layers, V, B, T + steps)
+    dec.init_weights(seed=51, std=0.02)
+    tokens = np.random.default_rng(51).integers(0, V, (B, T)).astype(np.uint32)
+    tb = ca.Buffer.from_array(tokens)
+    nxt = ca.Buffer(B * 4)
+    out = ca.Buffer(steps * B * 4)
+    pre, gen, hashes = [], [], set()
+    for r in range(reps + 1):
+        ca.synchronize()
+        ev.start()
+        dec.prefill(tb, B, T, nxt)
+        p_ms = ev.stop_ms()
+        ev.start()
+        dec.generate(steps, out)
+        g_ms = ev.stop_ms()
+        if r > 0:  # the first repetition allocates the activations
+            pre.append(p_ms)
+            gen.append(g_ms)
+        hashes.add(output_hash(out))
+    p_ms, g_ms = float(np.median(pre)), float(np.median(gen))
+    block_params = 4 * d * d + 3 * d * F
+    head_params = 2 * V * d  # embedding + LM head
+    prefill_flop = 2.0 * B * T * block_params + 2.0 * B * d * V
+    kv_step = 2.0 * B * H * 128 * 2 * (T + steps / 2)  # K + V read per step, average length
+    step_bytes = 2.0 * (block_params + d * V) + kv_step
+    res = {
+        "workload": "C5: d=2048, 16x128 heads, SwiGLU 5632, RMSNorm, RoPE, 1 block, vocab 32000 "
+                    "(embedding + LM head), batch 8, 512-token prefill then 128 greedy steps",
+        "prefill_ms": p_ms,
+        "prefill_tokens_per_s": B * T / (p_ms * 1e-3),
+        "prefill_gemm_tflops": prefill_flop / (p_ms * 1e-3) / 1e12,
+        "decode_ms_per_step": g_ms / steps,
+        "decode_tokens_per_s": B * steps / (g_ms * 1e-3),
+        "decode_bytes_per_step": step_bytes,
+        "decode_GB/s": step_bytes / (g_ms / steps * 1e-3) / 1e9,
+        "decode_frac_hbm": step_bytes / (g_ms / steps * 1e-3) / 1e9 / PEAK_HBM_GBS,
+        "params": {"block": block_params, "embedding_and_head": head_params},
+        "bitwise_run_to_run": len(hashes) == 1,
+    }
+    dec.close()
+    return res
+
+
 # ------------------------------------------------------------------ CPU baseline
 def cpu_baseline_gemm(a_buf, b_buf, rows: int, threads: int):
     import oracle
@@ -224,7 +275,11 @@ def main(argv=None) -> int:
         at = bench_attention(max(5, args.steps // 5), max(2, args.warmup // 5), ev)
         print("[bench] decode GEMMs M=16", file=sys.stderr, flush=True)
         dg = bench_decode_gemm(max(20, args.steps), args.warmup, ev)
+        print("[bench] decoder block C5 (prefill 8x512, 128 greedy steps)", file=sys.stderr,
+              flush=True)
+        dc = bench_decoder(3, ev)
         extra = {
+            "decoder_c5": dc,
             "decode_attention": {
                 "workload": "B=32 H=32 D=128 L=4096 bf16 KV, f32 softmax/out, bitwise vs sequential oracle",
                 "us_per_launch": at["us"], "GB/s": at["GB/s"], "bitwise_run_to_run": at["bitwise_run_to_run"],

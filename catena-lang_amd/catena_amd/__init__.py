@@ -132,7 +132,7 @@ SIGNATURES = {
     "catena_mi355x_embed_bf16": (_int, [_vp, _vp, _vp, _u64, _u32, _u32]),
     "catena_mi355x_rope_inv_freq": (_int, [ctypes.POINTER(_f32), _u32, ctypes.c_double]),
     "catena_mi355x_rope_qkv_bf16": (_int, [_vp] * 6 + [_u32] * 5),
-    "catena_mi355x_silu_mul_bf16": (_int, [_vp, _vp, _u64, _u32]),
+    "catena_mi355x_silu_mul_bf16": (_int, [_vp, _vp, _u64, _u32, _u32]),
     "catena_mi355x_argmax_f32": (_int, [_vp, _vp, _u64, _u64]),
     "program_nn_rmsnorm": (None, [Mem, ctypes.POINTER(Mem)]),
     "program_tensor_argmax_f32": (None, [Mem, ctypes.POINTER(_u64)]),
@@ -328,8 +328,8 @@ def rope_qkv_bf16(qkv, inv_freq, lens, q, k_cache, v_cache, batch: int, tq: int,
                                             _p(v_cache), batch, tq, heads, head_dim, max_len))
 
 
-def silu_mul_bf16(gu, out, rows: int, ffn: int) -> None:
-    check(lib().catena_mi355x_silu_mul_bf16(_p(gu), _p(out), rows, ffn))
+def silu_mul_bf16(gu, out, rows: int, ffn: int, group: int = 0) -> None:
+    check(lib().catena_mi355x_silu_mul_bf16(_p(gu), _p(out), rows, ffn, group))
 
 
 def argmax_f32(x, idx, rows: int, n: int) -> None:

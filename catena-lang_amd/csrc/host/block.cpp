@@ -4,6 +4,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstdlib>
+#include <cstring>
 
 #include "internal.h"
 
@@ -14,11 +15,15 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 
 int rmsnorm_launch(const float* x, const float* resid, const uint32_t* row_index, float* h_out,
-                   float* y_f32, uint16_t* y_bf16, uint64_t rows, uint64_t n) {
+                   float* y_f32, uint16_t* y_bf16, uint64_t rows, uint64_t n,
+                   const uint32_t* tokens = nullptr, const uint16_t* table = nullptr,
+                   uint32_t vocab = 0) {
   int st = ensure_init();
   if (st) return st;
   if (rows == 0 || n == 0) return CATENA_OK;
-  if (!x || (!y_f32 && !y_bf16)) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
+  if ((!x && !tokens) || (!y_f32 && !y_bf16)) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
+  if (tokens && (!table || (n % 4 == 0 && (reinterpret_cast<uintptr_t>(table) & 7u))))
+    return fail(CATENA_ERR_INVALID_ARGUMENT, "embedding table missing or misaligned");
   if (rows > 0x7FFFFFFFull || n > 0xFFFFFFFFull)
     return fail(CATENA_ERR_UNSUPPORTED, "rmsnorm shape too large");
   if (n % 4 == 0) {
@@ -35,10 +40,18 @@ int rmsnorm_launch(const float* x, const float* resid, const uint32_t* row_index
     return fail(CATENA_ERR_UNSUPPORTED, "rmsnorm row of %llu needs %zu B of LDS",
                 (unsigned long long)n, lds);
   uint32_t n32 = (uint32_t)n;
-  void* args[] = {&x, &resid, &row_index, &h_out, &y_f32, &y_bf16, &n32};
+  void* args[] = {&x, &resid, &row_index, &h_out, &y_f32, &y_bf16, &n32, &tokens, &table, &vocab};
   return launch(KernelId::RmsnormRows, dim3((unsigned)rows), dim3(256), lds, args);
 }
 }  // namespace
+
+namespace catena {
+int embed_rmsnorm_bf16(const uint32_t* tokens, const uint16_t* table, uint32_t vocab,
+                       float* x_out, uint16_t* y, uint64_t rows, uint64_t n) {
+  if (!tokens || !y) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
+  return rmsnorm_launch(nullptr, nullptr, nullptr, x_out, nullptr, y, rows, n, tokens, table, vocab);
+}
+}  // namespace catena
 
 extern "C" {
 
@@ -57,6 +70,22 @@ int catena_mi355x_attn_causal_bf16(const uint16_t* q, const uint16_t* k, const u
   if (!aligned16(k) || !aligned16(v))
     return fail(CATENA_ERR_INVALID_ARGUMENT, "K/V caches must be 16-byte aligned");
   if (blocks > 0x7FFFFFFFu) return fail(CATENA_ERR_UNSUPPORTED, "too many queries");
+  // Many queries per sequence: the block-of-16-queries kernel, which reads
+  // each K / V row once per block (its score buffer grows with max_len, so
+  // it is used while two workgroups still fit a CU).  CATENA_ATTN_PREFILL=0
+  // selects the one-query-per-workgroup kernel for comparison; both give the
+  // same bits.
+  const size_t lds_pf = 16 * 128 * 4 + 64 * 128 * 2 + 3 * 16 * 4 + (size_t)max_len * 17 * 4;
+  const char* pf = getenv("CATENA_ATTN_PREFILL");
+  const bool prefill_ok = !(pf && strcmp(pf, "0") == 0);
+  if (prefill_ok && tq >= 8 && lds_pf <= 80 * 1024) {
+    const uint64_t nqb = ceil_div(tq, 16);
+    const uint64_t grid = (uint64_t)batch * heads * nqb;
+    if (grid > 0x7FFFFFFFu) return fail(CATENA_ERR_UNSUPPORTED, "too many query blocks");
+    void* pargs[] = {&q, &k, &v, &lens, &o, &batch, &heads, &max_len, &tq, &scale};
+    return launch(out_f32 ? KernelId::AttnPrefillD128F32 : KernelId::AttnPrefillD128Bf16,
+                  dim3((unsigned)grid), dim3(256), lds_pf, pargs);
+  }
   const size_t lds = 128 * 4 + 20480 + 64 + (size_t)max_len * 4;
   if (lds > device().max_lds)
     return fail(CATENA_ERR_UNSUPPORTED, "max_len %u needs %zu B of LDS (device has %zu)", max_len,
@@ -121,15 +150,18 @@ int catena_mi355x_rope_qkv_bf16(const float* qkv, const float* inv_freq, const u
   return launch(KernelId::RopeQkvStore, dim3((unsigned)ceil_div(threads, 256)), dim3(256), 0, args);
 }
 
-int catena_mi355x_silu_mul_bf16(const float* gu, uint16_t* out, uint64_t rows, uint32_t ffn) {
+int catena_mi355x_silu_mul_bf16(const float* gu, uint16_t* out, uint64_t rows, uint32_t ffn,
+                                uint32_t group) {
   int st = ensure_init();
   if (st) return st;
   if (rows == 0 || ffn == 0) return CATENA_OK;
   if (!gu || !out) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
   if (ffn % 4 != 0 || !aligned16(gu) || (reinterpret_cast<uintptr_t>(out) & 7u))
     return fail(CATENA_ERR_INVALID_ARGUMENT, "silu_mul needs F %% 4 == 0 and aligned rows");
+  if (group != 0 && (group % 4 != 0 || ffn % group != 0))
+    return fail(CATENA_ERR_INVALID_ARGUMENT, "silu_mul group must divide F and be a multiple of 4");
   if (rows > 65535) return fail(CATENA_ERR_UNSUPPORTED, "silu_mul of more than 65535 rows");
-  void* args[] = {&gu, &out, &ffn};
+  void* args[] = {&gu, &out, &ffn, &group};
   return launch(KernelId::SiluMulBf16, dim3((unsigned)ceil_div(ffn, 1024), (unsigned)rows),
                 dim3(256), 0, args);
 }
@@ -141,9 +173,23 @@ int catena_mi355x_argmax_f32(const float* x, uint32_t* idx, uint64_t rows, uint6
   if (!idx || (n > 0 && !x)) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
   if (rows > 0x7FFFFFFFull || n >= 0x7FFFFFFFull)
     return fail(CATENA_ERR_UNSUPPORTED, "argmax shape too large");
-  uint32_t n32 = (uint32_t)n;
-  void* args[] = {&x, &idx, &n32};
-  return launch(KernelId::ArgmaxRowsF32, dim3((unsigned)rows), dim3(256), 0, args);
+  if (rows > 65535) return fail(CATENA_ERR_UNSUPPORTED, "argmax of more than 65535 rows");
+  // Chunks of 4096 elements per workgroup (fewer, longer ones when the
+  // per-row partials would not fit the library's scratch).
+  const Device& d = device();
+  const uint64_t max_parts = Device::kRowPartialBytes / 12;
+  uint64_t chunk = 4096;
+  if (rows > Device::kTicketsRows) {
+    chunk = n > 0 ? n : 1;  // one workgroup per row: no ticket needed
+  } else {
+    while (rows * ceil_div(n, chunk) > max_parts) chunk *= 2;
+  }
+  const uint64_t chunks = n > 0 ? ceil_div(n, chunk) : 1;
+  uint32_t n32 = (uint32_t)n, chunk32 = (uint32_t)chunk;
+  uint32_t* tickets = d.row_tickets();
+  uint32_t* partials = static_cast<uint32_t*>(d.row_partials());
+  void* args[] = {&x, &idx, &n32, &chunk32, &tickets, &partials};
+  return launch(KernelId::ArgmaxRowsF32, dim3((unsigned)chunks, (unsigned)rows), dim3(256), 0, args);
 }
 
 // ---------------------------------------------------------------- programs

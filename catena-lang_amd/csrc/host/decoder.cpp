@@ -111,7 +111,10 @@ void release(catena_decoder* m) {
 // One forward pass over rows = batch * tq tokens (tq per sequence), caches
 // already holding the earlier positions; lens = positions after the append;
 // final_rows selects each sequence's last row (NULL when tq == 1); next
-// receives the greedy tokens.
+// receives the greedy tokens.  A decode step (tq == 1, batch <= 16) runs the
+// projections on the decode-shape GEMM with fused epilogues: RoPE and the
+// cache append after W_qkv, the SwiGLU gate after W_gu, greedy argmax after
+// W_lm; the embedding gather is fused into the first RMSNorm in both cases.
 int forward(catena_decoder& m, const uint32_t* tokens, uint32_t batch, uint32_t tq,
             const uint32_t* lens, const uint32_t* final_rows, uint32_t* next) {
   const catena_decoder_config_t& c = m.cfg;
@@ -130,34 +133,61 @@ int forward(catena_decoder& m, const uint32_t* tokens, uint32_t batch, uint32_t 
   uint16_t* ACT = static_cast<uint16_t*>(A(CATENA_DEC_ACT));
   float* FO = static_cast<float*>(A(CATENA_DEC_FFN_OUT));
   const float scale = (float)(1.0 / std::sqrt((double)c.head_dim));
+  const float* inv = static_cast<const float*>(m.inv_freq);
+  const bool step = tq == 1 && batch <= 16;
 
-  TRY(catena_mi355x_embed_bf16(tokens, static_cast<const uint16_t*>(m.embed), X, rows, c.vocab,
-                               (uint32_t)d));
   for (uint32_t l = 0; l < c.n_layers; ++l) {
     // x_l = h_{l-1} + ffn_{l-1} (layer 0: the embedding), xn = bf16(rmsnorm(x_l))
     if (l == 0)
-      TRY(catena_mi355x_residual_rmsnorm_bf16(X, nullptr, nullptr, nullptr, XN, rows, d));
+      TRY(embed_rmsnorm_bf16(tokens, static_cast<const uint16_t*>(m.embed), c.vocab, X, XN, rows, d));
     else
       TRY(catena_mi355x_residual_rmsnorm_bf16(H, FO, nullptr, X, XN, rows, d));
-    TRY(catena_mi355x_gemm_bf16(XN, static_cast<const uint16_t*>(m.w_qkv[l]), QKV, rows, 3 * d, d, 1));
     uint16_t* kc = static_cast<uint16_t*>(m.kc[l]);
     uint16_t* vc = static_cast<uint16_t*>(m.vc[l]);
-    TRY(catena_mi355x_rope_qkv_bf16(QKV, static_cast<const float*>(m.inv_freq), lens, Q, kc, vc,
-                                    batch, tq, c.n_heads, c.head_dim, c.max_len));
+    const uint16_t* wqkv = static_cast<const uint16_t*>(m.w_qkv[l]);
+    if (step) {
+      DecodeEpiArgs e;
+      e.q_out = Q;
+      e.k_cache = kc;
+      e.v_cache = vc;
+      e.lens = lens;
+      e.inv_freq = inv;
+      e.heads = c.n_heads;
+      e.max_len = c.max_len;
+      TRY(gemm_bf16_decode(XN, wqkv, QKV, rows, 3 * d, d, DecodeEpilogue::Rope, e));
+    } else {
+      TRY(catena_mi355x_gemm_bf16(XN, wqkv, QKV, rows, 3 * d, d, 1));
+      TRY(catena_mi355x_rope_qkv_bf16(QKV, inv, lens, Q, kc, vc, batch, tq, c.n_heads, c.head_dim,
+                                      c.max_len));
+    }
     TRY(catena_mi355x_attn_causal_bf16(Q, kc, vc, lens, ATT, batch, tq, c.n_heads, c.max_len,
                                        c.head_dim, scale, 0));
     TRY(catena_mi355x_gemm_bf16(ATT, static_cast<const uint16_t*>(m.w_o[l]), AP, rows, d, d, 1));
     TRY(catena_mi355x_residual_rmsnorm_bf16(X, AP, nullptr, H, HN, rows, d));
-    TRY(catena_mi355x_gemm_bf16(HN, static_cast<const uint16_t*>(m.w_gu[l]), GU, rows, 2 * f, d, 1));
-    TRY(catena_mi355x_silu_mul_bf16(GU, ACT, rows, (uint32_t)f));
+    const uint16_t* wgu = static_cast<const uint16_t*>(m.w_gu[l]);
+    if (step) {
+      DecodeEpiArgs e;
+      e.act = ACT;
+      TRY(gemm_bf16_decode(HN, wgu, GU, rows, 2 * f, d, DecodeEpilogue::Silu, e));
+    } else {
+      TRY(catena_mi355x_gemm_bf16(HN, wgu, GU, rows, 2 * f, d, 1));
+      TRY(catena_mi355x_silu_mul_bf16(GU, ACT, rows, (uint32_t)f, 64));
+    }
     TRY(catena_mi355x_gemm_bf16(ACT, static_cast<const uint16_t*>(m.w_down[l]), FO, rows, d, f, 1));
   }
   float* FH = static_cast<float*>(A(CATENA_DEC_FINAL_H));
   uint16_t* FXN = static_cast<uint16_t*>(A(CATENA_DEC_FINAL_XN));
   float* LG = static_cast<float*>(A(CATENA_DEC_LOGITS));
   TRY(catena_mi355x_residual_rmsnorm_bf16(H, FO, final_rows, FH, FXN, batch, d));
-  TRY(catena_mi355x_gemm_bf16(FXN, static_cast<const uint16_t*>(m.w_lm), LG, batch, c.vocab, d, 1));
-  TRY(catena_mi355x_argmax_f32(LG, next, batch, c.vocab));
+  const uint16_t* wlm = static_cast<const uint16_t*>(m.w_lm);
+  if (batch <= 16) {
+    DecodeEpiArgs e;
+    e.idx = next;
+    TRY(gemm_bf16_decode(FXN, wlm, LG, batch, c.vocab, d, DecodeEpilogue::Argmax, e));
+  } else {
+    TRY(catena_mi355x_gemm_bf16(FXN, wlm, LG, batch, c.vocab, d, 1));
+    TRY(catena_mi355x_argmax_f32(LG, next, batch, c.vocab));
+  }
   return CATENA_OK;
 }
 
@@ -177,8 +207,8 @@ int catena_mi355x_decoder_create(const catena_decoder_config_t* cfg, catena_deco
     return fail(CATENA_ERR_INVALID_ARGUMENT, "decoder sizes must be non-zero");
   if ((uint64_t)c.n_heads * c.head_dim != c.d_model)
     return fail(CATENA_ERR_INVALID_ARGUMENT, "d_model must equal n_heads * head_dim");
-  if (c.ffn_dim % 8 != 0 || c.vocab % 8 != 0)
-    return fail(CATENA_ERR_INVALID_ARGUMENT, "ffn_dim and vocab must be multiples of 8");
+  if (c.ffn_dim % 64 != 0 || c.vocab % 8 != 0)
+    return fail(CATENA_ERR_INVALID_ARGUMENT, "ffn_dim must be a multiple of 64, vocab of 8");
   if (!(c.rope_base > 1.0f)) return fail(CATENA_ERR_INVALID_ARGUMENT, "rope_base must exceed 1");
 
   catena_decoder* m = new (std::nothrow) catena_decoder();

@@ -74,12 +74,17 @@ const KernelSpec kKernels[] = {
     {KernelId::GemmBf16DeepF32, "gemm_bf16_deep", "catena_gemm_bf16_deep4_f32out"},
     {KernelId::GemmBf16DeepFrontBf16, "gemm_bf16_deep", "catena_gemm_bf16_deep4f_bf16out"},
     {KernelId::GemmBf16DeepFrontF32, "gemm_bf16_deep", "catena_gemm_bf16_deep4f_f32out"},
-    {KernelId::GemmBf16Decode, "gemm_bf16_decode", "catena_gemm_bf16_decode"},
-    {KernelId::GemmBf16DecodeReduce, "gemm_bf16_decode", "catena_gemm_bf16_decode_reduce"},
+    {KernelId::GemmBf16DecodeF32, "gemm_bf16_decode", "catena_gemm_bf16_decode_f32out"},
+    {KernelId::GemmBf16DecodeBf16, "gemm_bf16_decode", "catena_gemm_bf16_decode_bf16out"},
+    {KernelId::GemmBf16DecodeRope, "gemm_bf16_decode", "catena_gemm_bf16_decode_rope"},
+    {KernelId::GemmBf16DecodeSilu, "gemm_bf16_decode", "catena_gemm_bf16_decode_silu"},
+    {KernelId::GemmBf16DecodeArgmax, "gemm_bf16_decode", "catena_gemm_bf16_decode_argmax"},
     {KernelId::AttnDecodeD128, "attn_decode", "catena_attn_decode_bf16_d128"},
     {KernelId::AttnDecodeD128KC, "attn_decode", "catena_attn_decode_bf16_d128_kc"},
     {KernelId::AttnCausalD128F32, "attn_decode", "catena_attn_causal_bf16_d128_f32out"},
     {KernelId::AttnCausalD128Bf16, "attn_decode", "catena_attn_causal_bf16_d128_bf16out"},
+    {KernelId::AttnPrefillD128F32, "attn_prefill", "catena_attn_prefill_bf16_d128_f32out"},
+    {KernelId::AttnPrefillD128Bf16, "attn_prefill", "catena_attn_prefill_bf16_d128_bf16out"},
     {KernelId::EmbedRowsBf16, "block", "catena_embed_rows_bf16"},
     {KernelId::RmsnormRows, "block", "catena_rmsnorm_rows"},
     {KernelId::RopeQkvStore, "block", "catena_rope_qkv_store"},
@@ -269,6 +274,12 @@ int catena_mi355x_init(int device_index) {
   d.cu_count = prop.multiProcessorCount;
   st = hip_check(hipStreamCreateWithFlags(&d.stream, hipStreamNonBlocking), "hipStreamCreate");
   if (st) return st;
+  void* small = nullptr;
+  st = hip_check(hipMalloc(&small, Device::kSmallBytes), "hipMalloc(tickets)");
+  if (st) return st;
+  st = hip_check(hipMemset(small, 0, Device::kSmallBytes), "hipMemset(tickets)");
+  if (st) return st;
+  d.small = static_cast<unsigned char*>(small);
   const std::string dir = library_dir();
   std::unordered_map<std::string, hipModule_t> modules;
   for (const KernelSpec& k : kKernels) {

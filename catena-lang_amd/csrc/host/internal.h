@@ -34,12 +34,17 @@ enum class KernelId : int {
   GemmBf16DeepF32,
   GemmBf16DeepFrontBf16,
   GemmBf16DeepFrontF32,
-  GemmBf16Decode,
-  GemmBf16DecodeReduce,
+  GemmBf16DecodeF32,
+  GemmBf16DecodeBf16,
+  GemmBf16DecodeRope,
+  GemmBf16DecodeSilu,
+  GemmBf16DecodeArgmax,
   AttnDecodeD128,
   AttnDecodeD128KC,
   AttnCausalD128F32,
   AttnCausalD128Bf16,
+  AttnPrefillD128F32,
+  AttnPrefillD128Bf16,
   EmbedRowsBf16,
   RmsnormRows,
   RopeQkvStore,
@@ -62,6 +67,21 @@ struct Device {
   hipFunction_t fn[static_cast<int>(KernelId::Count)] = {};
   void* ws = nullptr;  // split-K partials
   uint64_t ws_bytes = 0;
+  // Zeroed once at init; kernels that take completion tickets return their
+  // counters to zero.  Layout: kTicketsGemm column-block counters,
+  // kTicketsRows row counters, kTicketsMisc single counters, then
+  // kRowPartialBytes of per-row partials.
+  unsigned char* small = nullptr;
+  static constexpr uint32_t kTicketsGemm = 16384;
+  static constexpr uint32_t kTicketsRows = 16384;
+  static constexpr uint32_t kTicketsMisc = 256;
+  static constexpr uint64_t kRowPartialBytes = 896 * 1024;
+  static constexpr uint64_t kSmallBytes =
+      4ull * (kTicketsGemm + kTicketsRows + kTicketsMisc) + kRowPartialBytes;
+  uint32_t* gemm_tickets() const { return reinterpret_cast<uint32_t*>(small); }
+  uint32_t* row_tickets() const { return gemm_tickets() + kTicketsGemm; }
+  uint32_t* misc_tickets() const { return row_tickets() + kTicketsRows; }
+  void* row_partials() const { return misc_tickets() + kTicketsMisc; }
 };
 
 Device& device();
@@ -75,6 +95,32 @@ int pool_alloc(uint64_t len, void** out);
 int pool_free(void* ptr);
 uint64_t pool_capacity(void* ptr);
 int workspace(uint64_t bytes, void** out);
+
+// Extra operands of the fused decode-GEMM epilogues; layout shared with
+// struct DecodeEpi in gemm_bf16_decode.hip (passed by value as a kernel
+// argument).
+struct DecodeEpiArgs {
+  uint16_t* q_out = nullptr;
+  uint16_t* k_cache = nullptr;
+  uint16_t* v_cache = nullptr;
+  const uint32_t* lens = nullptr;
+  const float* inv_freq = nullptr;
+  uint32_t heads = 0, max_len = 0;
+  uint16_t* act = nullptr;
+  uint32_t* idx = nullptr;
+  uint32_t* arg_ticket = nullptr;
+  uint32_t* arg_partials = nullptr;
+};
+enum class DecodeEpilogue { StoreF32, StoreBf16, Rope, Silu, Argmax };
+// Decode-shape GEMM (n <= 16) with an epilogue; c is Y (f32, or bf16 for
+// StoreBf16).  Rope: m = 3 * heads * 128, one token per row; Silu: gate / up
+// interleaved in 64-column groups, act[n][m/2]; Argmax: idx[n].
+int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, uint64_t m,
+                     uint64_t k, DecodeEpilogue epi, const DecodeEpiArgs& ep);
+// nn.rmsnorm rows whose input is an embedding gather (x = widen(table[tok]))
+// written to x_out, bf16 output.
+int embed_rmsnorm_bf16(const uint32_t* tokens, const uint16_t* table, uint32_t vocab,
+                       float* x_out, uint16_t* y, uint64_t rows, uint64_t n);
 
 // Fail-stop used by the program ABI: message on stderr, then trap, like
 // catena_assert / catena_host_gpu_check (catena-lang/src/codegen/prelude.rs:38-55).

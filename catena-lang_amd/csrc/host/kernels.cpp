@@ -59,6 +59,67 @@ uint32_t decode_kw(uint64_t n_cols, uint64_t k) {
 }
 }  // namespace
 
+namespace catena {
+
+int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, uint64_t m,
+                     uint64_t k, DecodeEpilogue epi, const DecodeEpiArgs& ep) {
+  int st = ensure_init();
+  if (st) return st;
+  if (n == 0 || m == 0) return CATENA_OK;
+  if (n > 16 || k == 0 || m % 8 != 0 || k % 8 != 0 || !aligned16(a) || !aligned16(b) ||
+      !aligned16(c))
+    return fail(CATENA_ERR_INVALID_ARGUMENT, "decode GEMM shape or alignment");
+  Device& d = device();
+  const uint32_t M = (uint32_t)n;
+  const uint32_t kw = decode_kw(m, k);
+  const uint64_t chunks = ceil_div(k, kw);
+  const uint64_t S = ceil_div(chunks, 4);
+  const uint64_t gx = ceil_div(m, 128);
+  if (S > 65535 || gx > Device::kTicketsGemm)
+    return fail(CATENA_ERR_UNSUPPORTED, "decode GEMM grid too large");
+  KernelId id = KernelId::GemmBf16DecodeF32;
+  DecodeEpiArgs e = ep;
+  switch (epi) {
+    case DecodeEpilogue::StoreF32: break;
+    case DecodeEpilogue::StoreBf16: id = KernelId::GemmBf16DecodeBf16; break;
+    case DecodeEpilogue::Rope:
+      if (e.heads == 0 || m != 3ull * e.heads * 128 || !e.q_out || !e.k_cache || !e.v_cache ||
+          !e.lens || !e.inv_freq)
+        return fail(CATENA_ERR_INVALID_ARGUMENT, "rope epilogue operands");
+      id = KernelId::GemmBf16DecodeRope;
+      break;
+    case DecodeEpilogue::Silu:
+      if (m % 128 != 0 || !e.act) return fail(CATENA_ERR_INVALID_ARGUMENT, "silu epilogue operands");
+      id = KernelId::GemmBf16DecodeSilu;
+      break;
+    case DecodeEpilogue::Argmax:
+      if (!e.idx || m >= 0x7FFFFFFFull) return fail(CATENA_ERR_INVALID_ARGUMENT, "argmax epilogue operands");
+      if (n * gx * 12 > Device::kRowPartialBytes)
+        return fail(CATENA_ERR_UNSUPPORTED, "argmax epilogue over %llu column blocks",
+                    (unsigned long long)gx);
+      e.arg_ticket = d.misc_tickets();
+      e.arg_partials = static_cast<uint32_t*>(d.row_partials());
+      id = KernelId::GemmBf16DecodeArgmax;
+      break;
+  }
+  float* P = nullptr;
+  if (S > 1) {
+    void* ws = nullptr;
+    st = workspace(S * M * m * sizeof(float), &ws);
+    if (st) return st;
+    P = static_cast<float*>(ws);
+  }
+  const uint16_t* X = a;
+  const uint16_t* W = b;
+  void* Y = c;
+  uint64_t N = m, K = k;
+  uint32_t* tickets = d.gemm_tickets();
+  void* args[] = {&X, &W, &Y, &P, &tickets, (void*)&M, &N, &K, (void*)&kw, &e};
+  return launch(id, dim3((unsigned)gx, (unsigned)S), dim3(256), 0, args);
+}
+
+}  // namespace catena
+
 extern "C" {
 
 int catena_mi355x_gemm_f32_exact(const float* a, const float* b, float* c, uint64_t n, uint64_t m,
@@ -83,35 +144,10 @@ int catena_mi355x_gemm_bf16(const uint16_t* a, const uint16_t* b, void* c, uint6
 
   // decode shape: <= 16 rows of activations against a K x N weight
   if (n <= 16 && k > 0 && m % 8 == 0 && k % 8 == 0 && aligned16(a) && aligned16(b) &&
-      aligned16(c)) {
-    const uint32_t M = (uint32_t)n;
-    const uint32_t kw = decode_kw(m, k);
-    const uint64_t chunks = ceil_div(k, kw);
-    const uint64_t S = ceil_div(chunks, 4);
-    const uint64_t gx = ceil_div(m, 128);
-    if (S > 65535 || gx > 0x7FFFFFFFu) return fail(CATENA_ERR_UNSUPPORTED, "decode grid too large");
-    float* P = nullptr;
-    if (S > 1) {
-      void* ws = nullptr;
-      st = workspace(S * M * m * sizeof(float), &ws);
-      if (st) return st;
-      P = static_cast<float*>(ws);
-    }
-    const uint16_t* X = a;
-    const uint16_t* W = b;
-    void* Y = c;
-    uint64_t N = m, K = k;
-    uint32_t of32 = out_f32 ? 1u : 0u;
-    void* args[] = {&X, &W, &Y, &P, (void*)&M, &N, &K, (void*)&kw, &of32};
-    st = launch(KernelId::GemmBf16Decode, dim3((unsigned)gx, (unsigned)S), dim3(256), 0, args);
-    if (st || S == 1) return st;
-    uint32_t S32 = (uint32_t)S;
-    const uint64_t total4 = (uint64_t)M * m / 4;
-    const float* Pc = P;
-    void* rargs[] = {&Pc, &Y, (void*)&M, &N, &S32, &of32};
-    return launch(KernelId::GemmBf16DecodeReduce, dim3((unsigned)ceil_div(total4, 256)), dim3(256),
-                  0, rargs);
-  }
+      aligned16(c))
+    return gemm_bf16_decode(a, b, c, n, m, k,
+                            out_f32 ? DecodeEpilogue::StoreF32 : DecodeEpilogue::StoreBf16,
+                            DecodeEpiArgs{});
 
   const bool tile_ok = n % 256 == 0 && m % 256 == 0 && k % 64 == 0 && k > 0 && aligned16(a) &&
                        aligned16(b) && aligned16(c);

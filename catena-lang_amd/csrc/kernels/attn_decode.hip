@@ -219,45 +219,7 @@ CATENA_DEV void attn_body(const uint16_t* __restrict__ q, const uint16_t* __rest
   __syncthreads();
   if (tid == 0) {
     // The one sequential fold: den = (((0 + e_0) + e_1) + ...) in ascending t.
-    // The next 32 values are read from LDS before the current 32 are added.
-    float den = __uint_as_float(0u);
-    const uint32_t n4 = len / 4;
-    const f32x4_t* s4 = reinterpret_cast<const f32x4_t*>(sp);
-    uint32_t i = 0;
-    if (n4 >= 8) {
-      f32x4_t cur[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) cur[u] = s4[u];
-      for (i = 8; i + 8 <= n4; i += 8) {
-        f32x4_t nxt[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) nxt[u] = s4[i + u];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          den = den + cur[u][0];
-          den = den + cur[u][1];
-          den = den + cur[u][2];
-          den = den + cur[u][3];
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        den = den + cur[u][0];
-        den = den + cur[u][1];
-        den = den + cur[u][2];
-        den = den + cur[u][3];
-      }
-    }
-    for (; i < n4; ++i) {
-      const f32x4_t e = s4[i];
-      den = den + e[0];
-      den = den + e[1];
-      den = den + e[2];
-      den = den + e[3];
-    }
-    for (uint32_t t = n4 * 4; t < len; ++t) den = den + sp[t];
+    const float den = serial_sum_lds(sp, len);
     red_v[0] = den;
   }
   __syncthreads();

@@ -1,0 +1,307 @@
+// Causal KV-cache attention for many queries per sequence (prefill), with
+// exactly the per-query arithmetic of attn_decode.hip:
+//   s_t = (fold_{d asc} from +0 of q_d * k_{t,d}) * scale
+//   m   = f32.max-env fold from -inf;  e_t = exp~(s_t - m)
+//   den = fold_{t asc} from +0 of e_t;  p_t = e_t / den
+//   o_d = fold_{t asc} from +0 of p_t * v_{t,d}
+// (catena-lang/stdlib/matrix.hex:236-256, sum.hex:73-84, nn.hex:59-122,
+// math.hex:148-199), so every output is bitwise equal to the decode kernel
+// run on that query's prefix.
+//
+// One workgroup (4 waves) per (batch, head, block of QB = 16 consecutive
+// queries); the queries of a block share every K and V row they read.
+// Query tq of sequence b attends to the first lens[b] - (Tq - 1 - tq)
+// positions (clamped to [0, L]).
+//
+// Scores: waves take 64-key blocks round robin.  Lane l owns key kb*64 + l:
+// its 128 K values are widened into registers once and folded against each
+// of the 16 queries, whose f32 values are LDS broadcasts; the next block's
+// row is loaded while the current one is folded.  Scores go to
+// sT[key][query] (row stride QB + 1 floats: the writes of 64 keys and the
+// per-query reads of softmax are bank-conflict free).
+// Softmax: per query, the exact parallel form of the max fold (FirstMax,
+// common.h) by one wave; exp~ elementwise; the denominators are 16
+// independent serial folds, one lane per query; p = e / den elementwise.
+// Output: wave w owns queries 4w .. 4w+3 and lane l columns 2l, 2l+1 (8
+// accumulators); keys are walked in ascending order through 64-row V blocks
+// staged in LDS, the next block's loads in flight while one is folded.  Keys
+// below the shortest of the 4 prefixes need no mask; past it, a key beyond a
+// query's prefix leaves that accumulator untouched.
+#include "common.h"
+
+namespace {
+constexpr int D = 128;
+constexpr int QB = 16;               // queries per workgroup
+constexpr int HALF = QB / 2;         // queries per score item / output thread
+constexpr int ST = QB + 1;           // sT row stride (floats)
+constexpr int VBLK = 64;             // keys per V stage
+constexpr int VSTAGE = VBLK * D * 2; // bytes (bf16)
+
+CATENA_DEV int wave_max_i32(int v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const int o = __shfl_xor(v, off, 64);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+CATENA_DEV FirstMax wave_first_max(FirstMax a) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    FirstMax b;
+    b.v = __shfl_xor(a.v, off, 64);
+    b.i = (uint32_t)__shfl_xor((int)a.i, off, 64);
+    a = first_max_combine(a, b);
+  }
+  return a;
+}
+
+CATENA_DEV uint32_t query_len(uint32_t lens_b, uint32_t L, uint32_t Tq, uint32_t tq) {
+  uint32_t len = lens_b > L ? L : lens_b;
+  const uint32_t later = Tq - 1 - tq;
+  return len > later ? len - later : 0u;
+}
+}  // namespace
+
+template <bool OUT_BF16>
+CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                             const uint16_t* __restrict__ v, const uint32_t* __restrict__ lens,
+                             void* __restrict__ o, uint32_t B, uint32_t H, uint32_t L,
+                             uint32_t Tq, float scale) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  float* qf = reinterpret_cast<float*>(smem);                      // [QB][D]
+  unsigned char* vstage = smem + QB * D * 4;                       // [VBLK][D] bf16
+  float* red = reinterpret_cast<float*>(vstage + VSTAGE);          // [QB] max, [QB] den
+  float* sT = red + 3 * QB;                                        // [Lmax][ST] (after qlen)
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t BH = B * H;
+  const uint32_t nqb = (Tq + QB - 1) / QB;
+  // longest query blocks first; the blocks of one (b, h) are BH apart
+  const uint32_t qb = nqb - 1 - blockIdx.x / BH;
+  const uint32_t bh = blockIdx.x % BH;
+  const uint32_t b = bh / H, h = bh % H;
+  const uint32_t t0 = qb * QB;
+  const uint32_t nq = Tq - t0 < (uint32_t)QB ? Tq - t0 : (uint32_t)QB;
+  const uint32_t lb = lens[b];
+  // per-query lengths (LDS: indexed with runtime query numbers below); the
+  // last query of the block has the longest prefix
+  uint32_t* qlen = reinterpret_cast<uint32_t*>(red + 2 * QB);
+  if (tid < QB) qlen[tid] = (uint32_t)tid < nq ? query_len(lb, L, Tq, t0 + tid) : 0u;
+  const uint32_t lmax = query_len(lb, L, Tq, t0 + nq - 1);
+
+  const uint16_t* kb = k + (uint64_t)bh * L * D;
+  const uint16_t* vb = v + (uint64_t)bh * L * D;
+  // q rows of this block, widened (rows past nq are zero and never used)
+  for (uint32_t e = tid; e < (uint32_t)QB * D; e += 256) {
+    const uint32_t i = e / D, d = e % D;
+    float val = 0.0f;
+    if (i < nq) val = bf16_to_f32(q[(((uint64_t)b * Tq + t0 + i) * H + h) * D + d]);
+    qf[e] = val;
+  }
+  __syncthreads();
+
+  // ---------------------------------------------------------------- scores
+  {
+    const uint32_t nkb = (lmax + 63) / 64;
+    auto kload = [&](uint32_t kblk, u32x4_t r[D / 8]) {
+      const uint32_t j = kblk * 64 + lane;
+      const u32x4_t* src = reinterpret_cast<const u32x4_t*>(kb + (uint64_t)j * D);
+#pragma unroll
+      for (int c = 0; c < D / 8; ++c) r[c] = j < lmax ? src[c] : u32x4_t{0u, 0u, 0u, 0u};
+    };
+    u32x4_t raw[D / 8];
+    if ((uint32_t)wave < nkb) kload(wave, raw);
+    for (uint32_t kblk = wave; kblk < nkb; kblk += 4) {
+      float kf[D];
+#pragma unroll
+      for (int c = 0; c < D / 8; ++c) {
+        kf[8 * c + 0] = bf16lo(raw[c][0]); kf[8 * c + 1] = bf16hi(raw[c][0]);
+        kf[8 * c + 2] = bf16lo(raw[c][1]); kf[8 * c + 3] = bf16hi(raw[c][1]);
+        kf[8 * c + 4] = bf16lo(raw[c][2]); kf[8 * c + 5] = bf16hi(raw[c][2]);
+        kf[8 * c + 6] = bf16lo(raw[c][3]); kf[8 * c + 7] = bf16hi(raw[c][3]);
+      }
+      if (kblk + 4 < nkb) kload(kblk + 4, raw);
+      const uint32_t j = kblk * 64 + lane;
+#pragma unroll 1
+      for (int i = 0; i < QB; ++i) {
+        const uint32_t li = qlen[i];
+        if (kblk * 64 >= li) continue;
+        const f32x4_t* q4 = reinterpret_cast<const f32x4_t*>(qf + i * D);
+        float acc = __uint_as_float(0u);
+#pragma unroll
+        for (int c = 0; c < D / 4; ++c) {
+          const f32x4_t qq = q4[c];
+          float p;
+          p = qq[0] * kf[4 * c + 0]; acc = acc + p;
+          p = qq[1] * kf[4 * c + 1]; acc = acc + p;
+          p = qq[2] * kf[4 * c + 2]; acc = acc + p;
+          p = qq[3] * kf[4 * c + 3]; acc = acc + p;
+        }
+        if (j < li) sT[j * ST + i] = acc * scale;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---------------------------------------------------------------- max per query
+  for (int i = wave; i < QB; i += 4) {
+    const uint32_t len = qlen[i];
+    int lastnan = -1;
+    for (uint32_t t = lane; t < len; t += 64)
+      if (sT[t * ST + i] != sT[t * ST + i]) lastnan = (int)t;
+    const int J = wave_max_i32(lastnan);
+    FirstMax fm{__uint_as_float(0xFF800000u), 0xFFFFFFFFu};
+    for (uint32_t t = lane; t < len; t += 64)
+      if ((int)t > J) fm = first_max_combine(fm, FirstMax{sT[t * ST + i], t});
+    fm = wave_first_max(fm);
+    if (lane == 0) {
+      float mx;
+      if (len > 0 && J == (int)len - 1)
+        mx = sT[(len - 1) * ST + i];
+      else
+        mx = fm.i == 0xFFFFFFFFu ? __uint_as_float(0xFF800000u) : fm.v;
+      red[i] = mx;
+    }
+  }
+  __syncthreads();
+
+  // ---------------------------------------------------------------- exp~
+  for (uint32_t e = tid; e < lmax * QB; e += 256) {
+    const uint32_t t = e / QB, i = e % QB;
+    if (t < qlen[i]) {
+      const float shifted = sT[t * ST + i] - red[i];
+      sT[t * ST + i] = exp_approx(shifted);
+    }
+  }
+  __syncthreads();
+
+  // ---------------------------------------------------------------- denominators
+  if (tid < QB) {
+    // lane i: den_i = (((0 + e_0) + e_1) + ...), t ascending; the next 8
+    // values are read before the current 8 are added
+    const int i = tid;
+    const uint32_t len = qlen[i];
+    float den = __uint_as_float(0u);
+    uint32_t t = 0;
+    if (len >= 16) {
+      float cur[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) cur[u] = sT[u * ST + i];
+      for (t = 8; t + 8 <= len; t += 8) {
+        float nxt[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) nxt[u] = sT[(t + u) * ST + i];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) den = den + cur[u];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) den = den + cur[u];
+    }
+    for (; t < len; ++t) den = den + sT[t * ST + i];
+    red[QB + i] = den;
+  }
+  __syncthreads();
+  for (uint32_t e = tid; e < lmax * QB; e += 256) {
+    const uint32_t t = e / QB, i = e % QB;
+    if (t < qlen[i]) sT[t * ST + i] = sT[t * ST + i] / red[QB + i];
+  }
+  __syncthreads();
+
+  // ---------------------------------------------------------------- P V
+  const int qg = wave;                       // queries 4qg .. 4qg+3
+  const uint32_t cp = (uint32_t)lane;        // columns 2cp, 2cp+1
+  uint32_t glen[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) glen[u] = qlen[4 * qg + u];
+  const uint32_t lmin4 = glen[0], lmax4 = glen[3];  // prefixes grow with the query
+  float acc0[4], acc1[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) acc0[u] = acc1[u] = __uint_as_float(0u);
+
+  const uint32_t nvb = (lmax + VBLK - 1) / VBLK;
+  // cooperative V stage: 64 rows x 256 B = 1024 x 16 B, 4 per thread
+  auto vload = [&](uint32_t blk, u32x4_t r[4]) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t c = tid + 256 * u;  // 16-byte chunk
+      const uint32_t row = c >> 4, part = c & 15;
+      const uint32_t t = blk * VBLK + row;
+      r[u] = t < lmax ? *reinterpret_cast<const u32x4_t*>(vb + (uint64_t)t * D + part * 8)
+                      : u32x4_t{0u, 0u, 0u, 0u};
+    }
+  };
+  u32x4_t vr[4];
+  if (nvb > 0) vload(0, vr);
+  const uint32_t* vs32 = reinterpret_cast<const uint32_t*>(vstage);
+  for (uint32_t blk = 0; blk < nvb; ++blk) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      reinterpret_cast<u32x4_t*>(vstage)[tid + 256 * u] = vr[u];
+    __syncthreads();
+    if (blk + 1 < nvb) vload(blk + 1, vr);
+    const uint32_t tb = blk * VBLK;
+    const uint32_t rows = lmax - tb < (uint32_t)VBLK ? lmax - tb : (uint32_t)VBLK;
+    const uint32_t full = lmin4 > tb ? (lmin4 - tb < rows ? lmin4 - tb : rows) : 0u;
+    const uint32_t part = lmax4 > tb ? (lmax4 - tb < rows ? lmax4 - tb : rows) : 0u;
+    for (uint32_t r = 0; r < full; ++r) {
+      const uint32_t w = vs32[r * (D / 2) + cp];
+      const float v0 = bf16lo(w), v1 = bf16hi(w);
+      const float* prow = sT + (tb + r) * ST + 4 * qg;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float pu = prow[u];
+        const float x0 = pu * v0, x1 = pu * v1;
+        acc0[u] = acc0[u] + x0;
+        acc1[u] = acc1[u] + x1;
+      }
+    }
+    for (uint32_t r = full; r < part; ++r) {
+      const uint32_t t = tb + r;
+      const uint32_t w = vs32[r * (D / 2) + cp];
+      const float v0 = bf16lo(w), v1 = bf16hi(w);
+      const float* prow = sT + t * ST + 4 * qg;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (t < glen[u]) {
+          const float pu = prow[u];
+          const float x0 = pu * v0, x1 = pu * v1;
+          acc0[u] = acc0[u] + x0;
+          acc1[u] = acc1[u] + x1;
+        }
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const uint32_t qi = 4 * qg + u;
+    if (qi >= nq) continue;
+    const uint64_t off = (((uint64_t)b * Tq + t0 + qi) * H + h) * D + 2 * cp;
+    if (OUT_BF16)
+      *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(o) + off) = pack_bf16x2(acc0[u], acc1[u]);
+    else
+      *reinterpret_cast<float2*>(static_cast<float*>(o) + off) = make_float2(acc0[u], acc1[u]);
+  }
+}
+
+// grid = B * H * ceil(Tq / 16), block = 256, dynamic LDS =
+// 16*128*4 + 64*128*2 + 3*16*4 + Lmax*17*4 with Lmax >= min(max lens, L).
+extern "C" __global__ __launch_bounds__(256) void catena_attn_prefill_bf16_d128_f32out(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const uint32_t* __restrict__ lens, float* __restrict__ o, uint32_t B, uint32_t H, uint32_t L,
+    uint32_t Tq, float scale) {
+  prefill_body<false>(q, k, v, lens, o, B, H, L, Tq, scale);
+}
+
+extern "C" __global__ __launch_bounds__(256) void catena_attn_prefill_bf16_d128_bf16out(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const uint32_t* __restrict__ lens, uint16_t* __restrict__ o, uint32_t B, uint32_t H, uint32_t L,
+    uint32_t Tq, float scale) {
+  prefill_body<true>(q, k, v, lens, o, B, H, L, Tq, scale);
+}

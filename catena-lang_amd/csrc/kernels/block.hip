@@ -112,10 +112,13 @@ CATENA_DEV void rms_finish_row(const float* hs, uint32_t n, uint64_t row, float 
 }
 }  // namespace
 
+// With tokens given, the input row is the embedding gather
+// widen(table[tokens[src]]) (a token >= vocab gives NaN) instead of x[src].
 extern "C" __global__ __launch_bounds__(256) void catena_rmsnorm_rows(
     const float* __restrict__ x, const float* __restrict__ resid,
     const uint32_t* __restrict__ row_index, float* __restrict__ h_out,
-    float* __restrict__ y_f32, uint16_t* __restrict__ y_bf16, uint32_t n) {
+    float* __restrict__ y_f32, uint16_t* __restrict__ y_bf16, uint32_t n,
+    const uint32_t* __restrict__ tokens, const uint16_t* __restrict__ table, uint32_t vocab) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const uint32_t n_pad = (n + 3u) & ~3u;
   float* hs = reinterpret_cast<float*>(smem);  // [n_pad]
@@ -123,11 +126,29 @@ extern "C" __global__ __launch_bounds__(256) void catena_rmsnorm_rows(
   __shared__ float rms_s;
   const uint32_t row = blockIdx.x;
   const uint64_t src = row_index ? row_index[row] : row;
+  uint32_t tok = 0;
+  bool tok_ok = true;
+  if (tokens) {
+    tok = tokens[src];
+    tok_ok = tok < vocab;
+  }
+  const float nan = __uint_as_float(kNaNBits);
   if (n % 4 == 0) {
     const f32x4_t* x4 = reinterpret_cast<const f32x4_t*>(x + src * n);
     const f32x4_t* r4 = resid ? reinterpret_cast<const f32x4_t*>(resid + src * n) : nullptr;
+    const uint2* e4 = tokens ? reinterpret_cast<const uint2*>(table + (uint64_t)tok * n) : nullptr;
     for (uint32_t i = threadIdx.x; i < n / 4; i += 256) {
-      f32x4_t h = x4[i];
+      f32x4_t h;
+      if (tokens) {
+        if (tok_ok) {
+          const uint2 w = e4[i];
+          h = f32x4_t{bf16lo(w.x), bf16hi(w.x), bf16lo(w.y), bf16hi(w.y)};
+        } else {
+          h = f32x4_t{nan, nan, nan, nan};
+        }
+      } else {
+        h = x4[i];
+      }
       if (r4) {
         const f32x4_t rr = r4[i];
 #pragma unroll
@@ -142,7 +163,11 @@ extern "C" __global__ __launch_bounds__(256) void catena_rmsnorm_rows(
     }
   } else {
     for (uint32_t i = threadIdx.x; i < n; i += 256) {
-      float h = x[src * n + i];
+      float h;
+      if (tokens)
+        h = tok_ok ? bf16_to_f32(table[(uint64_t)tok * n + i]) : nan;
+      else
+        h = x[src * n + i];
       if (resid) h = h + resid[src * n + i];
       hs[i] = h;
       sq[i] = h * h;
@@ -215,17 +240,21 @@ extern "C" __global__ __launch_bounds__(256) void catena_rope_qkv_store(
   vc[cache + i + half] = (uint16_t)f32_to_bf16_bits(src[2 * HD + i + half]);
 }
 
-// SwiGLU gate: gu[R][2F] f32 (gate columns [0, F), up columns [F, 2F)) ->
-// out[R][F] = bf16(nn.silu(gate) * up).  4 elements per thread; requires
-// F % 4 == 0.  grid = (ceil(F / 1024), R).
+// SwiGLU gate: gu[R][2F] f32 -> out[R][F] = bf16(nn.silu(gate) * up).
+// group = 0: gate columns [0, F), up columns [F, 2F); group = G: columns
+// interleaved in groups of G (gate 0..G-1, up 0..G-1, gate G..2G-1, ...).
+// 4 elements per thread; requires F % 4 == 0 and G % 4 == 0.
+// grid = (ceil(F / 1024), R).
 extern "C" __global__ __launch_bounds__(256) void catena_silu_mul_bf16(
-    const float* __restrict__ gu, uint16_t* __restrict__ out, uint32_t F) {
+    const float* __restrict__ gu, uint16_t* __restrict__ out, uint32_t F, uint32_t group) {
   const uint32_t r = blockIdx.y;
   const uint32_t c = (blockIdx.x * 256 + threadIdx.x) * 4;
   if (c >= F) return;
   const float* row = gu + (uint64_t)r * 2 * F;
-  const f32x4_t g = *reinterpret_cast<const f32x4_t*>(row + c);
-  const f32x4_t u = *reinterpret_cast<const f32x4_t*>(row + F + c);
+  const uint32_t gcol = group ? (c / group) * 2 * group + c % group : c;
+  const uint32_t ucol = gcol + (group ? group : F);
+  const f32x4_t g = *reinterpret_cast<const f32x4_t*>(row + gcol);
+  const f32x4_t u = *reinterpret_cast<const f32x4_t*>(row + ucol);
   float a[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -243,25 +272,84 @@ extern "C" __global__ __launch_bounds__(256) void catena_silu_mul_bf16(
 // accumulator and is itself replaced by the next element, so the result is
 // the last NaN when it is the final element, else the first maximum of the
 // elements after the last NaN (FirstMax in common.h).  n = 0 writes
-// 0xFFFFFFFF (the reference asserts n != 0).  One workgroup per row.
+// 0xFFFFFFFF (the reference asserts n != 0).
+//
+// grid = (chunks, R): workgroup c covers [c*chunk, min(n, (c+1)*chunk)) and
+// reduces it to (J_c = last NaN index or -1, first max after J_c).  Chunks
+// compose in index order: a chunk holding a NaN replaces the state, one
+// without merges its first max into it.  The last workgroup of a row (by
+// completion ticket) composes the row's chunks in ascending order.
+// partials: R x chunks x {J, max bits, index}; tickets[R] start at zero.
 extern "C" __global__ __launch_bounds__(256) void catena_argmax_rows_f32(
-    const float* __restrict__ x, uint32_t* __restrict__ idx, uint32_t n) {
+    const float* __restrict__ x, uint32_t* __restrict__ idx, uint32_t n, uint32_t chunk,
+    uint32_t* __restrict__ tickets, uint32_t* __restrict__ partials) {
   __shared__ int red_i[4];
   __shared__ float red_v[4];
   __shared__ uint32_t red_u[4];
-  const uint32_t row = blockIdx.x;
+  __shared__ uint32_t last_flag;
+  const uint32_t row = blockIdx.y;
   const float* xr = x + (uint64_t)row * n;
   if (n == 0) {
-    if (threadIdx.x == 0) idx[row] = 0xFFFFFFFFu;
+    if (threadIdx.x == 0 && blockIdx.x == 0) idx[row] = 0xFFFFFFFFu;
     return;
   }
+  const uint32_t beg = blockIdx.x * chunk;
+  const uint32_t end = beg + chunk < n ? beg + chunk : n;
+  constexpr int PER = 16;  // elements per thread per batch
   int lastnan = -1;
-  for (uint32_t i = threadIdx.x; i < n; i += 256)
-    if (xr[i] != xr[i]) lastnan = (int)i;
+  for (uint32_t b0 = beg; b0 < end; b0 += 256 * PER) {
+    float v[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const uint32_t i = b0 + threadIdx.x + 256 * k;
+      v[k] = i < end ? xr[i] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const uint32_t i = b0 + threadIdx.x + 256 * k;
+      if (i < end && v[k] != v[k]) lastnan = (int)i;
+    }
+  }
   const int J = block_max_i32(lastnan, red_i);
   FirstMax fm{__uint_as_float(0xFF800000u), 0xFFFFFFFFu};
-  for (uint32_t i = threadIdx.x; i < n; i += 256)
-    if ((int)i > J) fm = first_max_combine(fm, FirstMax{xr[i], i});
-  const FirstMax all = block_first_max(fm, red_v, red_u);
-  if (threadIdx.x == 0) idx[row] = (J == (int)n - 1) ? (uint32_t)J : all.i;
+  for (uint32_t b0 = beg; b0 < end; b0 += 256 * PER) {
+    float v[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const uint32_t i = b0 + threadIdx.x + 256 * k;
+      v[k] = i < end ? xr[i] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const uint32_t i = b0 + threadIdx.x + 256 * k;
+      if (i < end && (int)i > J) fm = first_max_combine(fm, FirstMax{v[k], i});
+    }
+  }
+  const FirstMax part = block_first_max(fm, red_v, red_u);
+  const uint32_t chunks = gridDim.x;
+  if (chunks == 1) {
+    if (threadIdx.x == 0) idx[row] = (J == (int)n - 1) ? (uint32_t)J : part.i;
+    return;
+  }
+  uint32_t* pr = partials + 3ull * ((uint64_t)row * chunks);
+  if (threadIdx.x == 0) {
+    store_coherent(&pr[3 * blockIdx.x + 0], (uint32_t)J);
+    store_coherent(&pr[3 * blockIdx.x + 1], __float_as_uint(part.v));
+    store_coherent(&pr[3 * blockIdx.x + 2], part.i);
+  }
+  if (!last_arrival(&tickets[row], chunks, &last_flag)) return;
+  if (threadIdx.x != 0) return;
+  int sj = -1;
+  FirstMax st{__uint_as_float(0xFF800000u), 0xFFFFFFFFu};
+  for (uint32_t c = 0; c < chunks; ++c) {
+    const int jc = (int)load_coherent(&pr[3 * c]);
+    const FirstMax fc{__uint_as_float(load_coherent(&pr[3 * c + 1])), load_coherent(&pr[3 * c + 2])};
+    if (jc >= 0) {
+      sj = jc;
+      st = fc;
+    } else {
+      st = first_max_combine(st, fc);
+    }
+  }
+  idx[row] = (sj == (int)n - 1) ? (uint32_t)sj : st.i;
 }

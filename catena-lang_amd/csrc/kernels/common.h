@@ -174,8 +174,10 @@ CATENA_DEV float cos_full(float x) {
 }
 
 // The sequential left fold ((0 + s[0]) + s[1]) + ... over n floats in LDS
-// (16-byte aligned), by one lane: the next 32 values are read before the
-// current 32 are added, so LDS latency stays off the dependency chain.
+// (16-byte aligned), by one lane.  The next 32 values are requested before
+// the current 32 are added (the scheduling barrier keeps the compiler from
+// sinking those reads below the adds), so LDS latency stays off the
+// dependency chain.
 CATENA_DEV float serial_sum_lds(const float* s, uint32_t n) {
   typedef float f4 __attribute__((ext_vector_type(4)));
   float acc = __uint_as_float(0u);
@@ -190,6 +192,7 @@ CATENA_DEV float serial_sum_lds(const float* s, uint32_t n) {
       f4 nxt[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) nxt[u] = s4[i + u];
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         acc = acc + cur[u][0];
@@ -197,6 +200,7 @@ CATENA_DEV float serial_sum_lds(const float* s, uint32_t n) {
         acc = acc + cur[u][2];
         acc = acc + cur[u][3];
       }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
     }
@@ -217,6 +221,47 @@ CATENA_DEV float serial_sum_lds(const float* s, uint32_t n) {
   }
   for (uint32_t t = n4 * 4; t < n; ++t) acc = acc + s[t];
   return acc;
+}
+
+// Cross-workgroup partial results.  The XCDs' L2 caches are not coherent
+// with each other, so partials that another workgroup will read are stored
+// and loaded as agent-scope atomics (relaxed): those bypass the non-coherent
+// L2 state (write-through / coherent read) instead of writing back or
+// invalidating whole caches with agent-scope fences.
+CATENA_DEV void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+CATENA_DEV void store_coherent(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+CATENA_DEV float load_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+CATENA_DEV uint32_t load_coherent(const uint32_t* p) {
+  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Completion ticket shared by the workgroups of a group (e.g. the k-slices
+// of one output tile).  Each workgroup calls it once, with all its threads,
+// after writing its partials with store_coherent; it returns true in
+// exactly one of them, the last to arrive, which then reads every partial of
+// the group with load_coherent.  Each thread waits for its own stores to
+// complete before the barrier, so all of the workgroup's partials are in
+// place before thread 0 takes the ticket.  The last workgroup returns the
+// counter to zero, so counters need clearing only once, when allocated.
+// Which workgroup reduces depends on timing; what it computes does not.
+CATENA_DEV bool last_arrival(uint32_t* counter, uint32_t group_size, uint32_t* lds_flag) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t t =
+        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t last = t == group_size - 1 ? 1u : 0u;
+    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *lds_flag = last;
+  }
+  __syncthreads();
+  return *lds_flag != 0u;
 }
 
 // Exact parallel form of the f32.max-env fold (catena-lang/stdlib/

@@ -1,4 +1,5 @@
-// Decode-shape bf16 GEMM: Y[M x N] = X[M x K] * W[K x N] for M <= 16.
+// Decode-shape bf16 GEMM: Y[M x N] = X[M x K] * W[K x N] for M <= 16, with
+// optional fused epilogues for the decoder step.
 //
 // Same contraction as gemm_bf16.hip (catena-lang/stdlib/matrix.hex:236-327,
 // NN row-major, bf16 widened exactly, f32 accumulation) but shaped for the
@@ -10,23 +11,39 @@
 //   * a wave owns 128 consecutive columns and a contiguous chunk of KW k;
 //   * a workgroup holds 4 waves on 4 consecutive k chunks and adds their
 //     partials in ascending chunk order through LDS;
-//   * grid.y = number of such k groups (S).  S == 1 writes Y (bf16 or f32)
-//     directly; otherwise each workgroup writes an f32 partial P[s][m][n]
-//     and catena_gemm_bf16_decode_reduce adds them in ascending s.
-// No atomics; the addition order depends only on the shape, so results are
-// bitwise identical run to run.
+//   * grid.y = number of such k groups (S).  With S > 1 each workgroup
+//     stores an f32 partial P[s][m][n] and takes a completion ticket for its
+//     column block; the last of the S workgroups adds the S partials in
+//     ascending s.  The final M x 128 tile then goes through LDS to the
+//     epilogue.
+// The addition order depends only on the shape (the ticket decides which
+// workgroup adds, not how), so results are bitwise identical run to run.
+//
+// Epilogues (each also writes the f32 tile to Y unless EPI_STORE_BF16):
+//   EPI_STORE   Y f32;          EPI_STORE_BF16  Y bf16 (RNE)
+//   EPI_ROPE    fused q|k|v projection of one decode token per sequence:
+//               column block = one head of q, k or v; RoPE + bf16 q out and
+//               the K/V cache append, exactly as catena_rope_qkv_store
+//   EPI_SILU    SwiGLU with gate / up columns interleaved in groups of 64:
+//               act[m][64*bx + c] = bf16(silu(gate) * up), as catena_silu_mul_bf16
+//   EPI_ARGMAX  LM head: per row, (last NaN, first max) of the block's 128
+//               logits, then a second ticket over the column blocks; the
+//               last block composes them in column order: tensor.argmax-f32
+//               (catena-lang/stdlib/tensor.hex:204-227), as catena_argmax_rows_f32
 //
 // Lane mapping: lane l = 16*g + c.  For a k32 step at k0 the lane loads the
 // 8x8 bf16 block W[k0+8g .. k0+8g+7][n0+8c .. n0+8c+7] (8 x 16 B; per load
 // instruction the 16 lanes of a g read 256 contiguous bytes), transposes it
 // in registers, and feeds column n0+8c+j as the B operand of MFMA number j.
 // MFMA j's output column c therefore maps to global column n0 + 8c + j, so
-// each lane ends up holding 8 consecutive columns of 4 rows: stores are
-// 16-byte (bf16) / 32-byte (f32) runs.
+// each lane ends up holding 8 consecutive columns of 4 rows.
 #include "common.h"
 
 namespace {
 constexpr int COLS_PER_WAVE = 128;
+constexpr int TILE_LD = 132;  // f32 row stride of the LDS output tile
+
+enum Epi : int { EPI_STORE = 0, EPI_STORE_BF16 = 1, EPI_ROPE = 2, EPI_SILU = 3, EPI_ARGMAX = 4 };
 
 CATENA_DEV bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
 
@@ -54,13 +71,64 @@ CATENA_DEV void load_w(const uint16_t* __restrict__ W, uint64_t K, uint64_t N, u
       r[i] = u32x4_t{0u, 0u, 0u, 0u};
   }
 }
+
+CATENA_DEV int wave_max_i32(int v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const int o = __shfl_xor(v, off, 64);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+CATENA_DEV FirstMax wave_first_max(FirstMax a) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    FirstMax b;
+    b.v = __shfl_xor(a.v, off, 64);
+    b.i = (uint32_t)__shfl_xor((int)a.i, off, 64);
+    a = first_max_combine(a, b);
+  }
+  return a;
+}
+
+// Composition of argmax chunk summaries in index order: a chunk holding a
+// NaN replaces the state, one without merges its first max into it.
+struct ArgState {
+  int j;
+  FirstMax fm;
+};
+CATENA_DEV ArgState arg_compose(ArgState a, ArgState b) {
+  if (b.j >= 0) return b;
+  return ArgState{a.j, first_max_combine(a.fm, b.fm)};
+}
 }  // namespace
 
-// grid = (ceil(N/128), S), block = 256.  KW = k per wave (multiple of 32).
-extern "C" __global__ __launch_bounds__(256) void catena_gemm_bf16_decode(
-    const uint16_t* __restrict__ X, const uint16_t* __restrict__ W, void* __restrict__ Y,
-    float* __restrict__ P, uint32_t M, uint64_t N, uint64_t K, uint32_t KW, uint32_t out_f32) {
+// Extra operands of the fused epilogues (unused fields may be null).
+struct DecodeEpi {
+  // EPI_ROPE
+  uint16_t* q_out;          // [M][H*128] bf16
+  uint16_t* k_cache;        // [B][H][L][128]
+  uint16_t* v_cache;
+  const uint32_t* lens;     // [M] positions after the append
+  const float* inv_freq;    // [64]
+  uint32_t heads, max_len;
+  // EPI_SILU
+  uint16_t* act;            // [M][N/2] bf16
+  // EPI_ARGMAX
+  uint32_t* idx;            // [M]
+  uint32_t* arg_ticket;     // one counter, zero between launches
+  uint32_t* arg_partials;   // [M][gridDim.x][3]
+};
+
+template <int EPI>
+CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __restrict__ W,
+                            void* __restrict__ Y, float* __restrict__ P,
+                            uint32_t* __restrict__ tickets, uint32_t M, uint64_t N, uint64_t K,
+                            uint32_t KW, const DecodeEpi& ep) {
   __shared__ f32x4_t red[3][8][64];  // partials of waves 1..3
+  __shared__ float tile[16 * TILE_LD];
+  __shared__ uint32_t last_flag;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -104,57 +172,211 @@ extern "C" __global__ __launch_bounds__(256) void catena_gemm_bf16_decode(
     for (int j = 0; j < 8; ++j) red[wave - 1][j][lane] = acc[j];
   }
   __syncthreads();
-  if (wave != 0) return;
+  const uint32_t S = gridDim.y;
+  if (wave == 0) {
 #pragma unroll
-  for (int w = 0; w < 3; ++w)
+    for (int w = 0; w < 3; ++w)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      f32x4_t o = red[w][j][lane];
+      for (int j = 0; j < 8; ++j) {
+        f32x4_t o = red[w][j][lane];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) acc[j][q] = acc[j][q] + o[q];
+        for (int q = 0; q < 4; ++q) acc[j][q] = acc[j][q] + o[q];
+      }
+    // lane holds rows 4g+q, columns n0 + 8c + j (j = 0..7)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t row = 4 * g + q;
+      if (row >= M) continue;
+      if (S == 1) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) tile[row * TILE_LD + 8 * c + j] = acc[j][q];
+      } else if (col < N) {  // partial s of P, read by another workgroup
+        float* dst = P + ((uint64_t)blockIdx.y * M + row) * N + col;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) store_coherent(dst + j, acc[j][q]);
+      }
     }
-
-  // lane holds rows 4g+q, columns n0 + 8c + j (j = 0..7)
-  if (col >= N) return;
+  }
+  if (S > 1) {
+    if (!last_arrival(&tickets[blockIdx.x], S, &last_flag)) return;
+    // Last k group of this column block: P[0] + P[1] + ... + P[S-1],
+    // ascending s, for the block's M rows x 128 columns.
+    const uint64_t MN = (uint64_t)M * N;
+    for (uint32_t e = tid; e < M * 32u; e += 256) {
+      const uint32_t row = e >> 5, c4 = 4 * (e & 31u);
+      const uint64_t cc = n0 + c4;
+      f32x4_t sum = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      if (cc < N) {
+        const float* src = P + (uint64_t)row * N + cc;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const uint32_t row = 4 * g + q;
-    if (row >= M) continue;
-    if (gridDim.y == 1 && !out_f32) {
-      u32x4_t packed = u32x4_t{pack_bf16x2(acc[0][q], acc[1][q]), pack_bf16x2(acc[2][q], acc[3][q]),
-                               pack_bf16x2(acc[4][q], acc[5][q]), pack_bf16x2(acc[6][q], acc[7][q])};
-      *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(Y) + (uint64_t)row * N + col) = packed;
+        for (int q = 0; q < 4; ++q) sum[q] = load_coherent(src + q);
+        // partials 1..S-1 in batches of 8, every load of a batch issued
+        // before its adds
+        for (uint32_t s0 = 1; s0 < S; s0 += 8) {
+          f32x4_t part[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              part[u][q] = s0 + u < S ? load_coherent(src + (uint64_t)(s0 + u) * MN + q) : 0.0f;
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+            if (s0 + u < S)
+#pragma unroll
+              for (int q = 0; q < 4; ++q) sum[q] = sum[q] + part[u][q];
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) tile[row * TILE_LD + c4 + q] = sum[q];
+    }
+  }
+  __syncthreads();
+
+  // ---------------------------------------------------------------- epilogue
+  // tile[m][0..127] holds Y[m][n0 .. n0+127]
+  for (uint32_t e = tid; e < M * 32u; e += 256) {
+    const uint32_t row = e >> 5, c4 = 4 * (e & 31u);
+    const uint64_t cc = n0 + c4;
+    if (cc >= N) continue;
+    const float* t = tile + row * TILE_LD + c4;
+    if (EPI == EPI_STORE_BF16) {
+      uint2 o;
+      o.x = pack_bf16x2(t[0], t[1]);
+      o.y = pack_bf16x2(t[2], t[3]);
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(Y) + (uint64_t)row * N + cc) = o;
     } else {
-      // S == 1 with f32 output writes Y itself; otherwise partial s of P
-      float* dst = gridDim.y == 1 ? static_cast<float*>(Y) + (uint64_t)row * N + col
-                                  : P + ((uint64_t)blockIdx.y * M + row) * N + col;
-      *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{acc[0][q], acc[1][q], acc[2][q], acc[3][q]};
-      *reinterpret_cast<f32x4_t*>(dst + 4) = f32x4_t{acc[4][q], acc[5][q], acc[6][q], acc[7][q]};
+      *reinterpret_cast<f32x4_t*>(static_cast<float*>(Y) + (uint64_t)row * N + cc) =
+          f32x4_t{t[0], t[1], t[2], t[3]};
+    }
+  }
+
+  if (EPI == EPI_ROPE) {
+    // column block = (part, head): part 0 q, 1 k, 2 v; one token per row
+    const uint32_t H = ep.heads, L = ep.max_len;
+    const uint32_t part = blockIdx.x / H, head = blockIdx.x % H;
+    const uint64_t HD = (uint64_t)H * 128;
+    for (uint32_t e = tid; e < M * 64u; e += 256) {
+      const uint32_t r = e >> 6, i = e & 63u;
+      const uint32_t len = ep.lens[r];
+      const bool pos_ok = len >= 1 && len - 1 < L;
+      const uint32_t pos = pos_ok ? len - 1 : 0u;
+      const float* t = tile + r * TILE_LD;
+      const uint64_t cache = (((uint64_t)r * H + head) * L + pos) * 128;
+      if (part == 2) {
+        if (pos_ok) {
+          ep.v_cache[cache + i] = (uint16_t)f32_to_bf16_bits(t[i]);
+          ep.v_cache[cache + i + 64] = (uint16_t)f32_to_bf16_bits(t[i + 64]);
+        }
+        continue;
+      }
+      const float pf = (float)pos;
+      const float theta = pf * ep.inv_freq[i];
+      const float cs = cos_full(theta);
+      const float sn = sin_full(theta);
+      const float x1 = t[i], x2 = t[i + 64];
+      const float t1 = x1 * cs, t2 = x2 * sn, t3 = x2 * cs, t4 = x1 * sn;
+      const float y1 = t1 - t2, y2 = t3 + t4;
+      if (part == 0) {
+        uint16_t* dq = ep.q_out + (uint64_t)r * HD + (uint64_t)head * 128;
+        dq[i] = (uint16_t)f32_to_bf16_bits(y1);
+        dq[i + 64] = (uint16_t)f32_to_bf16_bits(y2);
+      } else if (pos_ok) {
+        ep.k_cache[cache + i] = (uint16_t)f32_to_bf16_bits(y1);
+        ep.k_cache[cache + i + 64] = (uint16_t)f32_to_bf16_bits(y2);
+      }
+    }
+  }
+
+  if (EPI == EPI_SILU) {
+    const uint64_t F = N / 2;
+    for (uint32_t e = tid; e < M * 64u; e += 256) {
+      const uint32_t r = e >> 6, cidx = e & 63u;
+      const float* t = tile + r * TILE_LD;
+      const float act = silu_approx(t[cidx]);
+      const float a = act * t[64 + cidx];
+      ep.act[(uint64_t)r * F + 64ull * blockIdx.x + cidx] = (uint16_t)f32_to_bf16_bits(a);
+    }
+  }
+
+  if (EPI == EPI_ARGMAX) {
+    const uint32_t gx = gridDim.x;
+    // this block's summary per row: columns n0 + lane, n0 + 64 + lane
+    for (uint32_t r = wave; r < M; r += 4) {
+      const float* t = tile + r * TILE_LD;
+      int lastnan = -1;
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const uint64_t cc = n0 + lane + 64 * h2;
+        if (cc < N && t[lane + 64 * h2] != t[lane + 64 * h2]) lastnan = (int)cc;
+      }
+      const int J = wave_max_i32(lastnan);
+      FirstMax fm{__uint_as_float(0xFF800000u), 0xFFFFFFFFu};
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const uint64_t cc = n0 + lane + 64 * h2;
+        if (cc < N && (int)cc > J) fm = first_max_combine(fm, FirstMax{t[lane + 64 * h2], (uint32_t)cc});
+      }
+      fm = wave_first_max(fm);
+      if (lane == 0) {
+        uint32_t* dst = ep.arg_partials + 3ull * ((uint64_t)r * gx + blockIdx.x);
+        store_coherent(dst + 0, (uint32_t)J);
+        store_coherent(dst + 1, __float_as_uint(fm.v));
+        store_coherent(dst + 2, fm.i);
+      }
+    }
+    if (!last_arrival(ep.arg_ticket, gx, &last_flag)) return;
+    // compose the gx chunk summaries of each row in column order: 16
+    // threads per row take contiguous runs, then one composes the 16 runs
+    __shared__ int run_j[16][16];
+    __shared__ float run_v[16][16];
+    __shared__ uint32_t run_i[16][16];
+    const uint32_t r = tid >> 4, sub = tid & 15u;
+    const uint32_t per = (gx + 15) / 16;
+    if (r < M) {
+      ArgState st{-1, FirstMax{__uint_as_float(0xFF800000u), 0xFFFFFFFFu}};
+      const uint32_t c0 = sub * per < gx ? sub * per : gx;
+      const uint32_t c1 = c0 + per < gx ? c0 + per : gx;
+      for (uint32_t cb = c0; cb < c1; cb += 8) {
+        uint32_t pj[8], pv[8], pi[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const bool live = cb + u < c1;
+          const uint32_t* src = ep.arg_partials + 3ull * ((uint64_t)r * gx + (live ? cb + u : c0));
+          pj[u] = live ? load_coherent(src) : 0xFFFFFFFFu;
+          pv[u] = live ? load_coherent(src + 1) : 0u;
+          pi[u] = live ? load_coherent(src + 2) : 0xFFFFFFFFu;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (cb + u < c1)
+            st = arg_compose(st, ArgState{(int)pj[u], FirstMax{__uint_as_float(pv[u]), pi[u]}});
+      }
+      run_j[r][sub] = st.j;
+      run_v[r][sub] = st.fm.v;
+      run_i[r][sub] = st.fm.i;
+    }
+    __syncthreads();
+    if (r < M && sub == 0) {
+      ArgState st{-1, FirstMax{__uint_as_float(0xFF800000u), 0xFFFFFFFFu}};
+      for (int s2 = 0; s2 < 16; ++s2)
+        st = arg_compose(st, ArgState{run_j[r][s2], FirstMax{run_v[r][s2], run_i[r][s2]}});
+      ep.idx[r] = (st.j == (int)N - 1) ? (uint32_t)st.j : st.fm.i;
     }
   }
 }
 
-// Y[m][n] = P[0][m][n] + P[1][m][n] + ... + P[S-1][m][n], ascending s, then
-// bf16 (RNE) unless out_f32.
-extern "C" __global__ __launch_bounds__(256) void catena_gemm_bf16_decode_reduce(
-    const float* __restrict__ P, void* __restrict__ Y, uint32_t M, uint64_t N, uint32_t S,
-    uint32_t out_f32) {
-  const uint64_t idx = (uint64_t)blockIdx.x * 256 + threadIdx.x;  // over M*N/4
-  const uint64_t total = (uint64_t)M * N / 4;
-  if (idx >= total) return;
-  const f32x4_t* p4 = reinterpret_cast<const f32x4_t*>(P);
-  f32x4_t acc = p4[idx];
-  for (uint32_t s = 1; s < S; ++s) {
-    f32x4_t v = p4[(uint64_t)s * total + idx];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) acc[q] = acc[q] + v[q];
+// grid = (ceil(N/128), S), block = 256.  KW = k per wave (multiple of 32).
+// tickets[ceil(N/128)] start at zero and are left at zero.
+#define CATENA_DECODE_KERNEL(NAME, EPI)                                                          \
+  extern "C" __global__ __launch_bounds__(256) void NAME(                                        \
+      const uint16_t* __restrict__ X, const uint16_t* __restrict__ W, void* __restrict__ Y,     \
+      float* __restrict__ P, uint32_t* __restrict__ tickets, uint32_t M, uint64_t N, uint64_t K, \
+      uint32_t KW, DecodeEpi ep) {                                                               \
+    decode_body<EPI>(X, W, Y, P, tickets, M, N, K, KW, ep);                                      \
   }
-  if (out_f32) {
-    reinterpret_cast<f32x4_t*>(Y)[idx] = acc;
-    return;
-  }
-  uint2 out;
-  out.x = pack_bf16x2(acc[0], acc[1]);
-  out.y = pack_bf16x2(acc[2], acc[3]);
-  reinterpret_cast<uint2*>(Y)[idx] = out;
-}
+
+CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_f32out, EPI_STORE)
+CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_bf16out, EPI_STORE_BF16)
+CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_rope, EPI_ROPE)
+CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_silu, EPI_SILU)
+CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_argmax, EPI_ARGMAX)

@@ -78,8 +78,29 @@ extern "C" __global__ __launch_bounds__(256) void catena_softmax_rows_f32(
   }
   __syncthreads();
   if (tid == 0) {
+    // den = (((0 + e_0) + e_1) + ...), ascending; the next 32 values are
+    // requested before the current 32 are added
     float den = __uint_as_float(0u);
-    for (uint64_t t = 0; t < n; ++t) den = den + yr[t];
+    uint64_t t = 0;
+    if (n >= 64) {
+      float cur[32];
+#pragma unroll
+      for (int u = 0; u < 32; ++u) cur[u] = yr[u];
+      for (t = 32; t + 32 <= n; t += 32) {
+        float nxt[32];
+#pragma unroll
+        for (int u = 0; u < 32; ++u) nxt[u] = yr[t + u];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 32; ++u) den = den + cur[u];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 32; ++u) cur[u] = nxt[u];
+      }
+#pragma unroll
+      for (int u = 0; u < 32; ++u) den = den + cur[u];
+    }
+    for (; t < n; ++t) den = den + yr[t];
     den_s = den;
   }
   __syncthreads();

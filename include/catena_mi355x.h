@@ -186,9 +186,13 @@ int catena_mi355x_rope_qkv_bf16(const float *qkv, const float *inv_freq, const u
                                 uint32_t batch, uint32_t tq, uint32_t heads, uint32_t head_dim,
                                 uint32_t max_len);
 
-/* SwiGLU gate: gu[rows][2F] f32 (gate | up) -> out[rows][F] =
- * bf16(nn.silu(gate) * up) (catena-lang/stdlib/nn.hex:1-21).  F % 4 == 0. */
-int catena_mi355x_silu_mul_bf16(const float *gu, uint16_t *out, uint64_t rows, uint32_t ffn);
+/* SwiGLU gate: gu[rows][2F] f32 -> out[rows][F] = bf16(nn.silu(gate) * up)
+ * (catena-lang/stdlib/nn.hex:1-21).  group = 0: columns gate | up; group =
+ * G: gate and up interleaved in groups of G columns (gate 0..G-1, up
+ * 0..G-1, gate G..2G-1, ...), the decoder's W_gu layout (G = 64).
+ * F % 4 == 0, G % 4 == 0, F % G == 0.  No reference counterpart. */
+int catena_mi355x_silu_mul_bf16(const float *gu, uint16_t *out, uint64_t rows, uint32_t ffn,
+                                uint32_t group);
 
 /* tensor.argmax-f32 per row (catena-lang/stdlib/tensor.hex:204-227):
  * idx[r] = first index of the maximum with the reference's NaN behaviour;
@@ -243,8 +247,9 @@ void program_tensor_argmax_f32(catena_mem_t x, uint64_t *out);
  *   gu  = hn * W_gu (f32);   a = bf16(silu(gate) * up);  x' = h + a * W_down.
  * Then bf16(rmsnorm(x)) of each sequence's last row times W_lm gives f32
  * logits and greedy argmax the next token.  Weights bf16, row-major NN:
- * W_qkv[d][3d], W_o[d][d], W_gu[d][2F], W_down[F][d], W_lm[d][vocab];
- * embedding[vocab][d]. */
+ * W_qkv[d][3d] (columns q heads | k heads | v heads), W_o[d][d],
+ * W_gu[d][2F] (gate and up columns interleaved in groups of 64),
+ * W_down[F][d], W_lm[d][vocab]; embedding[vocab][d]. */
 typedef struct catena_decoder catena_decoder_t;
 typedef struct catena_decoder_config {
   uint32_t d_model;  /* = n_heads * head_dim */
@@ -262,7 +267,7 @@ typedef enum catena_decoder_tensor {
   CATENA_DEC_EMBED = 0, /* [vocab][d] bf16 */
   CATENA_DEC_W_QKV,     /* per layer [d][3d] bf16 */
   CATENA_DEC_W_O,       /* per layer [d][d] bf16 */
-  CATENA_DEC_W_GU,      /* per layer [d][2F] bf16 */
+  CATENA_DEC_W_GU,      /* per layer [d][2F] bf16, gate / up interleaved by 64 */
   CATENA_DEC_W_DOWN,    /* per layer [F][d] bf16 */
   CATENA_DEC_W_LM,      /* [d][vocab] bf16 */
   CATENA_DEC_K_CACHE,   /* per layer [max_batch][H][max_len][D] bf16 */
@@ -278,7 +283,7 @@ typedef enum catena_decoder_tensor {
   CATENA_DEC_ATTN_PROJ, /* [rows][d] f32 */
   CATENA_DEC_H,         /* [rows][d] f32 */
   CATENA_DEC_HN,        /* [rows][d] bf16 */
-  CATENA_DEC_GU,        /* [rows][2F] f32 */
+  CATENA_DEC_GU,        /* [rows][2F] f32, gate / up interleaved by 64 */
   CATENA_DEC_ACT,       /* [rows][F] bf16 */
   CATENA_DEC_FFN_OUT,   /* [rows][d] f32 */
   CATENA_DEC_FINAL_H,   /* [batch][d] f32: residual stream at the last rows */

@@ -18,7 +18,8 @@ Stage definitions (one IEEE op per node, operands in this order):
                          reduction with the quadrant advanced by one
   attn_causal:           query tq of sequence b = decode attention over the
                          first lens[b] - (Tq - 1 - tq) cache rows
-  silu_mul_bf16:         bf16(nn.silu(g) * u)   (catena-lang/stdlib/nn.hex:1-21)
+  silu_mul_bf16:         bf16(nn.silu(g) * u)   (catena-lang/stdlib/nn.hex:1-21);
+                         the decoder's W_gu interleaves gate / up by 64 columns
   argmax:                tensor.argmax-f32 (catena-lang/stdlib/tensor.hex:204-227)
 """
 from __future__ import annotations
@@ -36,9 +37,15 @@ def residual_rmsnorm_bf16(x, r=None):
     return h, f32_to_bf16_bits_np(rmsnorm_f32(h))
 
 
-def silu_mul_bf16(gu, ffn: int):
+def silu_mul_bf16(gu, ffn: int, group: int = 0):
+    """group = 0: columns gate | up; group = G: interleaved in groups of G."""
     gu = np.ascontiguousarray(gu, np.float32)
-    g, u = gu[:, :ffn], gu[:, ffn:]
+    if group:
+        blocks = gu.reshape(gu.shape[0], ffn // group, 2, group)
+        g = np.ascontiguousarray(blocks[:, :, 0, :].reshape(gu.shape[0], ffn))
+        u = np.ascontiguousarray(blocks[:, :, 1, :].reshape(gu.shape[0], ffn))
+    else:
+        g, u = gu[:, :ffn], gu[:, ffn:]
     f = lib().or_silu
     s = np.array([f(float(v)) for v in g.ravel()], np.float32).reshape(g.shape)
     return f32_to_bf16_bits_np((s * u).astype(np.float32))
@@ -85,8 +92,8 @@ def gemm(a16, b16):
 class DecoderOracle:
     """Whole-model sequential forward (all GEMMs in the reference's k order).
     Weights are host arrays of bf16 bits laid out as the library's
-    (w_qkv [L][d][3d], w_o [L][d][d], w_gu [L][d][2F], w_down [L][F][d],
-    embed [V][d], w_lm [d][V])."""
+    (w_qkv [L][d][3d], w_o [L][d][d], w_gu [L][d][2F] with gate / up
+    interleaved by 64 columns, w_down [L][F][d], embed [V][d], w_lm [d][V])."""
 
     def __init__(self, weights: dict, n_heads: int, head_dim: int, ffn: int, max_len: int,
                  rope_base: float = 10000.0):
@@ -121,7 +128,7 @@ class DecoderOracle:
             ap, _ = gemm(f32_to_bf16_bits_np(o), self.w["w_o"][l])
             h, hn = residual_rmsnorm_bf16(x, ap)
             gu, _ = gemm(hn, self.w["w_gu"][l])
-            act = silu_mul_bf16(gu, F)
+            act = silu_mul_bf16(gu, F, 64)
             ffn_out, _ = gemm(act, self.w["w_down"][l])
         last = np.arange(batch) * tq + (tq - 1)
         _, fxn = residual_rmsnorm_bf16(h[last], ffn_out[last])

@@ -157,15 +157,16 @@ def test_rope_large_positions_against_libm():
     assert np.abs(q - want).max() < 2e-4 + 2 ** -7 * np.abs(want).max()
 
 
-@pytest.mark.parametrize("rows,F", [(3, 1024), (8, 5632), (1, 4)])
-def test_silu_mul(rows, F):
-    rng = np.random.default_rng(F)
+@pytest.mark.parametrize("rows,F,group", [(3, 1024, 0), (8, 5632, 0), (1, 4, 0), (8, 5632, 64),
+                                           (2, 256, 4)])
+def test_silu_mul(rows, F, group):
+    rng = np.random.default_rng(F + group)
     gu = (rng.standard_normal((rows, 2 * F)) * 4).astype(np.float32)
     gu[0, :4] = [0.0, -0.0, 100.0, -100.0]
     out = ca.Buffer(rows * F * 2)
-    say(f"silu_mul rows={rows} F={F}")
-    ca.silu_mul_bf16(ca.Buffer.from_array(gu), out, rows, F)
-    _bitwise(out.read(np.uint16, (rows, F)), od.silu_mul_bf16(gu, F))
+    say(f"silu_mul rows={rows} F={F} group={group}")
+    ca.silu_mul_bf16(ca.Buffer.from_array(gu), out, rows, F, group)
+    _bitwise(out.read(np.uint16, (rows, F)), od.silu_mul_bf16(gu, F, group))
 
 
 def _argmax_rows(rows):
@@ -265,3 +266,54 @@ def test_programs_rmsnorm_and_argmax():
     say("runtime exec tensor.argmax-f32")
     [res] = rt.exec("tensor.argmax-f32", [rt.mem_f32([1.0, 3.0, 3.0, 2.0])], 1)
     assert res.get() == 1  # first index of the tie (catena-lang/tests/runtime.rs:1176-1197)
+
+
+def test_argmax_chunked_nan_and_tie_patterns():
+    """Rows long enough to span several workgroups (4096 elements each):
+    NaNs and ties placed on and across chunk boundaries."""
+    n = 3 * 4096 + 17
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal((7, n)).astype(np.float32)
+    x[0, 4095] = np.nan                      # NaN at a chunk's last element
+    x[1, 4096] = np.nan                      # ... at a chunk's first element
+    x[1, 100] = 99.0                         # maximum before the NaN is ignored
+    x[2, n - 1] = np.nan                     # final NaN is the answer
+    x[3, [10, 5000, 9000]] = 77.0            # tie across chunks: first wins
+    x[4, 8192:] = np.nan                     # NaN run to the end
+    x[5, 3] = np.nan
+    x[5, 12000] = np.nan
+    x[5, [12001, 12100]] = 40.0              # tie after the last NaN
+    x[6, :] = -np.inf
+    idx = ca.Buffer(7 * 4)
+    say("argmax chunked patterns")
+    ca.argmax_f32(ca.Buffer.from_array(x), idx, 7, n)
+    assert list(idx.read(np.uint32)) == [oracle.argmax_f32(r) for r in x]
+    # the same rows again: the completion counters were returned to zero
+    ca.argmax_f32(ca.Buffer.from_array(x), idx, 7, n)
+    assert list(idx.read(np.uint32)) == [oracle.argmax_f32(r) for r in x]
+
+
+@pytest.mark.parametrize("B,Tq,H,L,lens", [(2, 37, 3, 200, [200, 37]), (1, 512, 2, 640, [512]),
+                                           (3, 8, 2, 96, [96, 8, 30]), (2, 100, 1, 700, [700, 120])])
+def test_attention_prefill_kernel_equals_per_query_kernel(monkeypatch, B, Tq, H, L, lens):
+    """The 16-query-block kernel against the one-query-per-workgroup kernel
+    (same bits by construction), including cached prefixes (lens > Tq),
+    partial last blocks and sequences shorter than Tq."""
+    D = 128
+    q, k, v = _attn_inputs(B, Tq, H, L, B * 7 + Tq)
+    lb = ca.Buffer.from_array(np.array(lens, np.uint32))
+    scale = 1.0 / math.sqrt(D)
+    a32, b32 = ca.Buffer(B * Tq * H * D * 4), ca.Buffer(B * Tq * H * D * 4)
+    a16, b16 = ca.Buffer(B * Tq * H * D * 2), ca.Buffer(B * Tq * H * D * 2)
+    say(f"prefill attention B={B} Tq={Tq} H={H} L={L} lens={lens}")
+    ca.attn_causal_bf16(q, k, v, lb, a32, B, Tq, H, L, D, scale, out_f32=True)
+    ca.attn_causal_bf16(q, k, v, lb, a16, B, Tq, H, L, D, scale, out_f32=False)
+    monkeypatch.setenv("CATENA_ATTN_PREFILL", "0")
+    ca.attn_causal_bf16(q, k, v, lb, b32, B, Tq, H, L, D, scale, out_f32=True)
+    ca.attn_causal_bf16(q, k, v, lb, b16, B, Tq, H, L, D, scale, out_f32=False)
+    assert np.array_equal(a32.read(np.uint32), b32.read(np.uint32))
+    assert np.array_equal(a16.read(np.uint16), b16.read(np.uint16))
+    if B * Tq * H <= 4096:
+        want = od.attn_causal(q.read(np.uint16), k.read(np.uint16, (B, H, L, D)),
+                              v.read(np.uint16, (B, H, L, D)), lens, B, Tq, H, D, scale)
+        _bitwise(a32.read(np.float32, (B * Tq, H * D)), want)

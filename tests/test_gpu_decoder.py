@@ -91,7 +91,7 @@ def _check_forward(dec, cfg, w, tokens, tq, cache_len):
     GU = rd(ca.DEC_GU, np.float32, (R, 2 * F))
     gemm_within_bound(HN, w["w_gu"][0], GU)
     ACT = rd(ca.DEC_ACT, np.uint16, (R, F))
-    _bitwise(ACT, od.silu_mul_bf16(GU, F))
+    _bitwise(ACT, od.silu_mul_bf16(GU, F, 64))
     FO = rd(ca.DEC_FFN_OUT, np.float32, (R, d))
     gemm_within_bound(ACT, w["w_down"][0], FO)
     last = np.arange(B) * tq + (tq - 1)

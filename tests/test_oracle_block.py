@@ -110,3 +110,16 @@ def test_rope():
         n0 = x1 ** 2 + x2 ** 2
         n1 = y[:64] ** 2 + y[64:] ** 2
         assert np.abs(n1 - n0).max() < 1e-4 * (1 + n0.max())
+
+
+def test_silu_mul_group_layout():
+    """The interleaved layout is a permutation of the gate | up layout."""
+    from oracle import decoder as od
+    rng = np.random.default_rng(4)
+    F, G = 256, 64
+    g = rng.standard_normal((3, F)).astype(np.float32)
+    u = rng.standard_normal((3, F)).astype(np.float32)
+    halves = np.concatenate([g, u], axis=1)
+    inter = np.concatenate([np.concatenate([g[:, i:i + G], u[:, i:i + G]], axis=1)
+                            for i in range(0, F, G)], axis=1)
+    assert np.array_equal(od.silu_mul_bf16(halves, F), od.silu_mul_bf16(inter, F, G))
