@@ -78,7 +78,7 @@ extern "C" __global__ __launch_bounds__(256) void catena_embed_rows_bf16(
 
 // One workgroup per output row.  h = x[src] (+ resid[src] when resid is
 // given: one f32 add per element); then nn.rmsnorm of h:
-//   sum_sq = fold_{i asc} from +0 of h_i * h_i   (one lane, over LDS)
+//   sum_sq = fold_{i asc} from +0 of h_i * h_i   (one wave, serial_sum_wave)
 //   rms    = math.sqrt(sum_sq / (f32)n + 0x3727C5AC)
 //   y_i    = h_i / rms
 // src = row_index ? row_index[row] : row.  Outputs (each optional): h_out
@@ -175,13 +175,15 @@ extern "C" __global__ __launch_bounds__(256) void catena_rmsnorm_rows(
     }
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const float sum_sq = serial_sum_lds(sq, n);
-    const float len_f = (float)(uint64_t)n;
-    const float mean_sq = sum_sq / len_f;
-    const float eps = u32_as_f32(0x3727C5ACu);
-    const float t = mean_sq + eps;
-    rms_s = sqrt_newton(t);
+  if (threadIdx.x < 64) {
+    const float sum_sq = serial_sum_wave(sq, n);
+    if (threadIdx.x == 0) {
+      const float len_f = (float)(uint64_t)n;
+      const float mean_sq = sum_sq / len_f;
+      const float eps = u32_as_f32(0x3727C5ACu);
+      const float t = mean_sq + eps;
+      rms_s = sqrt_newton(t);
+    }
   }
   __syncthreads();
   rms_finish_row(hs, n, row, rms_s, y_f32, y_bf16);

@@ -223,6 +223,58 @@ CATENA_DEV float serial_sum_lds(const float* s, uint32_t n) {
   return acc;
 }
 
+// The same sequential fold computed by one whole wave (all 64 lanes call
+// it; every lane gets the result).  Each 2048-value chunk is spread over
+// the lanes, lane L holding values 32L .. 32L+31 in registers; the running
+// sum then passes from lane to lane through a scalar register while the lane
+// owning the next 32 values adds them in order with the others masked off.
+// The dependency chain is one v_add_f32 per value with no memory access on
+// it (a single lane reading LDS per value is several times slower).
+CATENA_DEV float serial_sum_wave(const float* s, uint32_t n) {
+  const uint32_t lane = threadIdx.x & 63u;
+  float acc = __uint_as_float(0u);
+  for (uint32_t base = 0; base < n; base += 2048) {
+    const uint32_t cnt = n - base < 2048u ? n - base : 2048u;
+    const uint32_t lo = base + 32 * lane;
+    float v[32];
+    if (lo + 32 <= n && (reinterpret_cast<uintptr_t>(s + lo) & 15u) == 0) {
+      typedef float f4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const f4 e = *reinterpret_cast<const f4*>(s + lo + 4 * i);
+        v[4 * i + 0] = e[0];
+        v[4 * i + 1] = e[1];
+        v[4 * i + 2] = e[2];
+        v[4 * i + 3] = e[3];
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 32; ++k) v[k] = lo + k < n ? s[lo + k] : 0.0f;
+    }
+    // every load has landed before the chain starts, so no wait sits in it
+    __builtin_amdgcn_s_waitcnt(0);
+    const uint32_t full = cnt / 32, rem = cnt % 32;
+    for (uint32_t L = 0; L < full; ++L) {
+      float a = acc;
+      if (lane == L) {
+#pragma unroll
+        for (int k = 0; k < 32; ++k) a = a + v[k];
+      }
+      acc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), (int)L));
+    }
+    if (rem) {
+      float a = acc;
+      if (lane == full) {
+#pragma unroll
+        for (int k = 0; k < 32; ++k)
+          if ((uint32_t)k < rem) a = a + v[k];
+      }
+      acc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), (int)full));
+    }
+  }
+  return acc;
+}
+
 // Cross-workgroup partial results.  The XCDs' L2 caches are not coherent
 // with each other, so partials that another workgroup will read are stored
 // and loaded as agent-scope atomics (relaxed): those bypass the non-coherent

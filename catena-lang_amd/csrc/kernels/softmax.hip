@@ -8,8 +8,9 @@
 // The reference runs both folds serially on the host (the entry is host-only
 // because it contains a materialize).  Here one workgroup per row computes
 // the max with the exact parallel form of the fold (FirstMax, common.h),
-// writes exp~ values to the output, folds the denominator in one lane in
-// ascending order, and divides in place -- bitwise the sequential result.
+// writes exp~ values to the output, folds the denominator in ascending order
+// as one lane-to-lane chain in wave 0 (serial_sum_wave), and divides in
+// place -- bitwise the sequential result.
 #include "common.h"
 
 namespace {
@@ -77,31 +78,10 @@ extern "C" __global__ __launch_bounds__(256) void catena_softmax_rows_f32(
     yr[t] = exp_approx(shifted);
   }
   __syncthreads();
-  if (tid == 0) {
-    // den = (((0 + e_0) + e_1) + ...), ascending; the next 32 values are
-    // requested before the current 32 are added
-    float den = __uint_as_float(0u);
-    uint64_t t = 0;
-    if (n >= 64) {
-      float cur[32];
-#pragma unroll
-      for (int u = 0; u < 32; ++u) cur[u] = yr[u];
-      for (t = 32; t + 32 <= n; t += 32) {
-        float nxt[32];
-#pragma unroll
-        for (int u = 0; u < 32; ++u) nxt[u] = yr[t + u];
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int u = 0; u < 32; ++u) den = den + cur[u];
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int u = 0; u < 32; ++u) cur[u] = nxt[u];
-      }
-#pragma unroll
-      for (int u = 0; u < 32; ++u) den = den + cur[u];
-    }
-    for (; t < n; ++t) den = den + yr[t];
-    den_s = den;
+  if (tid < 64) {
+    // den = (((0 + e_0) + e_1) + ...), ascending, as one lane-to-lane chain
+    const float den = serial_sum_wave(yr, (uint32_t)n);
+    if (tid == 0) den_s = den;
   }
   __syncthreads();
   const float den = den_s;

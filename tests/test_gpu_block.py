@@ -41,7 +41,8 @@ def _rows(rows, n, seed, scale=1.0):
     return (rng.standard_normal((rows, n)) * scale).astype(np.float32)
 
 
-@pytest.mark.parametrize("rows,n", [(1, 6), (3, 2048), (2, 4097), (5, 5632), (1, 1), (4, 12)])
+@pytest.mark.parametrize("rows,n", [(1, 6), (3, 2048), (2, 4097), (5, 5632), (1, 1), (4, 12),
+                                    (2, 31), (2, 33), (3, 2049), (1, 6143), (1, 20000)])
 def test_rmsnorm_f32(rows, n):
     say(f"rmsnorm rows={rows} n={n}")
     x = _rows(rows, n, rows * 31 + n, scale=3.0)
