@@ -42,18 +42,33 @@ const GemmVariant kGemmVariants[] = {
 constexpr int kGemmVariantCount = sizeof(kGemmVariants) / sizeof(kGemmVariants[0]);
 constexpr int kGemmDefaultVariant = 7;
 
-// k per wave for the decode kernel: aim for ~1500 waves in flight (1024
-// SIMDs on MI355X), in whole 32-k MFMA steps.  CATENA_DECODE_KW overrides.
-uint32_t decode_kw(uint64_t n_cols, uint64_t k) {
+// k per wave for the decode kernel, in whole 32-k MFMA steps.
+// Streaming path (K % 32 == 0, one 4-wave workgroup per CU for its 144 KiB
+// LDS ring; each wave keeps 36 KiB in flight): the fewest k groups that
+// still give every CU a workgroup, so one round of workgroups streams the
+// weight and few partials are added, but no fewer than 8 steps per wave
+// (measured on the decoder's and the C3 shapes).  Register path: ~1500 waves.
+// CATENA_DECODE_KW overrides.
+uint32_t decode_kw(uint64_t n_cols, uint64_t k, int cu_count, bool regs_path) {
   const char* env = getenv("CATENA_DECODE_KW");
   if (env && *env) {
     long v = strtol(env, nullptr, 10);
     if (v >= 32 && v % 32 == 0) return (uint32_t)v;
   }
   const uint64_t blocks = ceil_div(n_cols, 128);
-  uint64_t kw = ceil_div(k * blocks, 1536);
-  kw = ceil_div(kw, 32) * 32;
-  if (kw < 64) kw = 64;
+  uint64_t kw;
+  if (!regs_path) {
+    // at least 8 steps of 32 k per wave: shorter chunks pay the ring's fill
+    // and the partials' reduction more often than they gain in spread
+    uint64_t groups = blocks >= (uint64_t)cu_count ? 1 : (uint64_t)cu_count / blocks;
+    kw = ceil_div(k, 4 * groups);
+    kw = ceil_div(kw, 32) * 32;
+    if (kw < 256) kw = 256;
+  } else {
+    kw = ceil_div(k * blocks, 1536);
+    kw = ceil_div(kw, 32) * 32;
+    if (kw < 64) kw = 64;
+  }
   if (kw > k) kw = ceil_div(k, 32) * 32;
   return (uint32_t)kw;
 }
@@ -71,7 +86,9 @@ int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, 
     return fail(CATENA_ERR_INVALID_ARGUMENT, "decode GEMM shape or alignment");
   Device& d = device();
   const uint32_t M = (uint32_t)n;
-  const uint32_t kw = decode_kw(m, k);
+  const char* dpath = getenv("CATENA_DECODE_PATH");
+  const bool regs_path = k % 32 != 0 || (dpath && strcmp(dpath, "regs") == 0);
+  const uint32_t kw = decode_kw(m, k, d.cu_count > 0 ? d.cu_count : 256, regs_path);
   const uint64_t chunks = ceil_div(k, kw);
   const uint64_t S = ceil_div(chunks, 4);
   const uint64_t gx = ceil_div(m, 128);
@@ -114,8 +131,15 @@ int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, 
   void* Y = c;
   uint64_t N = m, K = k;
   uint32_t* tickets = d.gemm_tickets();
-  void* args[] = {&X, &W, &Y, &P, &tickets, (void*)&M, &N, &K, (void*)&kw, &e};
-  return launch(id, dim3((unsigned)gx, (unsigned)S), dim3(256), 0, args);
+  // streaming ring (4 waves x 4 stages x 9 KiB) when K % 32 == 0, else the
+  // reduction buffers only (3 x 8 KiB partials + the 16 x 132 f32 tile);
+  // CATENA_DECODE_PATH=regs selects the register path for comparison
+  const char* path = getenv("CATENA_DECODE_PATH");
+  uint32_t stream_lds = (k % 32 == 0 && !(path && strcmp(path, "regs") == 0)) ? 1u : 0u;
+  const size_t lds = stream_lds ? 4 * 4 * 9216 : 3 * 8 * 64 * 16 + 16 * 132 * 4;
+  void* args[] = {&X, &W, &Y, &P, &tickets, (void*)&M, &N, &K, (void*)&kw, &stream_lds, &e};
+  if (lds > d.max_lds) return fail(CATENA_ERR_UNSUPPORTED, "decode GEMM needs %zu B of LDS", lds);
+  return launch(id, dim3((unsigned)gx, (unsigned)S), dim3(256), lds, args);
 }
 
 }  // namespace catena

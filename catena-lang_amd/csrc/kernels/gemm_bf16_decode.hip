@@ -31,12 +31,13 @@
 //               last block composes them in column order: tensor.argmax-f32
 //               (catena-lang/stdlib/tensor.hex:204-227), as catena_argmax_rows_f32
 //
-// Lane mapping: lane l = 16*g + c.  For a k32 step at k0 the lane loads the
-// 8x8 bf16 block W[k0+8g .. k0+8g+7][n0+8c .. n0+8c+7] (8 x 16 B; per load
-// instruction the 16 lanes of a g read 256 contiguous bytes), transposes it
-// in registers, and feeds column n0+8c+j as the B operand of MFMA number j.
-// MFMA j's output column c therefore maps to global column n0 + 8c + j, so
-// each lane ends up holding 8 consecutive columns of 4 rows.
+// Streaming (K % 32 == 0): each wave runs a private 4-deep LDS ring of
+// [32 k][128 cols] W slabs and [16][32] X slabs filled with direct
+// global->LDS loads (nothing held in registers while in flight, so 36 KiB
+// per wave are in flight), and reads B fragments with the transposing LDS
+// read (no register transpose).  Otherwise (K % 32 != 0): lane l = 16*g + c
+// loads the 8x8 block W[k0+8g ..][n0+8c ..] into registers, transposes it
+// and feeds column n0+8c+j to MFMA j.
 #include "common.h"
 
 namespace {
@@ -92,6 +93,31 @@ CATENA_DEV FirstMax wave_first_max(FirstMax a) {
   return a;
 }
 
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
+
+// LDS ring of the streaming path: per wave RING stages, each a W slab
+// [32 k][128 cols] (8 KiB, 256-byte rows) and an X slab [16 rows][32 k]
+// (1 KiB).  16-byte chunk p of W row r holds global chunk p ^ hW(r), which
+// makes the transposing fragment reads (16 rows x 32 bytes per
+// instruction) hit every bank pair once.
+constexpr int RING = 4;
+constexpr int W_SLAB = 32 * 128 * 2;
+constexpr int STAGE_BYTES = W_SLAB + 1024;
+constexpr int WAVE_RING = RING * STAGE_BYTES;
+CATENA_DEV uint32_t hW(uint32_t r) { return 2u * ((r & 3u) | (((r >> 3) & 1u) << 2)); }
+
+CATENA_DEV bf16x8_t cat_bf16(i16x4_t lo, i16x4_t hi) {
+  typedef short i16x8_t __attribute__((ext_vector_type(8)));
+  i16x8_t v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+// s_waitcnt on vmcnt only (gfx9 encoding: vmcnt[3:0], vmcnt[5:4] at 15:14)
+#define DEC_WAIT_VMCNT(n) \
+  __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | 0x0070 | 0x0F00)
+
 // Composition of argmax chunk summaries in index order: a chunk holding a
 // NaN replaces the state, one without merges its first max into it.
 struct ArgState {
@@ -125,10 +151,14 @@ template <int EPI>
 CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __restrict__ W,
                             void* __restrict__ Y, float* __restrict__ P,
                             uint32_t* __restrict__ tickets, uint32_t M, uint64_t N, uint64_t K,
-                            uint32_t KW, const DecodeEpi& ep) {
-  __shared__ f32x4_t red[3][8][64];  // partials of waves 1..3
-  __shared__ float tile[16 * TILE_LD];
+                            uint32_t KW, uint32_t stream_lds, const DecodeEpi& ep) {
+  // Dynamic LDS: the streaming ring, reused after the k loop for the
+  // partials of waves 1..3 (red[3][8][64]) and the output tile.
+  extern __shared__ __attribute__((aligned(1024))) unsigned char dsm[];
+  f32x4_t(*red)[8][64] = reinterpret_cast<f32x4_t(*)[8][64]>(dsm);
+  float* tile = reinterpret_cast<float*>(dsm + 3 * 8 * 64 * 16);
   __shared__ uint32_t last_flag;
+  const bool streamed = stream_lds != 0;  // host: only when K % 32 == 0
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -143,29 +173,112 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int xrow = lane & 15;
-  const bool xlive = xrow < (int)M;
-  if (kbeg < kend) {
-    u32x4_t cur[8], nxt[8];
-    load_w(W, K, N, kbeg, col, g, cur);
-    for (uint64_t k0 = kbeg; k0 < kend; k0 += 32) {
-      const bool more = k0 + 32 < kend;
-      if (more) load_w(W, K, N, k0 + 32, col, g, nxt);
-      const uint64_t xk = k0 + 8 * g;
-      u32x4_t xa = u32x4_t{0u, 0u, 0u, 0u};
-      if (xlive && xk < K) xa = *reinterpret_cast<const u32x4_t*>(X + (uint64_t)xrow * K + xk);
-      u32x4_t bt[8];
-      transpose8x8(cur, bt);
-      const bf16x8_t af = as_bf16x8(xa);
+  if (streamed) {
+    // Streaming path: W and X slabs go global -> LDS (global_load_lds, no
+    // registers held by loads in flight) through this wave's RING-deep
+    // ring; B fragments are read with the transposing LDS read, so lane
+    // (G, s) of MFMA block j gets W[k0 + 8G .. +7][n0 + 16j + s].  Output:
+    // lane (G, s) holds rows 4G .. 4G+3 of column n0 + 16j + s.
+    unsigned char* ring = dsm + wave * WAVE_RING;
+    const uint32_t steps = kbeg < kend ? (uint32_t)((kend - kbeg) / 32) : 0u;
+    // per-lane global byte offsets of the 8 W instructions (4 rows each)
+    uint32_t woff[8];
+    bool wlive[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t r = 4 * i + (lane >> 4);
+      const uint32_t q = (uint32_t)(lane & 15) ^ hW(r);
+      woff[i] = (uint32_t)(((uint64_t)r * N + 8 * q) * 2);
+      wlive[i] = n0 + 8 * q < N;
+    }
+    // X slab: lane l fetches row l / 4, 16-byte chunk l % 4
+    const uint32_t xr = lane >> 2, xq = lane & 3;
+    const bool xl = xr < M;
+    const char* wsrc = reinterpret_cast<const char*>(W) + (kbeg * N + n0) * 2;
+    const char* xsrc = reinterpret_cast<const char*>(X) + ((uint64_t)xr * K + kbeg + 8 * xq) * 2;
+    auto issue = [&](uint32_t t, int slot) {
+      unsigned char* st = ring + slot * STAGE_BYTES;
+      const char* w = wsrc + (uint64_t)t * 32 * N * 2;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (wlive[i]) __builtin_amdgcn_global_load_lds(w + woff[i], (lds_void*)(st + 1024 * i), 16, 0, 0);
+      if (xl) __builtin_amdgcn_global_load_lds(xsrc + (uint64_t)t * 64, (lds_void*)(st + W_SLAB), 16, 0, 0);
+    };
+    const uint32_t pre = steps < (uint32_t)RING ? steps : (uint32_t)RING;
+    for (uint32_t t = 0; t < pre; ++t) issue(t, (int)t);
+    // fragment read addresses inside a stage
+    const int G = lane >> 4, sl = lane & 15;
+    const uint32_t xa_off = W_SLAB + ((uint32_t)sl * 4 + (uint32_t)G) * 16;
+    const uint32_t brow = 8 * G + (sl >> 2);
+    const uint32_t hb = hW(brow);
+    uint32_t b_off[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t colq = 16 * j + 4 * (sl & 3);
+      b_off[j] = brow * 256 + 16 * ((colq >> 3) ^ hb) + 2 * (colq & 7);
+    }
+    for (uint32_t t = 0; t < steps; ++t) {
+      const int slot = (int)(t % RING);
+      const uint32_t later = steps - 1 - t < (uint32_t)(RING - 1) ? steps - 1 - t : (uint32_t)(RING - 1);
+      // every instruction of stage t has landed; the later stages may not
+      // have (9 instructions per stage, fewer when lanes are masked, which
+      // only makes the wait stricter)
+      if (later >= 3) {
+        DEC_WAIT_VMCNT(27);
+      } else if (later == 2) {
+        DEC_WAIT_VMCNT(18);
+      } else if (later == 1) {
+        DEC_WAIT_VMCNT(9);
+      } else {
+        DEC_WAIT_VMCNT(0);
+      }
+      asm volatile("" ::: "memory");
+      const unsigned char* st = ring + slot * STAGE_BYTES;
+      const bf16x8_t af = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(st + xa_off));
+      bf16x8_t bf[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const unsigned char* pb = st + b_off[j];
+        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(pb));
+        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(pb + 4 * 256));
+        bf[j] = cat_bf16(lo, hi);
+      }
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, as_bf16x8(bt[j]), acc[j], 0, 0, 0);
-      if (more) {
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bf[j], acc[j], 0, 0, 0);
+      if (t + RING < steps) {
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this slot's reads are done
+        asm volatile("" ::: "memory");
+        issue(t + RING, slot);
+      }
+    }
+  } else {
+    const int xrow = lane & 15;
+    const bool xlive = xrow < (int)M;
+    if (kbeg < kend) {
+      u32x4_t cur[8], nxt[8];
+      load_w(W, K, N, kbeg, col, g, cur);
+      for (uint64_t k0 = kbeg; k0 < kend; k0 += 32) {
+        const bool more = k0 + 32 < kend;
+        if (more) load_w(W, K, N, k0 + 32, col, g, nxt);
+        const uint64_t xk = k0 + 8 * g;
+        u32x4_t xa = u32x4_t{0u, 0u, 0u, 0u};
+        if (xlive && xk < K) xa = *reinterpret_cast<const u32x4_t*>(X + (uint64_t)xrow * K + xk);
+        u32x4_t bt[8];
+        transpose8x8(cur, bt);
+        const bf16x8_t af = as_bf16x8(xa);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
+        for (int j = 0; j < 8; ++j)
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, as_bf16x8(bt[j]), acc[j], 0, 0, 0);
+        if (more) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
+        }
       }
     }
   }
+  // the streaming path's LDS is reused below
+  __syncthreads();
 
   if (wave > 0) {
 #pragma unroll
@@ -182,18 +295,20 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
 #pragma unroll
         for (int q = 0; q < 4; ++q) acc[j][q] = acc[j][q] + o[q];
       }
-    // lane holds rows 4g+q, columns n0 + 8c + j (j = 0..7)
+    // lane holds rows 4g+q of tile column tc(j): 16j + c when streamed,
+    // else 8c + j
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const uint32_t row = 4 * g + q;
       if (row >= M) continue;
-      if (S == 1) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) tile[row * TILE_LD + 8 * c + j] = acc[j][q];
-      } else if (col < N) {  // partial s of P, read by another workgroup
-        float* dst = P + ((uint64_t)blockIdx.y * M + row) * N + col;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) store_coherent(dst + j, acc[j][q]);
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t tc = streamed ? 16 * j + c : 8 * c + j;
+        if (S == 1) {
+          tile[row * TILE_LD + tc] = acc[j][q];
+        } else if (n0 + tc < N) {  // partial s of P, read by another workgroup
+          store_coherent(P + ((uint64_t)blockIdx.y * M + row) * N + n0 + tc, acc[j][q]);
+        }
       }
     }
   }
@@ -371,8 +486,8 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
   extern "C" __global__ __launch_bounds__(256) void NAME(                                        \
       const uint16_t* __restrict__ X, const uint16_t* __restrict__ W, void* __restrict__ Y,     \
       float* __restrict__ P, uint32_t* __restrict__ tickets, uint32_t M, uint64_t N, uint64_t K, \
-      uint32_t KW, DecodeEpi ep) {                                                               \
-    decode_body<EPI>(X, W, Y, P, tickets, M, N, K, KW, ep);                                      \
+      uint32_t KW, uint32_t stream_lds, DecodeEpi ep) {                                          \
+    decode_body<EPI>(X, W, Y, P, tickets, M, N, K, KW, stream_lds, ep);                          \
   }
 
 CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_f32out, EPI_STORE)

@@ -160,3 +160,20 @@ def test_program_bf16_matmul():
     # small integers: every partial sum is exact, so any order gives the oracle's bits
     assert np.array_equal(got, oracle.matmul_bf16(a16, b16)[1])
     ca.mem_free(res.get())
+
+
+def test_decode_register_path(monkeypatch):
+    """The register-transpose decode path (used when K % 32 != 0), forced on
+    an aligned shape: same contract (bound, f32/bf16 consistency, run to run)."""
+    monkeypatch.setenv("CATENA_DECODE_PATH", "regs")
+    mrows, n, k = 16, 4096, 2048
+    say(f"bf16 decode gemm register path M={mrows} N={n} K={k}")
+    a, b, a16, b16 = _inputs(mrows, n, k, seed=91, wscale=0.02)
+    c16, c32 = ca.Buffer(mrows * n * 2), ca.Buffer(mrows * n * 4)
+    ca.gemm_bf16(a, b, c16, mrows, n, k)
+    ca.gemm_bf16(a, b, c32, mrows, n, k, out_f32=True)
+    g16, g32 = c16.read(np.uint16, (mrows, n)), c32.read(np.float32, (mrows, n))
+    assert np.array_equal(g16, oracle.f32_to_bf16_bits_np(g32))
+    _check(a16, b16, g32, g16)
+    ca.gemm_bf16(a, b, c16, mrows, n, k)
+    assert np.array_equal(c16.read(np.uint16, (mrows, n)), g16)
