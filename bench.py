@@ -254,7 +254,9 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["gemm", "all"], default="all")
+    ap.add_argument("--only", choices=["gemm", "core", "decoder", "all"], default="all",
+                    help="gemm: the headline GEMM only; core: + decode attention and decode "
+                         "GEMMs; decoder: + the C5 decoder only; all: everything")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also launch the plain copy kernel on 1 GiB (known traffic) three "
                          "times, for scaling FETCH_SIZE / WRITE_SIZE counter readings")
@@ -270,16 +272,17 @@ def main(argv=None) -> int:
     print("[bench] bf16 GEMM 4096^3", file=sys.stderr, flush=True)
     g = bench_gemm(args.steps, args.warmup, ev)
     extra = {}
-    if args.only == "all":
+    core = args.only in ("core", "all")
+    if args.only in ("decoder", "all"):
+        print("[bench] decoder block C5 (prefill 8x512, 128 greedy steps)", file=sys.stderr,
+              flush=True)
+        extra["decoder_c5"] = bench_decoder(3, ev)
+    if core:
         print("[bench] decode attention B32 H32 L4096 D128", file=sys.stderr, flush=True)
         at = bench_attention(max(5, args.steps // 5), max(2, args.warmup // 5), ev)
         print("[bench] decode GEMMs M=16", file=sys.stderr, flush=True)
         dg = bench_decode_gemm(max(20, args.steps), args.warmup, ev)
-        print("[bench] decoder block C5 (prefill 8x512, 128 greedy steps)", file=sys.stderr,
-              flush=True)
-        dc = bench_decoder(3, ev)
-        extra = {
-            "decoder_c5": dc,
+        extra.update({
             "decode_attention": {
                 "workload": "B=32 H=32 D=128 L=4096 bf16 KV, f32 softmax/out, bitwise vs sequential oracle",
                 "us_per_launch": at["us"], "GB/s": at["GB/s"], "bitwise_run_to_run": at["bitwise_run_to_run"],
@@ -288,7 +291,7 @@ def main(argv=None) -> int:
                              "traffic": measured_traffic("catena_attn_decode_bf16_d128_kc")},
                 "bytes_per_launch": at["bytes_per_launch"]},
             "decode_gemm_m16": dg,
-        }
+        })
     if args.copy_calibration:
         nbytes = 1 << 30
         src, dst = ca.Buffer(nbytes), ca.Buffer(nbytes)
@@ -304,7 +307,7 @@ def main(argv=None) -> int:
         print(f"[bench] cpu baseline ({threads} threads)", file=sys.stderr, flush=True)
         a, b = g["inputs"]
         cpu = cpu_baseline_gemm(a, b, rows=4096, threads=threads)
-        if args.only == "all":
+        if core:
             q, k, v = at["inputs"]
             extra["decode_attention"]["cpu_baseline"] = cpu_baseline_attention(q, k, v, 1024, threads)
 
