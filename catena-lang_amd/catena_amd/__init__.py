@@ -134,6 +134,23 @@ SIGNATURES = {
     "catena_mi355x_rope_qkv_bf16": (_int, [_vp] * 6 + [_u32] * 5),
     "catena_mi355x_silu_mul_bf16": (_int, [_vp, _vp, _u64, _u32, _u32]),
     "catena_mi355x_argmax_f32": (_int, [_vp, _vp, _u64, _u64]),
+    "catena_mi355x_broadcast_f32": (_int, [_vp, _u64, _f32]),
+    "catena_mi355x_arange_f32": (_int, [_vp, _u64]),
+    "catena_mi355x_copy_f32": (_int, [_vp, _vp, _u64]),
+    "catena_mi355x_sum_f32": (_int, [_vp, _vp, _u64, _u64]),
+    "catena_mi355x_mean_f32": (_int, [_vp, _vp, _u64, _u64]),
+    "catena_mi355x_max_f32": (_int, [_vp, _vp, _u64, _u64]),
+    "catena_mi355x_sum_u64": (_int, [_vp, _vp, _u64, _u64]),
+    "catena_mi355x_dot_u64": (_int, [_vp, _vp, _vp, _u64, _u64]),
+    "program_tensor_broadcast_f32": (None, [_f32, _u64, ctypes.POINTER(Mem)]),
+    "program_tensor_arange_f32": (None, [_u64, ctypes.POINTER(Mem)]),
+    "program_tensor_slice_f32": (None, [Mem, _u64, _u64, ctypes.POINTER(Mem)]),
+    "program_tensor_concat_f32": (None, [Mem, Mem, ctypes.POINTER(Mem)]),
+    "program_sum_f32": (None, [Mem, ctypes.POINTER(_f32)]),
+    "program_mean_f32": (None, [Mem, ctypes.POINTER(_f32)]),
+    "program_max_f32": (None, [Mem, ctypes.POINTER(_f32)]),
+    "program_sum_u64": (None, [Mem, ctypes.POINTER(_u64)]),
+    "program_dot_u64": (None, [Mem, Mem, ctypes.POINTER(_u64)]),
     "program_nn_rmsnorm": (None, [Mem, ctypes.POINTER(Mem)]),
     "program_tensor_argmax_f32": (None, [Mem, ctypes.POINTER(_u64)]),
     "catena_mi355x_decoder_create": (_int, [_vp, ctypes.POINTER(_vp)]),
@@ -334,6 +351,38 @@ def silu_mul_bf16(gu, out, rows: int, ffn: int, group: int = 0) -> None:
 
 def argmax_f32(x, idx, rows: int, n: int) -> None:
     check(lib().catena_mi355x_argmax_f32(_p(x), _p(idx), rows, n))
+
+
+def broadcast_f32(out, n: int, value: float) -> None:
+    check(lib().catena_mi355x_broadcast_f32(_p(out), n, value))
+
+
+def arange_f32(out, n: int) -> None:
+    check(lib().catena_mi355x_arange_f32(_p(out), n))
+
+
+def copy_f32(dst, src, n: int) -> None:
+    check(lib().catena_mi355x_copy_f32(_p(dst), _p(src), n))
+
+
+def sum_f32(x, out, rows: int, n: int) -> None:
+    check(lib().catena_mi355x_sum_f32(_p(x), _p(out), rows, n))
+
+
+def mean_f32(x, out, rows: int, n: int) -> None:
+    check(lib().catena_mi355x_mean_f32(_p(x), _p(out), rows, n))
+
+
+def max_f32(x, out, rows: int, n: int) -> None:
+    check(lib().catena_mi355x_max_f32(_p(x), _p(out), rows, n))
+
+
+def sum_u64(x, out, rows: int, n: int) -> None:
+    check(lib().catena_mi355x_sum_u64(_p(x), _p(out), rows, n))
+
+
+def dot_u64(a, b, out, rows: int, n: int) -> None:
+    check(lib().catena_mi355x_dot_u64(_p(a), _p(b), _p(out), rows, n))
 
 
 # ------------------------------------------------------------------ decoder

@@ -90,6 +90,12 @@ const KernelSpec kKernels[] = {
     {KernelId::RopeQkvStore, "block", "catena_rope_qkv_store"},
     {KernelId::SiluMulBf16, "block", "catena_silu_mul_bf16"},
     {KernelId::ArgmaxRowsF32, "block", "catena_argmax_rows_f32"},
+    {KernelId::BroadcastF32, "tensor", "catena_broadcast_f32"},
+    {KernelId::ArangeF32, "tensor", "catena_arange_f32"},
+    {KernelId::CopyF32, "tensor", "catena_copy_f32"},
+    {KernelId::SumRowsF32, "tensor", "catena_sum_rows_f32"},
+    {KernelId::MaxRowsF32, "tensor", "catena_max_rows_f32"},
+    {KernelId::SumRowsU64, "tensor", "catena_sum_rows_u64"},
     {KernelId::SoftmaxRows, "softmax", "catena_softmax_rows_f32"},
     {KernelId::ExpApprox, "softmax", "catena_exp_approx_f32"},
     {KernelId::FillNormalBf16, "fill", "catena_fill_normal_bf16"},

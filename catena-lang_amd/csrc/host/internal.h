@@ -50,6 +50,12 @@ enum class KernelId : int {
   RopeQkvStore,
   SiluMulBf16,
   ArgmaxRowsF32,
+  BroadcastF32,
+  ArangeF32,
+  CopyF32,
+  SumRowsF32,
+  MaxRowsF32,
+  SumRowsU64,
   SoftmaxRows,
   ExpApprox,
   FillNormalBf16,

@@ -7,10 +7,10 @@
 // The reference compiles every source program to generated C++; this build
 // has no front end (out of scope) and instead binds source programs BY NAME
 // to native lowerings, checking the kinds of the declared type against the
-// lowering's signature.  The hot-path stdlib programs (nn.softmax,
-// math.exp-approx, nn.rmsnorm, tensor.argmax-f32) and this build's new
-// programs are built in; user sources declare the rest (e.g.
-// matmul-2x2-via-mem).
+// lowering's signature.  The stdlib programs on and around the hot path
+// (nn.softmax, math.exp-approx, nn.rmsnorm, tensor.*, sum-f32, mean-f32,
+// max-f32) and this build's new programs are built in; user sources declare
+// the rest (e.g. matmul-2x2-via-mem, sum-u64, dot-u64).
 #include <cctype>
 #include <cstring>
 #include <memory>
@@ -94,6 +94,60 @@ void inv_argmax(const catena_value_t* in, catena_value_t* out) {
   out[0].as.u64 = r;
 }
 
+void inv_broadcast(const catena_value_t* in, catena_value_t* out) {
+  catena_mem_t r;
+  program_tensor_broadcast_f32(in[0].as.f32, in[1].as.u64, &r);
+  out[0] = mem_value(r);
+}
+void inv_arange(const catena_value_t* in, catena_value_t* out) {
+  catena_mem_t r;
+  program_tensor_arange_f32(in[0].as.u64, &r);
+  out[0] = mem_value(r);
+}
+void inv_slice(const catena_value_t* in, catena_value_t* out) {
+  catena_mem_t r;
+  program_tensor_slice_f32(in[0].as.mem, in[1].as.u64, in[2].as.u64, &r);
+  out[0] = mem_value(r);
+}
+void inv_concat(const catena_value_t* in, catena_value_t* out) {
+  catena_mem_t r;
+  program_tensor_concat_f32(in[0].as.mem, in[1].as.mem, &r);
+  out[0] = mem_value(r);
+}
+void set_f32(catena_value_t* out, float v) {
+  out[0].kind = kF32;
+  out[0].as.f32 = v;
+}
+void set_u64(catena_value_t* out, uint64_t v) {
+  out[0].kind = kU64;
+  out[0].as.u64 = v;
+}
+void inv_sum_f32(const catena_value_t* in, catena_value_t* out) {
+  float r;
+  program_sum_f32(in[0].as.mem, &r);
+  set_f32(out, r);
+}
+void inv_mean_f32(const catena_value_t* in, catena_value_t* out) {
+  float r;
+  program_mean_f32(in[0].as.mem, &r);
+  set_f32(out, r);
+}
+void inv_max_f32(const catena_value_t* in, catena_value_t* out) {
+  float r;
+  program_max_f32(in[0].as.mem, &r);
+  set_f32(out, r);
+}
+void inv_sum_u64(const catena_value_t* in, catena_value_t* out) {
+  uint64_t r;
+  program_sum_u64(in[0].as.mem, &r);
+  set_u64(out, r);
+}
+void inv_dot_u64(const catena_value_t* in, catena_value_t* out) {
+  uint64_t r;
+  program_dot_u64(in[0].as.mem, in[1].as.mem, &r);
+  set_u64(out, r);
+}
+
 const std::vector<Lowering>& lowerings() {
   static const std::vector<Lowering> t = {
       {"matmul-2x2-via-mem", false, {kMem, kMem, kU64, kU64, kU64, kU64, kU64, kU64}, {kMem},
@@ -104,6 +158,15 @@ const std::vector<Lowering>& lowerings() {
       {"math.exp-approx", true, {kF32}, {kF32}, inv_exp},
       {"nn.rmsnorm", true, {kMem}, {kMem}, inv_rmsnorm},
       {"tensor.argmax-f32", true, {kMem}, {kU64}, inv_argmax},
+      {"tensor.broadcast-f32", true, {kF32, kU64}, {kMem}, inv_broadcast},
+      {"tensor.arange-f32", true, {kU64}, {kMem}, inv_arange},
+      {"tensor.slice-f32", true, {kMem, kU64, kU64}, {kMem}, inv_slice},
+      {"tensor.concat-f32", true, {kMem, kMem}, {kMem}, inv_concat},
+      {"sum-f32", true, {kMem}, {kF32}, inv_sum_f32},
+      {"mean-f32", true, {kMem}, {kF32}, inv_mean_f32},
+      {"max-f32", true, {kMem}, {kF32}, inv_max_f32},
+      {"sum-u64", false, {kMem}, {kU64}, inv_sum_u64},
+      {"dot-u64", false, {kMem, kMem}, {kU64}, inv_dot_u64},
       {"bf16.matmul.row-major.via-mem", true,
        {kMem, kMem, kU64, kU64, kU64, kU64, kU64, kU64}, {kMem}, inv_bf16_matmul},
       {"attn.decode.via-mem", true, {kMem, kMem, kMem, kMem, kU64, kU64, kU64, kU64, kF32}, {kMem},

@@ -199,6 +199,28 @@ int catena_mi355x_silu_mul_bf16(const float *gu, uint16_t *out, uint64_t rows, u
  * n = 0 gives 0xFFFFFFFF (the reference asserts n != 0). */
 int catena_mi355x_argmax_f32(const float *x, uint32_t *idx, uint64_t rows, uint64_t n);
 
+/* -- buffer producers and folds (materializec / reducec programs) -- */
+
+/* tensor.broadcast-f32 body (catena-lang/stdlib/tensor.hex:1-21): out[i] = value. */
+int catena_mi355x_broadcast_f32(float *out, uint64_t n, float value);
+/* tensor.arange-f32 body (catena-lang/stdlib/tensor.hex:23-46): out[i] =
+ * u64.to-f32(i), round to nearest even. */
+int catena_mi355x_arange_f32(float *out, uint64_t n);
+/* Element copy behind tensor.slice-f32 / tensor.concat-f32
+ * (catena-lang/stdlib/tensor.hex:48-168); any 4-byte alignment. */
+int catena_mi355x_copy_f32(float *dst, const float *src, uint64_t n);
+/* sum-f32 / mean-f32 / max-f32 per row (catena-lang/stdlib/sum.hex:29-101):
+ * the reference's sequential folds (sum from +0, max-env from -inf),
+ * bitwise.  n < 2^32 (max: n < 2^31). */
+int catena_mi355x_sum_f32(const float *x, float *out, uint64_t rows, uint64_t n);
+int catena_mi355x_mean_f32(const float *x, float *out, uint64_t rows, uint64_t n);
+int catena_mi355x_max_f32(const float *x, float *out, uint64_t rows, uint64_t n);
+/* sum-u64 / dot-u64 per row (catena-lang/tests/cases/reducec/basic.hex):
+ * wrapping u64 arithmetic. */
+int catena_mi355x_sum_u64(const uint64_t *x, uint64_t *out, uint64_t rows, uint64_t n);
+int catena_mi355x_dot_u64(const uint64_t *a, const uint64_t *b, uint64_t *out, uint64_t rows,
+                          uint64_t n);
+
 /* ------------------------------------------------------------------ */
 /* program ABI (generated-module symbols; synchronous; fail-stop)        */
 
@@ -236,6 +258,22 @@ void program_nn_rmsnorm(catena_mem_t x, catena_mem_t *out);
 /* catena-lang/stdlib/tensor.hex:204-227 "tensor.argmax-f32": (mem) -> (u64);
  * traps on an empty input like the reference's u64.assert-nz. */
 void program_tensor_argmax_f32(catena_mem_t x, uint64_t *out);
+
+/* catena-lang/stdlib/tensor.hex producers: (f32 value, u64 len) -> (mem);
+ * (u64 len) -> (mem); (mem, u64 start, u64 len) -> (mem), trapping unless
+ * start + len <= len(input); (mem, mem) -> (mem). */
+void program_tensor_broadcast_f32(float value, uint64_t len, catena_mem_t *out);
+void program_tensor_arange_f32(uint64_t len, catena_mem_t *out);
+void program_tensor_slice_f32(catena_mem_t input, uint64_t start, uint64_t len, catena_mem_t *out);
+void program_tensor_concat_f32(catena_mem_t a, catena_mem_t b, catena_mem_t *out);
+/* catena-lang/stdlib/sum.hex folds: (mem) -> (f32). */
+void program_sum_f32(catena_mem_t x, float *out);
+void program_mean_f32(catena_mem_t x, float *out);
+void program_max_f32(catena_mem_t x, float *out);
+/* catena-lang/tests/cases/reducec/basic.hex: (mem) -> (u64); (mem, mem) ->
+ * (u64), trapping unless the lengths are equal. */
+void program_sum_u64(catena_mem_t x, uint64_t *out);
+void program_dot_u64(catena_mem_t a, catena_mem_t b, uint64_t *out);
 
 /* ------------------------------------------------------------------ */
 /* decoder (Llama-style blocks composed from the ops above)              */

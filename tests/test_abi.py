@@ -35,7 +35,7 @@ def test_library_exports_every_header_symbol():
 def test_code_objects_present_and_gfx950():
     objdump = "/opt/rocm/llvm/bin/llvm-readelf"
     for name in ["gemm_f32_exact", "gemm_bf16", "gemm_bf16_lds", "gemm_bf16_deep", "gemm_bf16_decode",
-                 "attn_decode", "block", "softmax", "fill"]:
+                 "attn_decode", "attn_prefill", "block", "tensor", "softmax", "fill"]:
         path = os.path.join(ca.LIB_DIR, name + ".co")
         assert os.path.exists(path), path
         if os.path.exists(objdump):
@@ -67,7 +67,7 @@ def test_attention_fma_only_inside_division():
     the correctly rounded f32 division sequence (v_div_scale / v_rcp / fma
     refinement / v_div_fmas / v_div_fixup): every function with a float FMA
     also has a v_div_fixup_f32, and the count of FMAs per division is fixed."""
-    for name in ["attn_decode", "softmax", "block"]:
+    for name in ["attn_decode", "attn_prefill", "softmax", "block", "tensor"]:
         text = _disasm(name)
         fmas = len(FLOAT_FMA.findall(text))
         fixups = len(re.findall(r"\bv_div_fixup_f32\b", text))
@@ -96,6 +96,11 @@ def test_runtime_parses_and_lists_programs():
     assert "matmul-2x2-via-mem" in names
     assert "nn.softmax" in names and "math.exp-approx" in names
     assert "nn.rmsnorm" in names and "tensor.argmax-f32" in names
+    for stdlib in ["tensor.broadcast-f32", "tensor.arange-f32", "tensor.slice-f32",
+                   "tensor.concat-f32", "sum-f32", "mean-f32", "max-f32"]:
+        assert stdlib in names
+    # test programs of the reference (not stdlib) are bound only when declared
+    assert "sum-u64" not in names and "dot-u64" not in names
     # identity programs are not declared, so they are not executable
     assert "matmul-right-identity-2x2-via-mem" not in names
 
