@@ -34,6 +34,8 @@ enum class KernelId : int {
   GemmBf16DeepF32,
   GemmBf16DeepFrontBf16,
   GemmBf16DeepFrontF32,
+  GemmBf16K32Bf16,  // four 32-k stages, spread buffer loads, LDS-staged epilogue (default)
+  GemmBf16K32F32,
   GemmBf16DecodeF32,
   GemmBf16DecodeBf16,
   GemmBf16DecodeRope,

@@ -38,9 +38,15 @@ const GemmVariant kGemmVariants[] = {
     {KernelId::GemmBf16LdsV7Bf16, KernelId::GemmBf16LdsV7F32, 64},
     /* 8 v6 with reads front-loaded 1:1 */
     {KernelId::GemmBf16DeepFrontBf16, KernelId::GemmBf16DeepFrontF32, 128},
+    /* 9 four 32-k stages through buffer loads spread over the MFMAs, LDS-staged
+       bf16 epilogue (gemm_bf16_k32.hip) */
+    {KernelId::GemmBf16K32Bf16, KernelId::GemmBf16K32F32, 128},
 };
 constexpr int kGemmVariantCount = sizeof(kGemmVariants) / sizeof(kGemmVariants[0]);
-constexpr int kGemmDefaultVariant = 7;
+// Default: variant 9 when K % 128 == 0 (and its 32-bit buffer offsets hold),
+// else variant 7.
+constexpr int kGemmDefaultVariant = 9;
+constexpr int kGemmFallbackVariant = 7;
 
 // k per wave for the decode kernel, in whole 32-k MFMA steps.
 // Streaming path (K % 32 == 0, one 4-wave workgroup per CU for its 144 KiB
@@ -192,7 +198,12 @@ int catena_mi355x_gemm_bf16(const uint16_t* a, const uint16_t* b, void* c, uint6
       const long x = strtol(v, nullptr, 10);
       if (x >= 0 && x < kGemmVariantCount) variant = (int)x;
     }
-    if (k < kGemmVariants[variant].min_k) variant = kGemmDefaultVariant;
+    // the 32-k stage kernels need K % 128 == 0 (whole groups of 4 stages);
+    // variant 9's buffer offsets need A's 256-row tile and B's 32-row slab
+    // within 31-bit byte ranges
+    const bool k32_ok = k % 128 == 0 && k <= (1ull << 22) && m <= (1ull << 24);
+    if (k < kGemmVariants[variant].min_k || (kGemmVariants[variant].min_k == 128 && !k32_ok))
+      variant = kGemmFallbackVariant;
     const GemmVariant& gv = kGemmVariants[variant];
     return launch(out_f32 ? gv.f32 : gv.bf16, dim3((unsigned)tiles), dim3(512), lds, args);
   }
