@@ -8,12 +8,15 @@
 // zero), so one v_mfma_f32_16x16x32_bf16 consumes a 32(k) x 16(n) piece of W.
 //
 // Work split (fixed, data independent):
-//   * a wave owns 128 consecutive columns and a contiguous chunk of KW k;
-//   * a workgroup holds 4 waves on 4 consecutive k chunks and adds their
-//     partials in ascending chunk order through LDS;
-//   * grid.y = number of such k groups (S).  With S > 1 each workgroup
-//     stores an f32 partial P[s][m][n] and takes a completion ticket for its
-//     column block; the last of the S workgroups adds the S partials in
+//   * a workgroup owns 128 consecutive columns and a k range of 4 * KW;
+//     its 4 waves each accumulate all 128 columns over part of that range
+//     (streaming path: the range's 32-k slabs dealt round robin, wave w
+//     taking slabs w, w+4, ...; register path: 4 consecutive chunks of KW),
+//     and the workgroup adds the 4 wave sums in wave order through LDS;
+//   * grid.y = number of k ranges (S).  With S > 1 each workgroup stores
+//     its f32 partial P[s][m][n] (16-byte stores that bypass the XCD caches)
+//     and takes a completion ticket for its column block; the last of the S
+//     workgroups loads the S partials the same way and adds them in
 //     ascending s.  The final M x 128 tile then goes through LDS to the
 //     epilogue.
 // The addition order depends only on the shape (the ticket decides which
@@ -114,6 +117,12 @@ CATENA_DEV bf16x8_t cat_bf16(i16x4_t lo, i16x4_t hi) {
   return __builtin_bit_cast(bf16x8_t, v);
 }
 
+// Buffer descriptor word 3 for raw (unswizzled, stride 0) 32-bit access, and
+// the cache-policy operand that sets sc1: the encoding the compiler uses for
+// agent-scope atomic loads and stores, which bypass the XCD-private caches.
+constexpr int kRsrcWord3 = 0x00020000;
+constexpr int kCpolSc1 = 16;
+
 // s_waitcnt on vmcnt only (gfx9 encoding: vmcnt[3:0], vmcnt[5:4] at 15:14)
 #define DEC_WAIT_VMCNT(n) \
   __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | 0x0070 | 0x0F00)
@@ -180,7 +189,15 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
     // (G, s) of MFMA block j gets W[k0 + 8G .. +7][n0 + 16j + s].  Output:
     // lane (G, s) holds rows 4G .. 4G+3 of column n0 + 16j + s.
     unsigned char* ring = dsm + wave * WAVE_RING;
-    const uint32_t steps = kbeg < kend ? (uint32_t)((kend - kbeg) / 32) : 0u;
+    // The workgroup's k range [kg0, kg1) is dealt to its waves in 32-k
+    // slabs, round robin (wave w takes slabs w, w+4, ...), so the four
+    // streams cover neighbouring rows of W and finish together.
+    const uint64_t kg0 = (uint64_t)blockIdx.y * 4 * KW;
+    uint64_t kg1 = kg0 + 4ull * KW;
+    if (kg1 > K) kg1 = K;
+    const uint32_t nslab = kg0 < kg1 ? (uint32_t)((kg1 - kg0) / 32) : 0u;
+    const uint32_t steps = nslab > (uint32_t)wave ? (nslab - (uint32_t)wave + 3u) / 4u : 0u;
+    const uint64_t kw0 = kg0 + 32ull * wave;
     // per-lane global byte offsets of the 8 W instructions (4 rows each)
     uint32_t woff[8];
     bool wlive[8];
@@ -194,15 +211,15 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
     // X slab: lane l fetches row l / 4, 16-byte chunk l % 4
     const uint32_t xr = lane >> 2, xq = lane & 3;
     const bool xl = xr < M;
-    const char* wsrc = reinterpret_cast<const char*>(W) + (kbeg * N + n0) * 2;
-    const char* xsrc = reinterpret_cast<const char*>(X) + ((uint64_t)xr * K + kbeg + 8 * xq) * 2;
-    auto issue = [&](uint32_t t, int slot) {
+    const char* wsrc = reinterpret_cast<const char*>(W) + (kw0 * N + n0) * 2;
+    const char* xsrc = reinterpret_cast<const char*>(X) + ((uint64_t)xr * K + kw0 + 8 * xq) * 2;
+    auto issue = [&](uint32_t t, int slot) {  // slab t of this wave = k kw0 + 128 t
       unsigned char* st = ring + slot * STAGE_BYTES;
-      const char* w = wsrc + (uint64_t)t * 32 * N * 2;
+      const char* w = wsrc + (uint64_t)t * 128 * N * 2;
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         if (wlive[i]) __builtin_amdgcn_global_load_lds(w + woff[i], (lds_void*)(st + 1024 * i), 16, 0, 0);
-      if (xl) __builtin_amdgcn_global_load_lds(xsrc + (uint64_t)t * 64, (lds_void*)(st + W_SLAB), 16, 0, 0);
+      if (xl) __builtin_amdgcn_global_load_lds(xsrc + (uint64_t)t * 256, (lds_void*)(st + W_SLAB), 16, 0, 0);
     };
     const uint32_t pre = steps < (uint32_t)RING ? steps : (uint32_t)RING;
     for (uint32_t t = 0; t < pre; ++t) issue(t, (int)t);
@@ -304,41 +321,55 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const uint32_t tc = streamed ? 16 * j + c : 8 * c + j;
-        if (S == 1) {
-          tile[row * TILE_LD + tc] = acc[j][q];
-        } else if (n0 + tc < N) {  // partial s of P, read by another workgroup
-          store_coherent(P + ((uint64_t)blockIdx.y * M + row) * N + n0 + tc, acc[j][q]);
-        }
+        tile[row * TILE_LD + tc] = acc[j][q];
       }
     }
   }
   if (S > 1) {
+    // This workgroup's partial, P[blockIdx.y][m][n0 ..], read by another
+    // workgroup: 16-byte stores that bypass the XCD-private caches (sc1), as
+    // agent-scope atomics do, from all threads.
+    __syncthreads();
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)P, (short)0, (int)(S * (uint64_t)M * N * 4), kRsrcWord3);
+    for (uint32_t e = tid; e < M * 32u; e += 256) {
+      const uint32_t row = e >> 5, c4 = 4 * (e & 31u);
+      if (n0 + c4 < N) {
+        const float* t = tile + row * TILE_LD + c4;
+        const u32x4_t v = u32x4_t{__float_as_uint(t[0]), __float_as_uint(t[1]),
+                                  __float_as_uint(t[2]), __float_as_uint(t[3])};
+        __builtin_amdgcn_raw_buffer_store_b128(
+            v, prs, (int)((((uint64_t)blockIdx.y * M + row) * N + n0 + c4) * 4), 0, kCpolSc1);
+      }
+    }
     if (!last_arrival(&tickets[blockIdx.x], S, &last_flag)) return;
     // Last k group of this column block: P[0] + P[1] + ... + P[S-1],
-    // ascending s, for the block's M rows x 128 columns.
-    const uint64_t MN = (uint64_t)M * N;
+    // ascending s, for the block's M rows x 128 columns; every partial's
+    // 16-byte coherent load of a batch (16 partials) is issued before the
+    // adds.
     for (uint32_t e = tid; e < M * 32u; e += 256) {
       const uint32_t row = e >> 5, c4 = 4 * (e & 31u);
       const uint64_t cc = n0 + c4;
       f32x4_t sum = f32x4_t{0.f, 0.f, 0.f, 0.f};
       if (cc < N) {
-        const float* src = P + (uint64_t)row * N + cc;
+        const uint64_t base = ((uint64_t)row * N + cc) * 4, MN4 = (uint64_t)M * N * 4;
+        for (uint32_t s0 = 0; s0 < S; s0 += 16) {
+          u32x4_t part[16];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) sum[q] = load_coherent(src + q);
-        // partials 1..S-1 in batches of 8, every load of a batch issued
-        // before its adds
-        for (uint32_t s0 = 1; s0 < S; s0 += 8) {
-          f32x4_t part[8];
-#pragma unroll
-          for (int u = 0; u < 8; ++u)
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-              part[u][q] = s0 + u < S ? load_coherent(src + (uint64_t)(s0 + u) * MN + q) : 0.0f;
-#pragma unroll
-          for (int u = 0; u < 8; ++u)
+          for (int u = 0; u < 16; ++u)
             if (s0 + u < S)
+              part[u] = __builtin_amdgcn_raw_buffer_load_b128(prs, (int)(base + (s0 + u) * MN4), 0, kCpolSc1);
 #pragma unroll
-              for (int q = 0; q < 4; ++q) sum[q] = sum[q] + part[u][q];
+          for (int u = 0; u < 16; ++u)
+            if (s0 + u < S) {
+              if (s0 + u == 0) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) sum[q] = __uint_as_float(part[u][q]);
+              } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) sum[q] = sum[q] + __uint_as_float(part[u][q]);
+              }
+            }
         }
       }
 #pragma unroll
