@@ -331,7 +331,7 @@ def main(argv=None) -> int:
         "bitwise_run_to_run": g["bitwise_run_to_run"],
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
-                     "traffic": measured_traffic("catena_gemm_bf16_lds_v7_bf16out")},
+                     "traffic": measured_traffic("catena_gemm_bf16_k32_bf16out")},
         "cpu_baseline": cpu,
         "extra": extra,
     }
