@@ -93,6 +93,32 @@ def timed(fn, steps: int, warmup: int, ev: HipEvents) -> float:
     return ms / steps
 
 
+def per_launch_us(fn, launches: int, ev: HipEvents) -> dict:
+    """Each launch bracketed by its own events (after the timed run):
+    median / p10 / p90 in microseconds, the protocol's per-launch spread."""
+    t = []
+    for i in range(launches):
+        ev.start()
+        fn(i)
+        t.append(ev.stop_ms() * 1e3)
+    t = np.array(t)
+    return {"median": round(float(np.median(t)), 2), "p10": round(float(np.percentile(t, 10)), 2),
+            "p90": round(float(np.percentile(t, 90)), 2), "launches": launches}
+
+
+def host_cpu() -> dict:
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"model": model, "cpus_visible": len(os.sched_getaffinity(0))}
+
+
 def output_hash(buf: ca.Buffer) -> str:
     import hashlib
     return hashlib.sha256(buf.read(np.uint8).tobytes()).hexdigest()[:16]
@@ -109,8 +135,11 @@ def bench_gemm(steps, warmup, ev):
     ms = timed(lambda i: ca.gemm_bf16(a, b, c, n, m, k), steps, warmup, ev)
     flop = 2.0 * n * m * k
     tflops = flop / (ms * 1e-3) / 1e12
-    return {"ms": ms, "tflops": tflops, "flop": flop, "bitwise_run_to_run": output_hash(c) == h0,
-            "inputs": (a, b)}
+    same = output_hash(c) == h0
+    spread = per_launch_us(lambda i: ca.gemm_bf16(a, b, c, n, m, k), max(10, steps), ev)
+    same = same and output_hash(c) == h0
+    return {"ms": ms, "tflops": tflops, "flop": flop, "bitwise_run_to_run": same,
+            "per_launch_us": spread, "inputs": (a, b)}
 
 
 def bench_decode_gemm(steps, warmup, ev):
@@ -129,11 +158,13 @@ def bench_decode_gemm(steps, warmup, ev):
             ca.fill_normal_bf16(w, K * N, 8, c, 0.02)
             ws.append(w)
         y = ca.Buffer(M * N * 2)
-        ms = timed(lambda i: ca.gemm_bf16(x, ws[i % copies], y, M, N, K), steps, warmup, ev)
+        call = lambda i: ca.gemm_bf16(x, ws[i % copies], y, M, N, K)  # noqa: E731
+        ms = timed(call, steps, warmup, ev)
         nbytes = 2.0 * N * K + 2.0 * M * K + 2.0 * M * N
         res[f"N{N}_K{K}"] = {"us": ms * 1e3, "GB/s": nbytes / (ms * 1e-3) / 1e9,
                              "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
-                             "bytes_per_launch": nbytes}
+                             "bytes_per_launch": nbytes,
+                             "per_launch_us": per_launch_us(call, max(10, steps), ev)}
         del ws
     return res
 
@@ -155,8 +186,11 @@ def bench_attention(steps, warmup, ev):
     ms = timed(call, steps, warmup, ev)
     nbytes = 2.0 * B * H * L * D * 2 + B * H * D * 2 + B * H * D * 4
     gbs = nbytes / (ms * 1e-3) / 1e9
+    same = output_hash(o) == h0
+    spread = per_launch_us(call, max(10, steps), ev)
+    same = same and output_hash(o) == h0
     return {"us": ms * 1e3, "GB/s": gbs, "frac_hbm": gbs / PEAK_HBM_GBS, "bytes_per_launch": nbytes,
-            "bitwise_run_to_run": output_hash(o) == h0, "inputs": (q, k, v)}
+            "bitwise_run_to_run": same, "per_launch_us": spread, "inputs": (q, k, v)}
 
 
 def bench_decoder(reps: int, ev):
@@ -286,6 +320,7 @@ def main(argv=None) -> int:
             "decode_attention": {
                 "workload": "B=32 H=32 D=128 L=4096 bf16 KV, f32 softmax/out, bitwise vs sequential oracle",
                 "us_per_launch": at["us"], "GB/s": at["GB/s"], "bitwise_run_to_run": at["bitwise_run_to_run"],
+                "per_launch_us": at["per_launch_us"],
                 "roofline": {"bound": "hbm", "achieved": at["GB/s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                              "frac": at["frac_hbm"],
                              "traffic": measured_traffic("catena_attn_decode_bf16_d128_kc")},
@@ -307,6 +342,9 @@ def main(argv=None) -> int:
         print(f"[bench] cpu baseline ({threads} threads)", file=sys.stderr, flush=True)
         a, b = g["inputs"]
         cpu = cpu_baseline_gemm(a, b, rows=4096, threads=threads)
+        single = cpu_baseline_gemm(a, b, rows=64, threads=1)
+        extra["cpu_baseline_single_thread"] = {k_: single[k_] for k_ in ("value", "unit", "cores", "kind", "sample")}
+        extra["host_cpu"] = host_cpu()
         if core:
             q, k, v = at["inputs"]
             extra["decode_attention"]["cpu_baseline"] = cpu_baseline_attention(q, k, v, 1024, threads)
@@ -329,6 +367,7 @@ def main(argv=None) -> int:
                                "fixed K order (BASELINE configs[1])",
                    "M": 4096, "N": 4096, "K": 4096, "parallelism": "single GPU"},
         "bitwise_run_to_run": g["bitwise_run_to_run"],
+        "per_launch_us": g["per_launch_us"],
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
                      "traffic": measured_traffic("catena_gemm_bf16_k32_bf16out")},
