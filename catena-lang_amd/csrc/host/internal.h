@@ -36,6 +36,8 @@ enum class KernelId : int {
   GemmBf16DeepFrontF32,
   GemmBf16K32Bf16,  // four 32-k stages, spread buffer loads, LDS-staged epilogue (default)
   GemmBf16K32F32,
+  GemmBf16K32N128Bf16,  // the same on 256 x 128 tiles
+  GemmBf16K32N128F32,
   GemmBf16DecodeF32,
   GemmBf16DecodeBf16,
   GemmBf16DecodeRope,

@@ -41,12 +41,29 @@ const GemmVariant kGemmVariants[] = {
     /* 9 four 32-k stages through buffer loads spread over the MFMAs, LDS-staged
        bf16 epilogue (gemm_bf16_k32.hip) */
     {KernelId::GemmBf16K32Bf16, KernelId::GemmBf16K32F32, 128},
+    /* 10 variant 9 on 256 x 128 tiles (8 waves of 64 x 64) */
+    {KernelId::GemmBf16K32N128Bf16, KernelId::GemmBf16K32N128F32, 128},
 };
 constexpr int kGemmVariantCount = sizeof(kGemmVariants) / sizeof(kGemmVariants[0]);
 // Default: variant 9 when K % 128 == 0 (and its 32-bit buffer offsets hold),
-// else variant 7.
+// else variant 7; variant 9 on 256 x 128 tiles (10) when that takes fewer
+// rounds of the chip (see prefer_n128).
 constexpr int kGemmDefaultVariant = 9;
 constexpr int kGemmFallbackVariant = 7;
+constexpr int kGemmN128Variant = 10;
+
+// 256 x 128 tiles instead of 256 x 256: measured on the box, a round of
+// 256 x 128 tiles (one per CU) takes ~0.6 of a round of 256 x 256 tiles at the
+// same K, so the narrow tiles win when the wide ones leave CUs idle (W_o and
+// W_down of the C5 prefill: 128 wide tiles for 256 CUs, 52.6 -> 37.6 us and
+// 124 -> 93 us) and lose on full rounds (4096^3: 115 -> 138 us).
+bool prefer_n128(uint64_t rows, uint64_t cols, int cu_count) {
+  const uint64_t cus = cu_count > 0 ? (uint64_t)cu_count : 256;
+  const uint64_t wide = (rows / 256) * (cols / 256);
+  const uint64_t narrow = (rows / 256) * (cols / 128);
+  const double r_wide = (double)ceil_div(wide, cus), r_narrow = (double)ceil_div(narrow, cus);
+  return 0.62 * r_narrow < r_wide;
+}
 
 // k per wave for the decode kernel, in whole 32-k MFMA steps.
 // Streaming path (K % 32 == 0, one 4-wave workgroup per CU for its 144 KiB
@@ -127,6 +144,11 @@ int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, 
   }
   float* P = nullptr;
   if (S > 1) {
+    // the partials are addressed through one buffer descriptor with 32-bit
+    // byte offsets
+    if (S * M * m * sizeof(float) >= (1ull << 31))
+      return fail(CATENA_ERR_UNSUPPORTED, "decode GEMM partials exceed 2 GiB (%llu k groups)",
+                  (unsigned long long)S);
     void* ws = nullptr;
     st = workspace(S * M * m * sizeof(float), &ws);
     if (st) return st;
@@ -179,33 +201,42 @@ int catena_mi355x_gemm_bf16(const uint16_t* a, const uint16_t* b, void* c, uint6
                             out_f32 ? DecodeEpilogue::StoreF32 : DecodeEpilogue::StoreBf16,
                             DecodeEpiArgs{});
 
-  const bool tile_ok = n % 256 == 0 && m % 256 == 0 && k % 64 == 0 && k > 0 && aligned16(a) &&
-                       aligned16(b) && aligned16(c);
+  const bool ptr_ok = aligned16(a) && aligned16(b) && aligned16(c);
+  const bool tile_ok = n % 256 == 0 && m % 256 == 0 && k % 64 == 0 && k > 0 && ptr_ok;
+  // the 32-k stage kernels need K % 128 == 0 (whole groups of 4 stages);
+  // variants 9 and 10 address A's 256-row tile and B's 32-row slab with
+  // 32-bit buffer offsets
+  const bool k32_ok = k % 128 == 0 && k > 0 && k <= (1ull << 22) && m <= (1ull << 24);
+  const bool n128_ok = n % 256 == 0 && m % 128 == 0 && k32_ok && ptr_ok;
   const uint64_t tiles = ceil_div(n, 256) * ceil_div(m, 256);
-  if (tiles > 0x7FFFFFFFu) return fail(CATENA_ERR_UNSUPPORTED, "matrix too large");
+  if (ceil_div(n, 256) * ceil_div(m, 128) > 0x7FFFFFFFu)
+    return fail(CATENA_ERR_UNSUPPORTED, "matrix too large");
   void* args[] = {&a, &b, &c, &n, &m, &k};
-  // Aligned shapes: direct-to-LDS kernel (8 waves, 128 KiB LDS).  The older
+  // Aligned shapes: direct-to-LDS kernels (8 waves).  The older
   // register-staged tile kernel stays selectable with CATENA_GEMM_TILE=regs
   // for comparison; it computes in the same order per output tile.
   const char* sel = getenv("CATENA_GEMM_TILE");
   const bool use_regs = sel && strcmp(sel, "regs") == 0;
-  if (tile_ok && !use_regs) {
-    const size_t lds = 2ull * (256 * 64 + 64 * 256) * sizeof(uint16_t);  // 131072 B
-    if (lds > d.max_lds) return fail(CATENA_ERR_UNSUPPORTED, "device LDS %zu < %zu", d.max_lds, lds);
+  if ((tile_ok || n128_ok) && !use_regs) {
     int variant = kGemmDefaultVariant;
     const char* v = getenv("CATENA_GEMM_VARIANT");
-    if (v && *v) {
+    const bool forced = v && *v;
+    if (forced) {
       const long x = strtol(v, nullptr, 10);
       if (x >= 0 && x < kGemmVariantCount) variant = (int)x;
     }
-    // the 32-k stage kernels need K % 128 == 0 (whole groups of 4 stages);
-    // variant 9's buffer offsets need A's 256-row tile and B's 32-row slab
-    // within 31-bit byte ranges
-    const bool k32_ok = k % 128 == 0 && k <= (1ull << 22) && m <= (1ull << 24);
+    if (!tile_ok || (!forced && n128_ok && prefer_n128(n, m, d.cu_count))) variant = kGemmN128Variant;
+    if (variant == kGemmN128Variant && !n128_ok) variant = kGemmDefaultVariant;
     if (k < kGemmVariants[variant].min_k || (kGemmVariants[variant].min_k == 128 && !k32_ok))
       variant = kGemmFallbackVariant;
     const GemmVariant& gv = kGemmVariants[variant];
-    return launch(out_f32 ? gv.f32 : gv.bf16, dim3((unsigned)tiles), dim3(512), lds, args);
+    const bool narrow = variant == kGemmN128Variant;
+    // two-stage kernels: 2 x (A 256x64 + B 64x256); four-stage: 4 x (A 256x32 + B 32xBN)
+    const size_t lds = narrow ? 4ull * (256 + 128) * 32 * sizeof(uint16_t)   // 98304 B
+                              : 2ull * (256 * 64 + 64 * 256) * sizeof(uint16_t);  // 131072 B
+    if (lds > d.max_lds) return fail(CATENA_ERR_UNSUPPORTED, "device LDS %zu < %zu", d.max_lds, lds);
+    const uint64_t grid = narrow ? (n / 256) * (m / 128) : tiles;
+    return launch(out_f32 ? gv.f32 : gv.bf16, dim3((unsigned)grid), dim3(512), lds, args);
   }
   const size_t lds = 2ull * 2 * 256 * 72 * sizeof(uint16_t);  // 147456 B
   if (lds > d.max_lds) return fail(CATENA_ERR_UNSUPPORTED, "device LDS %zu < %zu", d.max_lds, lds);

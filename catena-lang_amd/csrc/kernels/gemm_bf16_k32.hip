@@ -1,42 +1,47 @@
-// bf16 GEMM, aligned shapes (M % 256 == 0, N % 256 == 0, K % 128 == 0): the
-// default tile kernel.  Four 32-k stages in LDS fed by buffer loads spread
+// bf16 GEMM, aligned shapes (M % 256 == 0, N % BN == 0, K % 128 == 0): the
+// default tile kernels.  Four 32-k stages in LDS fed by buffer loads spread
 // through the MFMA stream, and (bf16 output) an LDS-staged epilogue that
 // writes whole 128-byte rows.
 //
 // Contraction, tile and order are those of gemm_bf16_lds.hip (reference
 // semantics: catena-lang/stdlib/matrix.hex:236-327 on bf16 inputs widened
-// exactly, f32 accumulation, NN row-major): one workgroup per 256x256 output
-// tile, 8 waves of 128x64, v_mfma_f32_16x16x32_bf16 with the B fragment as
-// the first operand, K ascending in k32 steps, no split-K, no atomics, so the
-// output is bitwise identical to the other tile kernels and run to run.
+// exactly, f32 accumulation, NN row-major): one workgroup per 256 x BN
+// output tile, v_mfma_f32_16x16x32_bf16 with the B fragment as the first
+// operand, K ascending in k32 steps, no split-K, no atomics, so the output
+// is bitwise identical to the other tile kernels and run to run (each
+// output element sees the same MFMA sequence whatever the tile width).
 //
-// Pipeline (S = 4 stages of A [256][32] + B [32][256] = 32 KiB):
+// Tile widths (8 waves each):
+//   BN = 256: waves 2 (m) x 4 (n), wave tile 128 x 64 (8 x 4 MFMA blocks);
+//   BN = 128: waves 4 (m) x 2 (n), wave tile  64 x 64 (4 x 4 MFMA blocks),
+//     for shapes whose 256 x 256 tiles leave CUs idle (the host picks).
+//
+// Pipeline (S = 4 stages of A [256][32] + B [32][BN]):
 //   step s multiplies slab s (fragments already in registers), reads slab
-//   s+1's fragments from its stage between the first 16 MFMAs, and issues
-//   slab s+4 into slab s's stage (free since the barrier that closed step
-//   s-1), one 1-KiB load after every 8th MFMA.  The barrier that closes step
-//   s waits for slab s+2 only, so a slab has about three steps to arrive.
-//   Slabs past the end are loaded through descriptors with no records: the
-//   hardware returns zeros without touching memory, and every step keeps the
-//   same wait counts.
+//   s+1's fragments from its stage between its first MFMAs (one read per
+//   MFMA), and issues slab s+4 into slab s's stage (free since the barrier
+//   that closed step s-1), the loads spread over the step.  The barrier that
+//   closes step s waits for slab s+2 only, so a slab has about three steps
+//   to arrive.  Slabs past the end are loaded through descriptors with no
+//   records: the hardware returns zeros without touching memory, and every
+//   step keeps the same wait counts.
 //   Spreading the loads matters: the CU's global->LDS path moves 64 B per
-//   clock, half of what the MFMAs consume in a step, and a burst of loads at
-//   the barrier stalls the issuing waves.
-// LDS layout: A stages [S][256][32] then B stages [S][32][256], so every read
-// offset from the two per-lane bases fits a DS instruction's immediate.
+//   clock, half of what the MFMAs consume in a step (BN = 256), and a burst
+//   of loads at the barrier stalls the issuing waves.
+// LDS layout: A stages [S][256][32] then B stages [S][32][BN], so every read
+// offset from the per-lane bases fits a DS instruction's immediate.
 // Swizzles (conflict-free through the direct-to-LDS write layout):
-//   A [256][64 B]: LDS chunk p of row r holds global chunk p ^ ((r >> 2) & 3);
-//   B [32][512 B]: LDS chunk p of row k holds global chunk p ^ hB(k),
-//                  hB(k) = 2 * ((k & 3) | ((k >> 3) & 1) << 2)  (row bit 4 unused,
-//                  so a load 16 rows further shares the lane offset).
+//   A [256][64 B]:   LDS chunk p of row r holds global chunk p ^ ((r >> 2) & 3);
+//   B [32][2*BN B]:  LDS chunk p of row k holds global chunk p ^ hB(k),
+//                    hB(k) = 2 * ((k & 3) | ((k >> 3) & 1) << 2)  (row bit 4
+//                    unused, so a load 16 rows further shares the lane offset).
 #include <type_traits>
 
 #include "common.h"
 
 namespace {
-constexpr int BM = 256, BN = 256, BK = 32, S = 4;
+constexpr int BM = 256, BK = 32, S = 4;
 constexpr int A_ST = BM * BK;  // elements per A stage
-constexpr int B_ST = BK * BN;  // elements per B stage
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
@@ -74,31 +79,41 @@ CATENA_DEV void tile_of(uint32_t bid, uint32_t tiles_m, uint32_t tiles_n, uint32
 // buffer descriptor word 3 for raw (unswizzled, stride 0) 32-bit access
 constexpr int kRsrcWord3 = 0x00020000;
 
-template <bool OUT_BF16>
+template <bool OUT_BF16, int BN>
 CATENA_DEV void gemm_k32_body(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                               void* __restrict__ C, uint64_t M, uint64_t N, uint64_t K) {
+  static_assert(BN == 256 || BN == 128, "tile widths 256 and 128");
+  constexpr int B_ST = BK * BN;                // elements per B stage
+  constexpr int WI = BN == 256 ? 8 : 4;        // 16-row MFMA blocks per wave
+  constexpr int WAVES_N = BN == 256 ? 4 : 2;   // waves across the tile's columns
+  constexpr int NB_LOADS = BN / 128;           // B loads per wave per slab
+  constexpr int LOADS = 2 + NB_LOADS;          // loads per wave per slab
+  constexpr int READS = WI + 8;                // fragment reads per wave per step
+  constexpr int MFMAS = WI * 4;                // MFMAs per wave per step
+  constexpr int B_LANES = BN / 8;              // lanes per B row in one load
   extern __shared__ __attribute__((aligned(1024))) uint16_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, 0..7
-  const int wm = wave >> 2, wn = wave & 3;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const uint32_t tiles_m = (uint32_t)(M / BM), tiles_n = (uint32_t)(N / BN);
   uint32_t tm, tn;
   tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const uint64_t m0 = (uint64_t)tm * BM, n0 = (uint64_t)tn * BN;
 
-  // Loads per slab: A 16 one-KiB instructions (16 rows of 64 B each), B 16
-  // (2 rows of 512 B each); per wave 2 + 2, the second 16 rows below the
-  // first (soffset), with the lane offsets of the first.
+  // Loads per slab: A 16 one-KiB instructions (16 rows of 64 B each) and B
+  // BN / 16 (64 / B_LANES rows of 2 * BN bytes each); per wave 2 of A, the
+  // second 16 rows below the first, and NB_LOADS of B, the second 16 rows
+  // below the first (soffset), with the lane offsets of the first.
   uint32_t aoff, boff;
   {
     const uint32_t r = 32 * wave + (lane >> 2);
     const uint32_t q = (uint32_t)(lane & 3) ^ ((r >> 2) & 3u);
     aoff = (uint32_t)((r * K + 8 * q) * 2);
-    const uint32_t kr = 2 * wave + (lane >> 5);
-    const uint32_t qb = (uint32_t)(lane & 31) ^ hB(kr);
+    const uint32_t kr = (64 / B_LANES) * wave + (uint32_t)lane / B_LANES;
+    const uint32_t qb = (uint32_t)(lane % B_LANES) ^ hB(kr);
     boff = (uint32_t)((kr * N + 8 * qb) * 2);
   }
-  // Load idx (0, 1: A; 2, 3: B) of slab `slab` into stage `stage`.
+  // Load idx (0, 1: A; 2 .. LOADS-1: B) of slab `slab` into stage `stage`.
   auto issue_one = [&](uint64_t slab, int stage, int idx) {
     const uint64_t k0 = slab * BK;
     const bool live = k0 < K;
@@ -109,27 +124,28 @@ CATENA_DEV void gemm_k32_body(const uint16_t* __restrict__ A, const uint16_t* __
           rs, (lds_void*)(smem + stage * A_ST + (32 * wave + 16 * idx) * BK), 16, (int)aoff,
           idx ? (int)(16 * K * 2) : 0, 0, 0);
     } else {
+      const int b = idx - 2;
       const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
           (void*)(B + (live ? k0 : 0) * N + n0), (short)0, live ? (int)(BK * N * 2) : 0, kRsrcWord3);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rs, (lds_void*)(smem + S * A_ST + stage * B_ST + (2 * wave + 16 * (idx - 2)) * BN), 16,
-          (int)boff, idx == 3 ? (int)(16 * N * 2) : 0, 0, 0);
+          rs, (lds_void*)(smem + S * A_ST + stage * B_ST + ((64 / B_LANES) * wave + 16 * b) * BN), 16,
+          (int)boff, b ? (int)(16 * N * 2) : 0, 0, 0);
     }
   };
 
-  f32x4_t acc[8][4];  // [row block i][col block j], transposed blocks
+  f32x4_t acc[WI][4];  // [row block i][col block j], transposed blocks
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < WI; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // Fragment read bases.  A: lane (G, s) reads row wm*128 + 16 i + s, chunk
+  // Fragment read bases.  A: lane (G, s) reads row wm*16*WI + 16 i + s, chunk
   // G ^ ((s >> 2) & 3) (row + 16 i leaves the swizzle unchanged).  B: two
   // ds_read_b64_tr_b16 per 32x16 block (rows 8G + s/4 and +4, columns
   // 16 j + 4 (s % 4)), so lane i of a 16-lane group receives 4 consecutive k
   // of one column, matching A's k order.
   const int G = lane >> 4, s = lane & 15;
-  const uint32_t a_lds = (wm * 128 + s) * BK * 2 + 16 * ((uint32_t)G ^ ((uint32_t)(s >> 2) & 3u));
+  const uint32_t a_lds = (wm * 16 * WI + s) * BK * 2 + 16 * ((uint32_t)G ^ ((uint32_t)(s >> 2) & 3u));
   const uint32_t b_krow = 8 * G + (s >> 2);
   const uint32_t hb = hB(b_krow);
   uint32_t b_lds[4];
@@ -140,14 +156,14 @@ CATENA_DEV void gemm_k32_body(const uint16_t* __restrict__ A, const uint16_t* __
   }
 
   struct Frags {
-    bf16x8_t a[8];
+    bf16x8_t a[WI];
     bf16x8_t b[4];
   };
   auto load_frags = [&](int stage, Frags& f) {
     const char* sa = reinterpret_cast<const char*>(smem + stage * A_ST);
     const char* sb = reinterpret_cast<const char*>(smem + stage * B_ST);
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < WI; ++i)
       f.a[i] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(sa + a_lds + i * 16 * BK * 2));
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -160,58 +176,52 @@ CATENA_DEV void gemm_k32_body(const uint16_t* __restrict__ A, const uint16_t* __
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int i = 0; i < WI; ++i)
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.b[j], f.a[i], acc[i][j], 0, 0, 0);
   };
-  // One step: the MFMAs of `cur`; reads of `next` from stage rs one per MFMA
-  // over the first 16; slab islab's four loads into stage ws after MFMAs 0,
-  // 8, 16 and 24.  Scheduling barriers pin the interleave.
+  // One step: the MFMAs of `cur`; the reads of `next` from stage rs one per
+  // MFMA over the first READS; slab islab's LOADS loads into stage ws spread
+  // over the step (after MFMA LOAD_AT(l)).  Scheduling barriers pin the
+  // interleave.
+  auto load_at = [](int l) { return (l * MFMAS) / LOADS; };
   auto step = [&](int rs, Frags& next, const Frags& cur, uint64_t islab, int ws) {
     const char* sa = reinterpret_cast<const char*>(smem + rs * A_ST);
     const char* sb = reinterpret_cast<const char*>(smem + rs * B_ST);
     i16x4_t blo[4], bhi[4];
 #pragma unroll
-    for (int g = 0; g < 16; ++g) {
-      if (g < 8) {
+    for (int g = 0; g < MFMAS; ++g) {
+      if (g < WI) {
         next.a[g] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(sa + a_lds + g * 16 * BK * 2));
-      } else {
-        const int j = (g - 8) >> 1;
-        if ((g & 1) == 0)
+      } else if (g < READS) {
+        const int j = (g - WI) >> 1;
+        if (((g - WI) & 1) == 0)
           blo[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(sb + b_lds[j]));
         else
           bhi[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(sb + b_lds[j] + 4 * BN * 2));
       }
-      const int j = g >> 3, i = g & 7;
+      const int j = g / WI, i = g % WI;
       acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.b[j], cur.a[i], acc[i][j], 0, 0, 0);
-      if ((g & 7) == 0) issue_one(islab, ws, g >> 3);
+#pragma unroll
+      for (int l = 0; l < LOADS; ++l)
+        if (g == load_at(l)) issue_one(islab, ws, l);
     }
 #pragma unroll
-    for (int m = 16; m < 32; ++m) {
-      const int j = m >> 3, i = m & 7;
-      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.b[j], cur.a[i], acc[i][j], 0, 0, 0);
-      if ((m & 7) == 0) issue_one(islab, ws, m >> 3);
-    }
+    for (int g = 0; g < MFMAS; ++g) {
+      if (g < READS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                 // one MFMA
 #pragma unroll
-    for (int g = 0; g < 16; ++g) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-      if ((g & 7) == 0) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one load
-    }
-#pragma unroll
-    for (int g = 16; g < 32; g += 8) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 7, 0);
+      for (int l = 0; l < LOADS; ++l)
+        if (g == load_at(l)) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one load
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) next.b[j] = cat_bf16(blo[j], bhi[j]);
   };
   // Closing a step: this wave's fragment reads have landed and its loads of
-  // slab s+2 have (two later slabs of 4 loads stay in flight); after the
+  // slab s+2 have (two later slabs of LOADS loads stay in flight); after the
   // barrier every wave is past the same point.
   auto end_step = [&]() {
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    CATENA_WAIT_VMCNT(4 * (S - 2));
+    CATENA_WAIT_VMCNT(LOADS * (S - 2));
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -221,8 +231,8 @@ CATENA_DEV void gemm_k32_body(const uint16_t* __restrict__ A, const uint16_t* __
 #pragma unroll
   for (int t = 0; t < S; ++t)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) issue_one((uint64_t)t, t, q);
-  CATENA_WAIT_VMCNT(4 * (S - 2));  // slabs 0 and 1 landed
+    for (int q = 0; q < LOADS; ++q) issue_one((uint64_t)t, t, q);
+  CATENA_WAIT_VMCNT(LOADS * (S - 2));  // slabs 0 and 1 landed
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   Frags f0, f1;
@@ -243,14 +253,13 @@ CATENA_DEV void gemm_k32_body(const uint16_t* __restrict__ A, const uint16_t* __
   CATENA_WAIT_VMCNT(0);  // no LDS writes outstanding past this point
 
   if constexpr (OUT_BF16) {
-    // Stage the wave's 128 x 64 bf16 tile in its own 16 KiB of LDS (row r,
-    // 16-byte chunk c at r * 128 + 16 * (c ^ ((r >> 1) & 7))), then store
-    // whole 128-byte rows: 8 lanes per row, 8 rows per instruction.  The
-    // barrier above (closing the last step) left every wave done with the
-    // stages.
-    char* wt = reinterpret_cast<char*>(smem) + wave * 16384;
+    // Stage the wave's (16 WI) x 64 bf16 tile in its own LDS (row r, 16-byte
+    // chunk c at r * 128 + 16 * (c ^ ((r >> 1) & 7))), then store whole
+    // 128-byte rows: 8 lanes per row, 8 rows per instruction.  The barrier
+    // above (closing the last step) left every wave done with the stages.
+    char* wt = reinterpret_cast<char*>(smem) + wave * (WI * 16 * 128);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < WI; ++i) {
       const uint32_t r = 16 * i + s;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -264,18 +273,18 @@ CATENA_DEV void gemm_k32_body(const uint16_t* __restrict__ A, const uint16_t* __
     }
     const uint32_t rr = (uint32_t)lane >> 3, cc = (uint32_t)lane & 7;
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {
+    for (int t = 0; t < 2 * WI; ++t) {
       const uint32_t r = 8 * t + rr;
       const u32x4_t v = *reinterpret_cast<const u32x4_t*>(wt + r * 128 + 16 * (cc ^ ((r >> 1) & 7u)));
-      const uint64_t gr = m0 + wm * 128 + r;
+      const uint64_t gr = m0 + wm * 16 * WI + r;
       const uint64_t gc = n0 + wn * 64 + 8 * cc;
       *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(C) + gr * N + gc) = v;
     }
   } else {
     // acc[i][j] lane (G, s) holds C[row 16 i + s][cols 16 j + 4G .. +3]
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint64_t gr = m0 + wm * 128 + 16 * i + s;
+    for (int i = 0; i < WI; ++i) {
+      const uint64_t gr = m0 + wm * 16 * WI + 16 * i + s;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint64_t gc = n0 + wn * 64 + 16 * j + 4 * G;
@@ -286,14 +295,15 @@ CATENA_DEV void gemm_k32_body(const uint16_t* __restrict__ A, const uint16_t* __
 }
 }  // namespace
 
-extern "C" __global__ __launch_bounds__(512) void catena_gemm_bf16_k32_bf16out(
-    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C,
-    uint64_t M, uint64_t N, uint64_t K) {
-  gemm_k32_body<true>(A, B, C, M, N, K);
-}
+#define CATENA_GEMM_K32_KERNEL(NAME, OUTB, BN_)                                           \
+  extern "C" __global__ __launch_bounds__(512) void NAME(                                 \
+      const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C, \
+      uint64_t M, uint64_t N, uint64_t K) {                                               \
+    gemm_k32_body<OUTB, BN_>(A, B, C, M, N, K);                                           \
+  }
 
-extern "C" __global__ __launch_bounds__(512) void catena_gemm_bf16_k32_f32out(
-    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C,
-    uint64_t M, uint64_t N, uint64_t K) {
-  gemm_k32_body<false>(A, B, C, M, N, K);
-}
+// grid = (M / 256) * (N / BN), block = 512, dynamic LDS S * (256 + BN) * 32 * 2 B
+CATENA_GEMM_K32_KERNEL(catena_gemm_bf16_k32_bf16out, true, 256)
+CATENA_GEMM_K32_KERNEL(catena_gemm_bf16_k32_f32out, false, 256)
+CATENA_GEMM_K32_KERNEL(catena_gemm_bf16_k32n128_bf16out, true, 128)
+CATENA_GEMM_K32_KERNEL(catena_gemm_bf16_k32n128_f32out, false, 128)

@@ -94,19 +94,33 @@ def test_register_staged_tile_kernel(monkeypatch):
 
 @pytest.mark.parametrize("n,m,k", [(512, 768, 1024), (256, 256, 4224)])
 def test_tile_variants_bitwise_identical(monkeypatch, n, m, k):
-    """Every aligned-tile scheduling variant (CATENA_GEMM_VARIANT 0..9) keeps
-    the same per-accumulator k32 order, so all outputs are the same bits."""
+    """Every aligned-tile scheduling variant (CATENA_GEMM_VARIANT 0..10, tile
+    widths 256 and 128) keeps the same per-accumulator k32 order, so all
+    outputs are the same bits."""
     say(f"bf16 gemm tile variants {n}x{m}x{k}")
     a, b, _, _ = _inputs(n, m, k, seed=900 + k)
     outs = {}
-    for v in range(10):
+    for v in range(11):
         monkeypatch.setenv("CATENA_GEMM_VARIANT", str(v))
         c16, c32 = ca.Buffer(n * m * 2), ca.Buffer(n * m * 4)
         ca.gemm_bf16(a, b, c16, n, m, k)
         ca.gemm_bf16(a, b, c32, n, m, k, out_f32=True)
         outs[v] = (c16.read(np.uint16).tobytes(), c32.read(np.float32).tobytes())
-    for v in range(1, 10):
+    for v in range(1, 11):
         assert outs[v] == outs[0], v
+
+
+@pytest.mark.parametrize("n,m,k", [(256, 384, 256), (512, 128, 1152)])
+def test_narrow_tile_kernel_full_compare(n, m, k):
+    """N % 256 == 128: only the 256 x 128 tile kernel applies."""
+    say(f"bf16 gemm 256x128 tiles {n}x{m}x{k}")
+    a, b, a16, b16 = _inputs(n, m, k, seed=400 + n + m + k)
+    c32, c16 = ca.Buffer(n * m * 4), ca.Buffer(n * m * 2)
+    ca.gemm_bf16(a, b, c32, n, m, k, out_f32=True)
+    ca.gemm_bf16(a, b, c16, n, m, k, out_f32=False)
+    g32, g16 = c32.read(np.float32, (n, m)), c16.read(np.uint16, (n, m))
+    assert np.array_equal(g16, oracle.f32_to_bf16_bits_np(g32))
+    _check(a16, b16, g32, g16)
 
 
 @pytest.mark.parametrize("n,m,k", [(1, 1, 1), (17, 9, 5), (300, 200, 100), (257, 513, 72),
