@@ -29,8 +29,9 @@
 // V pass: waves 0 and 1 own 64 output columns each (lane = column) and walk
 // t ascending through 64-row batches staged in LDS, with the next two
 // batches' loads in flight while one is folded; the first batch is requested
-// before the softmax phase so HBM stays busy through it.  Every K and V byte
-// is read from HBM once.
+// before the softmax phase so HBM stays busy through it.  A full batch is
+// read back four rows at a time with the transposing LDS read, p four at a
+// time.  Every K and V byte is read from HBM once.
 #include "common.h"
 
 namespace {
@@ -44,6 +45,9 @@ CATENA_DEV void wave_sync() {
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
+
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
 
 CATENA_DEV int wave_max_i32(int v) {
 #pragma unroll
@@ -233,6 +237,8 @@ CATENA_DEV void attn_body(const uint16_t* __restrict__ q, const uint16_t* __rest
     if (vnb > 1) vload(1, vbuf);
     float acc = __uint_as_float(0u);
     const uint16_t* st16 = reinterpret_cast<const uint16_t*>(vst);
+    const uint32_t tr_j = (uint32_t)(lane & 15) >> 2;  // row within a group of 4
+    const uint32_t tr_col = 16u * ((uint32_t)lane >> 4) + 4u * ((uint32_t)lane & 3);
     auto process = [&](uint32_t bt, u32x4_t* r) {
 #pragma unroll
       for (int i = 0; i < 8; ++i)
@@ -242,11 +248,20 @@ CATENA_DEV void attn_body(const uint16_t* __restrict__ q, const uint16_t* __rest
       const uint32_t t0 = bt * 64;
       const uint32_t rows = (len - t0) < 64u ? (len - t0) : 64u;
       if (rows == 64) {
-#pragma unroll 16
-        for (uint32_t rr = 0; rr < 64; ++rr) {
-          const float pv = sp[t0 + rr];
-          const float prod = pv * bf16_to_f32(st16[rr * 64 + lane]);
-          acc = acc + prod;
+        // Four rows of this lane's column per transposing read: lane 4j + a
+        // of a 16-lane group addresses row 4u + j, columns 16g + 4a .. +3,
+        // and lane i receives column 16g + i of rows 4u .. 4u+3; p comes
+        // four at a time (one broadcast read).  Same t-ascending chain.
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const f32x4_t p4 = *reinterpret_cast<const f32x4_t*>(sp + t0 + 4 * u);
+          const i16x4_t v4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_i16x4*)(vst + (4 * u + tr_j) * 128 + tr_col * 2));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float prod = p4[e] * bf16_to_f32((uint16_t)v4[e]);
+            acc = acc + prod;
+          }
         }
       } else {
         for (uint32_t rr = 0; rr < rows; ++rr) {
