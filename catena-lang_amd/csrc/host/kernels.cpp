@@ -134,7 +134,7 @@ int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, 
       break;
     case DecodeEpilogue::Argmax:
       if (!e.idx || m >= 0x7FFFFFFFull) return fail(CATENA_ERR_INVALID_ARGUMENT, "argmax epilogue operands");
-      if (n * gx * 12 > Device::kRowPartialBytes)
+      if (n * gx * 16 > Device::kRowPartialBytes)
         return fail(CATENA_ERR_UNSUPPORTED, "argmax epilogue over %llu column blocks",
                     (unsigned long long)gx);
       e.arg_ticket = d.misc_tickets();

@@ -30,8 +30,9 @@
 //   EPI_SILU    SwiGLU with gate / up columns interleaved in groups of 64:
 //               act[m][64*bx + c] = bf16(silu(gate) * up), as catena_silu_mul_bf16
 //   EPI_ARGMAX  LM head: per row, (last NaN, first max) of the block's 128
-//               logits, then a second ticket over the column blocks; the
-//               last block composes them in column order: tensor.argmax-f32
+//               logits as one 16-byte summary, then a second ticket over the
+//               column blocks; the last block composes them in column order:
+//               tensor.argmax-f32
 //               (catena-lang/stdlib/tensor.hex:204-227), as catena_argmax_rows_f32
 //
 // Streaming (K % 32 == 0): each wave runs a private 4-deep LDS ring of
@@ -153,7 +154,7 @@ struct DecodeEpi {
   // EPI_ARGMAX
   uint32_t* idx;            // [M]
   uint32_t* arg_ticket;     // one counter, zero between launches
-  uint32_t* arg_partials;   // [M][gridDim.x][3]
+  uint32_t* arg_partials;   // [M][gridDim.x][4]: last NaN, max value, max index, pad
 };
 
 template <int EPI>
@@ -446,6 +447,8 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
 
   if (EPI == EPI_ARGMAX) {
     const uint32_t gx = gridDim.x;
+    const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)ep.arg_partials, (short)0, (int)((uint64_t)M * gx * 16), kRsrcWord3);
     // this block's summary per row: columns n0 + lane, n0 + 64 + lane
     for (uint32_t r = wave; r < M; r += 4) {
       const float* t = tile + r * TILE_LD;
@@ -464,15 +467,16 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
       }
       fm = wave_first_max(fm);
       if (lane == 0) {
-        uint32_t* dst = ep.arg_partials + 3ull * ((uint64_t)r * gx + blockIdx.x);
-        store_coherent(dst + 0, (uint32_t)J);
-        store_coherent(dst + 1, __float_as_uint(fm.v));
-        store_coherent(dst + 2, fm.i);
+        // one 16-byte summary, stored past the XCD caches (sc1)
+        const u32x4_t v = u32x4_t{(uint32_t)J, __float_as_uint(fm.v), fm.i, 0u};
+        __builtin_amdgcn_raw_buffer_store_b128(v, ars, (int)(((uint64_t)r * gx + blockIdx.x) * 16), 0,
+                                               kCpolSc1);
       }
     }
     if (!last_arrival(ep.arg_ticket, gx, &last_flag)) return;
     // compose the gx chunk summaries of each row in column order: 16
-    // threads per row take contiguous runs, then one composes the 16 runs
+    // threads per row take contiguous runs (every summary of a run loaded
+    // in one batch of 16-byte coherent loads), then one composes the 16 runs
     __shared__ int run_j[16][16];
     __shared__ float run_v[16][16];
     __shared__ uint32_t run_i[16][16];
@@ -482,20 +486,17 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
       ArgState st{-1, FirstMax{__uint_as_float(0xFF800000u), 0xFFFFFFFFu}};
       const uint32_t c0 = sub * per < gx ? sub * per : gx;
       const uint32_t c1 = c0 + per < gx ? c0 + per : gx;
-      for (uint32_t cb = c0; cb < c1; cb += 8) {
-        uint32_t pj[8], pv[8], pi[8];
+      for (uint32_t cb = c0; cb < c1; cb += 16) {
+        u32x4_t pe[16];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const bool live = cb + u < c1;
-          const uint32_t* src = ep.arg_partials + 3ull * ((uint64_t)r * gx + (live ? cb + u : c0));
-          pj[u] = live ? load_coherent(src) : 0xFFFFFFFFu;
-          pv[u] = live ? load_coherent(src + 1) : 0u;
-          pi[u] = live ? load_coherent(src + 2) : 0xFFFFFFFFu;
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
+        for (int u = 0; u < 16; ++u)
           if (cb + u < c1)
-            st = arg_compose(st, ArgState{(int)pj[u], FirstMax{__uint_as_float(pv[u]), pi[u]}});
+            pe[u] = __builtin_amdgcn_raw_buffer_load_b128(ars, (int)(((uint64_t)r * gx + cb + u) * 16), 0,
+                                                         kCpolSc1);
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+          if (cb + u < c1)
+            st = arg_compose(st, ArgState{(int)pe[u][0], FirstMax{__uint_as_float(pe[u][1]), pe[u][2]}});
       }
       run_j[r][sub] = st.j;
       run_v[r][sub] = st.fm.v;
