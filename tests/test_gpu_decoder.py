@@ -135,6 +135,32 @@ def test_decoder_stagewise_prefill_and_steps():
     dec.close()
 
 
+class C5Step(Tiny):
+    H, F, V, B, T, L, layers = 16, 5632, 32000, 8, 4, 8, 1
+    d = H * D
+
+
+def test_decoder_c5_width_decode_step_stagewise():
+    """A decode step at the C5 model width (d 2048, SwiGLU 5632, vocab 32000,
+    batch 8: the shapes the decode-GEMM epilogues and split-K run at in the
+    benchmark), stage by stage, as above."""
+    cfg = C5Step
+    dec = ca.Decoder(cfg.d, cfg.H, cfg.F, cfg.layers, cfg.V, cfg.B, cfg.L)
+    dec.init_weights(seed=11, std=0.02)
+    w = _weights(dec, cfg)
+    tokens = np.random.default_rng(3).integers(0, cfg.V, (cfg.B, cfg.T)).astype(np.uint32)
+    nxt = ca.Buffer(cfg.B * 4)
+    say("decoder prefill (C5 width)")
+    dec.prefill(ca.Buffer.from_array(tokens), cfg.B, cfg.T, nxt)
+    prev = nxt.read(np.uint32)
+    out = ca.Buffer(cfg.B * 4)
+    say("decoder step (C5 width)")
+    dec.generate(1, out)
+    want = _check_forward(dec, cfg, w, prev, 1, cfg.T + 1)
+    assert np.array_equal(out.read(np.uint32), want)
+    dec.close()
+
+
 def _run_model(cfg, tokens, steps, seed):
     dec = ca.Decoder(cfg.d, cfg.H, cfg.F, cfg.layers, cfg.V, cfg.B, cfg.L)
     dec.init_weights(seed=seed, std=0.02)
