@@ -69,8 +69,12 @@ bool prefer_n128(uint64_t rows, uint64_t cols, int cu_count) {
 // Streaming path (K % 32 == 0, one 4-wave workgroup per CU for its 144 KiB
 // LDS ring; each wave keeps 36 KiB in flight): the fewest k groups that
 // still give every CU a workgroup, so one round of workgroups streams the
-// weight and few partials are added, but no fewer than 8 steps per wave
-// (measured on the decoder's and the C3 shapes).  Register path: ~1500 waves.
+// weight and few partials are added, but no fewer than 8 steps per wave,
+// or 2 when the weight is at most 16 MiB: such a kernel is bound by
+// latency, not by HBM, and more workgroups shorten each stream (measured:
+// 8 x 2048 x 2048 takes 7.5 us at 2 steps per wave against 9.4 us at 8;
+// the C3 shapes and the larger decoder projections are fastest at the
+// 8-step floor or within 0.5 us of it).  Register path: ~1500 waves.
 // CATENA_DECODE_KW overrides.
 uint32_t decode_kw(uint64_t n_cols, uint64_t k, int cu_count, bool regs_path) {
   const char* env = getenv("CATENA_DECODE_KW");
@@ -86,7 +90,8 @@ uint32_t decode_kw(uint64_t n_cols, uint64_t k, int cu_count, bool regs_path) {
     uint64_t groups = blocks >= (uint64_t)cu_count ? 1 : (uint64_t)cu_count / blocks;
     kw = ceil_div(k, 4 * groups);
     kw = ceil_div(kw, 32) * 32;
-    if (kw < 256) kw = 256;
+    const uint64_t min_kw = n_cols * k * 2 <= (16ull << 20) ? 64 : 256;
+    if (kw < min_kw) kw = min_kw;
   } else {
     kw = ceil_div(k * blocks, 1536);
     kw = ceil_div(kw, 32) * 32;
