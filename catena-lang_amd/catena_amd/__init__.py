@@ -44,6 +44,8 @@ INIT_NO_LOWERING = 11
 INIT_SIGNATURE_MISMATCH = 12
 INIT_DIALECT = 13
 INIT_DEVICE = 14
+INIT_HOST_MEMORY = 15
+EXEC_BAD_CALL = 20
 
 
 class CatenaError(RuntimeError):

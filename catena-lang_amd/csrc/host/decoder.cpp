@@ -210,6 +210,18 @@ int catena_mi355x_decoder_create(const catena_decoder_config_t* cfg, catena_deco
   if (c.ffn_dim % 64 != 0 || c.vocab % 8 != 0)
     return fail(CATENA_ERR_INVALID_ARGUMENT, "ffn_dim must be a multiple of 64, vocab of 8");
   if (!(c.rope_base > 1.0f)) return fail(CATENA_ERR_INVALID_ARGUMENT, "rope_base must exceed 1");
+  // sizes the kernels and tables can hold: the attention keeps one f32 score
+  // per cache position in LDS; the uniform-length lens table has
+  // (max_len + 1) x max_batch entries; every byte count below fits 64 bits
+  const size_t attn_lds = 128 * 4 + 20480 + 64 + (size_t)c.max_len * 4;
+  if (attn_lds > device().max_lds)
+    return fail(CATENA_ERR_UNSUPPORTED, "max_len %u exceeds the attention's LDS (%zu B > %zu B)",
+                c.max_len, attn_lds, device().max_lds);
+  if (c.max_batch > 4096 || c.n_heads > 4096 || c.n_layers > 4096 || c.ffn_dim > (1u << 24) ||
+      c.vocab > (1u << 26))
+    return fail(CATENA_ERR_UNSUPPORTED,
+                "decoder config beyond the supported sizes (max_batch, n_heads, n_layers <= 4096; "
+                "ffn_dim <= 2^24; vocab <= 2^26)");
 
   catena_decoder* m = new (std::nothrow) catena_decoder();
   if (!m) return fail(CATENA_ERR_OUT_OF_MEMORY, "decoder allocation");
@@ -224,6 +236,11 @@ int catena_mi355x_decoder_create(const catena_decoder_config_t* cfg, catena_deco
   };
   if ((st = alloc((uint64_t)c.vocab * d * 2, &m->embed))) return fail_out(st);
   if ((st = alloc(d * c.vocab * 2, &m->w_lm))) return fail_out(st);
+  try {
+    for (auto* v : {&m->w_qkv, &m->w_o, &m->w_gu, &m->w_down, &m->kc, &m->vc}) v->reserve(c.n_layers);
+  } catch (const std::bad_alloc&) {
+    return fail_out(fail(CATENA_ERR_OUT_OF_MEMORY, "decoder layer tables"));
+  }
   for (uint32_t l = 0; l < c.n_layers; ++l) {
     void *a = nullptr, *b = nullptr, *g = nullptr, *dn = nullptr, *k = nullptr, *v = nullptr;
     if ((st = alloc(d * 3 * d * 2, &a))) return fail_out(st);
@@ -246,11 +263,17 @@ int catena_mi355x_decoder_create(const catena_decoder_config_t* cfg, catena_deco
   if ((st = alloc(c.max_batch * 4, &m->cur_tok))) return fail_out(st);
 
   // host-computed tables: RoPE frequencies and the uniform-length lens rows
-  std::vector<float> inv(c.head_dim / 2);
+  std::vector<float> inv;
+  std::vector<uint32_t> lt;
+  try {
+    inv.resize(c.head_dim / 2);
+    lt.resize((uint64_t)(c.max_len + 1) * c.max_batch);
+  } catch (const std::bad_alloc&) {
+    return fail_out(fail(CATENA_ERR_OUT_OF_MEMORY, "host tables of the decoder"));
+  }
   if ((st = catena_mi355x_rope_inv_freq(inv.data(), c.head_dim, (double)c.rope_base)))
     return fail_out(st);
   if ((st = alloc(inv.size() * 4, &m->inv_freq))) return fail_out(st);
-  std::vector<uint32_t> lt((uint64_t)(c.max_len + 1) * c.max_batch);
   for (uint64_t t = 0; t <= c.max_len; ++t)
     for (uint32_t b = 0; b < c.max_batch; ++b) lt[t * c.max_batch + b] = (uint32_t)t;
   if ((st = alloc(lt.size() * 4, &m->lens_table))) return fail_out(st);

@@ -127,7 +127,7 @@ Device& device() {
 
 int ensure_init() {
   Device& d = device();
-  if (d.ready) return CATENA_OK;
+  if (d.ready.load(std::memory_order_acquire)) return CATENA_OK;
   return catena_mi355x_init(0);
 }
 
@@ -232,7 +232,8 @@ uint64_t pool_capacity(void* ptr) {
 }
 
 // Library-held scratch (split-K partials): grown on demand, never shrunk
-// while the library is loaded.
+// while the library is loaded.  The caller holds Device::ws_mu until it has
+// enqueued the launch that uses the block.
 int workspace(uint64_t bytes, void** out) {
   Device& d = device();
   if (bytes <= d.ws_bytes) {
@@ -262,11 +263,26 @@ using namespace catena;
 
 extern "C" {
 
+namespace {
+// Undo a partial init (stream, ticket block, loaded modules) so a later call
+// starts clean.
+int init_failed(int status, hipModule_t* mods, size_t n_mods) {
+  Device& d = device();
+  for (size_t i = 0; i < n_mods; ++i) hipModuleUnload(mods[i]);
+  if (d.small) hipFree(d.small);
+  d.small = nullptr;
+  if (d.stream) hipStreamDestroy(d.stream);
+  d.stream = nullptr;
+  for (hipFunction_t& f : d.fn) f = nullptr;
+  return status;
+}
+}  // namespace
+
 int catena_mi355x_init(int device_index) {
   Device& d = device();
   static std::mutex init_mu;
   std::lock_guard<std::mutex> g(init_mu);
-  if (d.ready) return CATENA_OK;
+  if (d.ready.load(std::memory_order_acquire)) return CATENA_OK;
   int count = 0;
   if (hipGetDeviceCount(&count) != hipSuccess || count == 0)
     return fail(CATENA_ERR_NOT_INITIALIZED, "no HIP device visible");
@@ -283,15 +299,16 @@ int catena_mi355x_init(int device_index) {
   d.max_lds = prop.sharedMemPerBlock;
   d.cu_count = prop.multiProcessorCount;
   st = hip_check(hipStreamCreateWithFlags(&d.stream, hipStreamNonBlocking), "hipStreamCreate");
-  if (st) return st;
+  if (st) return init_failed(st, nullptr, 0);
   void* small = nullptr;
   st = hip_check(hipMalloc(&small, Device::kSmallBytes), "hipMalloc(tickets)");
-  if (st) return st;
-  st = hip_check(hipMemset(small, 0, Device::kSmallBytes), "hipMemset(tickets)");
-  if (st) return st;
+  if (st) return init_failed(st, nullptr, 0);
   d.small = static_cast<unsigned char*>(small);
+  st = hip_check(hipMemset(small, 0, Device::kSmallBytes), "hipMemset(tickets)");
+  if (st) return init_failed(st, nullptr, 0);
   const std::string dir = library_dir();
   std::unordered_map<std::string, hipModule_t> modules;
+  std::vector<hipModule_t> loaded;
   for (const KernelSpec& k : kKernels) {
     auto it = modules.find(k.module);
     if (it == modules.end()) {
@@ -299,17 +316,22 @@ int catena_mi355x_init(int device_index) {
       hipModule_t m = nullptr;
       hipError_t e = hipModuleLoad(&m, path.c_str());
       if (e != hipSuccess)
-        return fail(CATENA_ERR_LOAD, "hipModuleLoad(%s): %s", path.c_str(), hipGetErrorString(e));
+        return init_failed(fail(CATENA_ERR_LOAD, "hipModuleLoad(%s): %s", path.c_str(),
+                                hipGetErrorString(e)),
+                           loaded.data(), loaded.size());
+      loaded.push_back(m);
       it = modules.emplace(k.module, m).first;
     }
     hipFunction_t f = nullptr;
     hipError_t e = hipModuleGetFunction(&f, it->second, k.symbol);
     if (e != hipSuccess)
-      return fail(CATENA_ERR_LOAD, "hipModuleGetFunction(%s): %s", k.symbol, hipGetErrorString(e));
+      return init_failed(fail(CATENA_ERR_LOAD, "hipModuleGetFunction(%s): %s", k.symbol,
+                              hipGetErrorString(e)),
+                         loaded.data(), loaded.size());
     d.fn[static_cast<int>(k.id)] = f;
   }
   d.device = device_index;
-  d.ready = true;
+  d.ready.store(true, std::memory_order_release);
   clear_error();
   return CATENA_OK;
 }
@@ -389,7 +411,7 @@ int catena_pool_stats(uint64_t* bytes_live, uint64_t* bytes_cached, uint64_t* de
 
 int catena_pool_trim(void) {
   Device& d = device();
-  if (!d.ready) return CATENA_OK;
+  if (!d.ready.load(std::memory_order_acquire)) return CATENA_OK;
   int st = hip_check(hipStreamSynchronize(d.stream), "hipStreamSynchronize");
   if (st) return st;
   Pool& p = pool();

@@ -4,7 +4,9 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdint>
+#include <mutex>
 
 #include "catena_mi355x.h"
 
@@ -69,7 +71,11 @@ enum class KernelId : int {
 };
 
 struct Device {
-  bool ready = false;
+  // set (release) once init has finished; read (acquire) by every entry point
+  std::atomic<bool> ready{false};
+  // held from workspace() through the launch that uses it, so no thread can
+  // launch with a block another thread is replacing
+  std::mutex ws_mu;
   int device = -1;
   hipStream_t stream = nullptr;
   size_t max_lds = 0;

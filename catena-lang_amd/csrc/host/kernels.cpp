@@ -148,6 +148,7 @@ int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, 
       break;
   }
   float* P = nullptr;
+  std::lock_guard<std::mutex> ws_guard(d.ws_mu);  // the workspace block stays ours until launched
   if (S > 1) {
     // the partials are addressed through one buffer descriptor with 32-bit
     // byte offsets

@@ -13,6 +13,7 @@
 // the rest (e.g. matmul-2x2-via-mem, sum-u64, dot-u64).
 #include <cctype>
 #include <cstring>
+#include <new>
 #include <memory>
 #include <string>
 #include <vector>
@@ -185,8 +186,10 @@ struct Node {
 };
 
 struct Reader {
+  static constexpr int kMaxDepth = 4096;  // nesting bound (the reader recurses)
   const char* s;
   size_t i = 0, n;
+  int depth = 0;
   std::string err;
   explicit Reader(const char* src) : s(src), n(strlen(src)) {}
   void skip() {
@@ -206,6 +209,10 @@ struct Reader {
     if (i >= n) return false;
     char c = s[i];
     if (c == '(' || c == '[' || c == '{') {
+      if (depth >= kMaxDepth) {
+        err = "brackets nested too deeply";
+        return false;
+      }
       ++i;
       out.open = c;
       for (;;) {
@@ -223,7 +230,10 @@ struct Reader {
           return false;
         }
         Node k;
-        if (!read(k)) {
+        ++depth;
+        const bool ok = read(k);
+        --depth;
+        if (!ok) {
           if (err.empty()) err = "unexpected end";
           return false;
         }
@@ -350,10 +360,28 @@ struct catena_runtime {
 
 extern "C" {
 
+namespace {
+int from_sources(const char* const* sources, size_t n_sources, const char* dialect,
+                 catena_runtime_t** out);
+}
+
 int catena_runtime_from_sources(const char* const* sources, size_t n_sources, const char* dialect,
                                 catena_runtime_t** out) {
-  if (!out) return fail(CATENA_ERR_INVALID_ARGUMENT, "out is NULL");
+  if (!out) return fail(CATENA_EXEC_BAD_CALL, "out is NULL");
   *out = nullptr;
+  if (n_sources > 0 && !sources) return fail(CATENA_EXEC_BAD_CALL, "sources is NULL");
+  try {
+    return from_sources(sources, n_sources, dialect, out);
+  } catch (const std::bad_alloc&) {
+    return fail(CATENA_INIT_HOST_MEMORY, "out of host memory while reading sources");
+  }
+}
+
+}  // extern "C"
+
+namespace {
+int from_sources(const char* const* sources, size_t n_sources, const char* dialect,
+                 catena_runtime_t** out) {
   // GpuDialect (catena-lang/src/codegen/mod.rs:50-54): only Hip is served.
   if (!dialect || strcmp(dialect, "hip") != 0)
     return fail(CATENA_INIT_DIALECT, "GPU dialect `%s` is not supported; expected `hip`",
@@ -392,13 +420,16 @@ int catena_runtime_from_sources(const char* const* sources, size_t n_sources, co
   *out = rt.release();
   return CATENA_OK;
 }
+}  // namespace
+
+extern "C" {
 
 void catena_runtime_destroy(catena_runtime_t* rt) { delete rt; }
 
 int catena_runtime_exec(catena_runtime_t* rt, const char* name, const catena_value_t* args,
                         size_t n_args, catena_value_t* outs, size_t n_outs) {
   g_detail = ErrDetail{};
-  if (!rt || !name) return fail(CATENA_ERR_INVALID_ARGUMENT, "null runtime or name");
+  if (!rt || !name) return fail(CATENA_EXEC_BAD_CALL, "null runtime or name");
   const Program* p = rt->find(name);
   if (!p)
     return exec_fail(CATENA_EXEC_UNKNOWN_SOURCE_FUNCTION, -1, -1, -1,
@@ -410,6 +441,8 @@ int catena_runtime_exec(catena_runtime_t* rt, const char* name, const catena_val
   if (l.outputs.size() != n_outs)
     return exec_fail(CATENA_EXEC_OUTPUT_ARITY_MISMATCH, -1, (int64_t)l.outputs.size(),
                      (int64_t)n_outs, "Function '%s' output arity mismatch", name);
+  if ((n_args > 0 && !args) || (n_outs > 0 && !outs))
+    return fail(CATENA_EXEC_BAD_CALL, "null argument or output array");
   for (size_t i = 0; i < n_args; ++i)
     if (args[i].kind != l.inputs[i])
       return exec_fail(CATENA_EXEC_TYPE_MISMATCH, (int64_t)i, (int64_t)l.inputs[i],

@@ -296,10 +296,13 @@ typedef struct catena_decoder_config {
   uint32_t ffn_dim;  /* SwiGLU width F */
   uint32_t n_layers;
   uint32_t vocab;
-  uint32_t max_batch;
-  uint32_t max_len; /* cache positions per sequence */
+  uint32_t max_batch; /* <= 4096 */
+  uint32_t max_len;   /* cache positions per sequence; the attention holds one
+                         f32 score per position in LDS: <= 35,696 on gfx950 */
   float rope_base;
 } catena_decoder_config_t;
+/* create() rejects (CATENA_ERR_UNSUPPORTED) n_heads or n_layers > 4096,
+ * ffn_dim > 2^24, vocab > 2^26 and the limits above. */
 
 typedef enum catena_decoder_tensor {
   CATENA_DEC_EMBED = 0, /* [vocab][d] bf16 */
@@ -382,7 +385,11 @@ typedef enum catena_exec_status {
   CATENA_INIT_NO_LOWERING = 11,
   CATENA_INIT_SIGNATURE_MISMATCH = 12,
   CATENA_INIT_DIALECT = 13,
-  CATENA_INIT_DEVICE = 14
+  CATENA_INIT_DEVICE = 14,
+  /* not reference error kinds: host memory ran out while reading sources;
+   * a NULL runtime, name, source list, argument or output array */
+  CATENA_INIT_HOST_MEMORY = 15,
+  CATENA_EXEC_BAD_CALL = 20
 } catena_exec_status_t;
 
 typedef struct catena_runtime catena_runtime_t;

@@ -114,6 +114,28 @@ def test_runtime_rejects_cuda_dialect_and_bad_source():
     assert e.value.status == ca.INIT_PARSE
 
 
+def test_runtime_bounds_bracket_nesting():
+    """Nesting deeper than the reader's bound is a parse error, not a stack
+    overflow."""
+    deep = "(" * 100000 + ")" * 100000
+    with pytest.raises(ca.ExecError) as e:
+        ca.Runtime([deep])
+    assert e.value.status == ca.INIT_PARSE
+    ok = "(def program nn.softmax : " + "(" * 50 + "cap.own mem" + ")" * 50 + " -> (cap.own mem) = x)"
+    ca.Runtime([ok])  # moderate nesting still reads
+
+
+def test_exec_rejects_null_argument_array():
+    """n_args > 0 with a NULL array, or a NULL runtime, is refused before any
+    dereference, with a status outside the reference's error kinds."""
+    rt = ca.Runtime([MATMUL_DECL])
+    L = ca.lib()
+    outs = (ca.Value * 1)()
+    st = L.catena_runtime_exec(rt._h, b"math.exp-approx", None, 1, outs, 1)
+    assert st == ca.EXEC_BAD_CALL
+    assert L.catena_runtime_exec(None, b"math.exp-approx", None, 0, outs, 1) == ca.EXEC_BAD_CALL
+
+
 def test_runtime_signature_mismatch():
     bad = "(def program nn.softmax : (f32 val) -> (cap.own mem) = x)"
     with pytest.raises(ca.ExecError) as e:

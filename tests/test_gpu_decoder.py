@@ -161,6 +161,15 @@ def test_decoder_c5_width_decode_step_stagewise():
     dec.close()
 
 
+def test_decoder_create_rejects_unsupported_configs():
+    """A cache longer than the attention's LDS holds, or a batch beyond the
+    lens table's bound, fails at create with CATENA_ERR_UNSUPPORTED."""
+    with pytest.raises(ca.CatenaError):
+        ca.Decoder(256, 2, 512, 1, 512, 2, 40000)
+    with pytest.raises(ca.CatenaError):
+        ca.Decoder(256, 2, 512, 1, 512, 5000, 16)
+
+
 def _run_model(cfg, tokens, steps, seed):
     dec = ca.Decoder(cfg.d, cfg.H, cfg.F, cfg.layers, cfg.V, cfg.B, cfg.L)
     dec.init_weights(seed=seed, std=0.02)
