@@ -285,8 +285,12 @@ def cpu_baseline_attention(q, k, v, heads: int, threads: int):
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=100)
+    # The first ~8 ms of back-to-back GEMMs cross a power-management
+    # transient (a trace shows launches 18-60 stretching from 108 us to 140
+    # us and back to 120 us); 100 warmup launches (~11 ms) put the timed
+    # region in the steady state (109 us per launch).
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["gemm", "core", "decoder", "all"], default="all",
                     help="gemm: the headline GEMM only; core: + decode attention and decode "
