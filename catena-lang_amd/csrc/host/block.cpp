@@ -86,7 +86,7 @@ int catena_mi355x_attn_causal_bf16(const uint16_t* q, const uint16_t* k, const u
     return launch(out_f32 ? KernelId::AttnPrefillD128F32 : KernelId::AttnPrefillD128Bf16,
                   dim3((unsigned)grid), dim3(256), lds_pf, pargs);
   }
-  const size_t lds = 128 * 4 + 20480 + 64 + (size_t)max_len * 4;
+  const size_t lds = attn_lds_bytes(max_len);
   if (lds > device().max_lds)
     return fail(CATENA_ERR_UNSUPPORTED, "max_len %u needs %zu B of LDS (device has %zu)", max_len,
                 lds, device().max_lds);

@@ -213,7 +213,7 @@ int catena_mi355x_decoder_create(const catena_decoder_config_t* cfg, catena_deco
   // sizes the kernels and tables can hold: the attention keeps one f32 score
   // per cache position in LDS; the uniform-length lens table has
   // (max_len + 1) x max_batch entries; every byte count below fits 64 bits
-  const size_t attn_lds = 128 * 4 + 20480 + 64 + (size_t)c.max_len * 4;
+  const size_t attn_lds = attn_lds_bytes(c.max_len);
   if (attn_lds > device().max_lds)
     return fail(CATENA_ERR_UNSUPPORTED, "max_len %u exceeds the attention's LDS (%zu B > %zu B)",
                 c.max_len, attn_lds, device().max_lds);

@@ -100,6 +100,11 @@ struct Device {
   void* row_partials() const { return misc_tickets() + kTicketsMisc; }
 };
 
+// LDS of the one-query attention kernels (attn_decode.hip): q in f32, the
+// K / V staging area, reduction slots, then one f32 score per position.
+constexpr size_t kAttnLdsFixed = 128 * 4 + 16384 + 64;
+inline size_t attn_lds_bytes(uint32_t max_len) { return kAttnLdsFixed + (size_t)max_len * 4; }
+
 Device& device();
 int ensure_init();
 int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));

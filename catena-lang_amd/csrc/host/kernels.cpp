@@ -266,7 +266,7 @@ int catena_mi355x_attn_decode_bf16(const uint16_t* q, const uint16_t* k, const u
     return fail(CATENA_ERR_INVALID_ARGUMENT, "K/V caches must be 16-byte aligned");
   if (bh > 0x7FFFFFFFu) return fail(CATENA_ERR_UNSUPPORTED, "too many heads");
   Device& d = device();
-  const size_t lds = 128 * 4 + 20480 + 64 + (size_t)max_len * 4;
+  const size_t lds = attn_lds_bytes(max_len);
   if (lds > d.max_lds)
     return fail(CATENA_ERR_UNSUPPORTED, "max_len %u needs %zu B of LDS (device has %zu)", max_len,
                 lds, d.max_lds);

@@ -36,9 +36,15 @@
 
 namespace {
 constexpr int D = 128;
-constexpr int KSTAGE_ROW = 80;                // bytes: 64 B of data + 16 B pad
-constexpr int KSTAGE_WAVE = 64 * KSTAGE_ROW;  // 5120 B per wave
-constexpr int STAGE_BYTES = 4 * KSTAGE_WAVE;  // 20480 B (V pass uses 2 x 8192)
+// K stage: per wave [64 rows][64 B]; 16-byte chunk c of row t sits at
+// position c ^ ((t >> 2) & 3).  Measured with SQ_LDS_BANK_CONFLICT on
+// gfx950, both the staging writes (4 lanes per row) and the read-back (lane
+// t: row t) are then conflict-free; the earlier 80-byte padded rows made
+// every staging write take 3x its LDS cycles.
+constexpr int KSTAGE_ROW = 64;
+constexpr int KSTAGE_WAVE = 64 * KSTAGE_ROW;  // 4096 B per wave
+constexpr int STAGE_BYTES = 4 * KSTAGE_WAVE;  // 16384 B (V pass uses 2 x 8192)
+CATENA_DEV uint32_t kswz(uint32_t row, uint32_t chunk) { return 16u * (chunk ^ ((row >> 2) & 3u)); }
 
 CATENA_DEV void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -133,14 +139,14 @@ CATENA_DEV void attn_body(const uint16_t* __restrict__ q, const uint16_t* __rest
       const uint32_t seg = step & 3;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        *reinterpret_cast<u32x4_t*>(st + (lrow + 16 * i) * KSTAGE_ROW + lchunk * 16) = r[i];
+        *reinterpret_cast<u32x4_t*>(st + (lrow + 16 * i) * KSTAGE_ROW + kswz(lrow, lchunk)) = r[i];
       wave_sync();
       if (step + 2 < steps) gload(step + 2, r);
       if (seg == 0) acc = __uint_as_float(0u);
       const unsigned char* myrow = st + lane * KSTAGE_ROW;
 #pragma unroll
       for (int ch = 0; ch < 4; ++ch) {
-        const u32x4_t kv = *reinterpret_cast<const u32x4_t*>(myrow + ch * 16);
+        const u32x4_t kv = *reinterpret_cast<const u32x4_t*>(myrow + kswz(lane, ch));
         const f32x4_t q0 = *reinterpret_cast<const f32x4_t*>(qf + seg * 32 + ch * 8);
         const f32x4_t q1 = *reinterpret_cast<const f32x4_t*>(qf + seg * 32 + ch * 8 + 4);
         float p;

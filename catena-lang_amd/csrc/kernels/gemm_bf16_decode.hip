@@ -103,7 +103,7 @@ typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
 
 // LDS ring of the streaming path: per wave RING stages, each a W slab
 // [32 k][128 cols] (8 KiB, 256-byte rows) and an X slab [16 rows][32 k]
-// (1 KiB).  16-byte chunk p of W row r holds global chunk p ^ hW(r), which
+// (1 KiB, chunks swizzled by row bits 1-2).  16-byte chunk p of W row r holds global chunk p ^ hW(r), which
 // makes the transposing fragment reads (16 rows x 32 bytes per
 // instruction) hit every bank pair once.
 constexpr int RING = 4;
@@ -209,8 +209,12 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
       woff[i] = (uint32_t)(((uint64_t)r * N + 8 * q) * 2);
       wlive[i] = n0 + 8 * q < N;
     }
-    // X slab: lane l fetches row l / 4, 16-byte chunk l % 4
-    const uint32_t xr = lane >> 2, xq = lane & 3;
+    // X slab: lane l fetches row l / 4 into slot l % 4, which holds the
+    // row's global chunk (l % 4) ^ ((row >> 1) & 3): the fragment read
+    // (lane 16 G + s: row s, chunk G) is then free of LDS bank conflicts
+    // (measured with SQ_LDS_BANK_CONFLICT; unswizzled it costs 8 LDS cycles
+    // per read instead of 4)
+    const uint32_t xr = lane >> 2, xq = (uint32_t)(lane & 3) ^ ((xr >> 1) & 3u);
     const bool xl = xr < M;
     const char* wsrc = reinterpret_cast<const char*>(W) + (kw0 * N + n0) * 2;
     const char* xsrc = reinterpret_cast<const char*>(X) + ((uint64_t)xr * K + kw0 + 8 * xq) * 2;
@@ -226,7 +230,7 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
     for (uint32_t t = 0; t < pre; ++t) issue(t, (int)t);
     // fragment read addresses inside a stage
     const int G = lane >> 4, sl = lane & 15;
-    const uint32_t xa_off = W_SLAB + ((uint32_t)sl * 4 + (uint32_t)G) * 16;
+    const uint32_t xa_off = W_SLAB + ((uint32_t)sl * 4 + ((uint32_t)G ^ (((uint32_t)sl >> 1) & 3u))) * 16;
     const uint32_t brow = 8 * G + (sl >> 2);
     const uint32_t hb = hW(brow);
     uint32_t b_off[8];

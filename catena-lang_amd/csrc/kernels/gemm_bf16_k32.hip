@@ -31,7 +31,11 @@
 // LDS layout: A stages [S][256][32] then B stages [S][32][BN], so every read
 // offset from the per-lane bases fits a DS instruction's immediate.
 // Swizzles (conflict-free through the direct-to-LDS write layout):
-//   A [256][64 B]:   LDS chunk p of row r holds global chunk p ^ ((r >> 2) & 3);
+//   A [256][64 B]:   LDS chunk p of row r holds global chunk p ^ ((r >> 1) & 3).
+//                    Measured with SQ_LDS_BANK_CONFLICT on gfx950, the
+//                    fragment read (lane 16 G + s: row s, chunk G) costs 8
+//                    LDS cycles per ds_read_b128 with p ^ ((r >> 2) & 3) or
+//                    no swizzle and the conflict-free 4 with this one;
 //   B [32][2*BN B]:  LDS chunk p of row k holds global chunk p ^ hB(k),
 //                    hB(k) = 2 * ((k & 3) | ((k >> 3) & 1) << 2)  (row bit 4
 //                    unused, so a load 16 rows further shares the lane offset).
@@ -107,7 +111,7 @@ CATENA_DEV void gemm_k32_body(const uint16_t* __restrict__ A, const uint16_t* __
   uint32_t aoff, boff;
   {
     const uint32_t r = 32 * wave + (lane >> 2);
-    const uint32_t q = (uint32_t)(lane & 3) ^ ((r >> 2) & 3u);
+    const uint32_t q = (uint32_t)(lane & 3) ^ ((r >> 1) & 3u);
     aoff = (uint32_t)((r * K + 8 * q) * 2);
     const uint32_t kr = (64 / B_LANES) * wave + (uint32_t)lane / B_LANES;
     const uint32_t qb = (uint32_t)(lane % B_LANES) ^ hB(kr);
@@ -140,12 +144,12 @@ CATENA_DEV void gemm_k32_body(const uint16_t* __restrict__ A, const uint16_t* __
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   // Fragment read bases.  A: lane (G, s) reads row wm*16*WI + 16 i + s, chunk
-  // G ^ ((s >> 2) & 3) (row + 16 i leaves the swizzle unchanged).  B: two
+  // G ^ ((s >> 1) & 3) (row + 16 i leaves the swizzle unchanged).  B: two
   // ds_read_b64_tr_b16 per 32x16 block (rows 8G + s/4 and +4, columns
   // 16 j + 4 (s % 4)), so lane i of a 16-lane group receives 4 consecutive k
   // of one column, matching A's k order.
   const int G = lane >> 4, s = lane & 15;
-  const uint32_t a_lds = (wm * 16 * WI + s) * BK * 2 + 16 * ((uint32_t)G ^ ((uint32_t)(s >> 2) & 3u));
+  const uint32_t a_lds = (wm * 16 * WI + s) * BK * 2 + 16 * ((uint32_t)G ^ ((uint32_t)(s >> 1) & 3u));
   const uint32_t b_krow = 8 * G + (s >> 2);
   const uint32_t hb = hB(b_krow);
   uint32_t b_lds[4];

@@ -298,7 +298,7 @@ typedef struct catena_decoder_config {
   uint32_t vocab;
   uint32_t max_batch; /* <= 4096 */
   uint32_t max_len;   /* cache positions per sequence; the attention holds one
-                         f32 score per position in LDS: <= 35,696 on gfx950 */
+                         f32 score per position in LDS: <= 36,720 on gfx950 */
   float rope_base;
 } catena_decoder_config_t;
 /* create() rejects (CATENA_ERR_UNSUPPORTED) n_heads or n_layers > 4096,
