@@ -17,6 +17,7 @@ sequential arithmetic restated in C, gcc -O2 -ffp-contract=off) on a bounded
 sample of the same workload on this host.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+                       [--only gemm|core|decoder|all] [--no-ceilings]
 """
 from __future__ import annotations
 
@@ -282,19 +283,95 @@ def cpu_baseline_attention(q, k, v, heads: int, threads: int):
             "sample": f"{nbh} of 1024 (batch, head) slices, {dt:.1f} s"}
 
 
+def bench_ceilings(ev: HipEvents) -> dict:
+    """Measured ceilings of the resources the hot kernels are bound by, from
+    the measurement kernels in csrc/kernels/calibrate.hip (a code object the
+    library itself never loads): bf16 MFMA throughput and clock on random
+    operands (registers only, then fed from LDS at the bf16 GEMM's read
+    ratio), plain HBM read rate, and the 4096^2 bf16 C-store write rate."""
+    hip = ctypes.CDLL("libamdhip64.so")
+    vp = ctypes.c_void_p
+
+    def ck(e, what):
+        if e != 0:
+            raise RuntimeError(f"{what}: hip error {e}")
+
+    path = os.path.join(ca.LIB_DIR, "calibrate.co")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: run `python catena-lang_amd/build.py` first")
+    mod = vp()
+    ck(hip.hipModuleLoad(ctypes.byref(mod), path.encode()), "hipModuleLoad calibrate.co")
+    stream = vp(ca.stream())
+
+    def kernel(name):
+        f = vp()
+        ck(hip.hipModuleGetFunction(ctypes.byref(f), mod, name.encode()), name)
+        return f
+
+    def launcher(f, grid, block, vals):
+        argv = (vp * len(vals))(*[ctypes.cast(ctypes.pointer(v), vp) for v in vals])
+
+        def go():
+            ck(hip.hipModuleLaunchKernel(f, grid, 1, 1, block, 1, 1, 0, stream, argv, None), "launch")
+        go.keep = (vals, argv)
+        return go
+
+    def time_us(go, warmup, launches):
+        for _ in range(warmup):
+            go()
+        ca.synchronize()
+        ev.start()
+        for _ in range(launches):
+            go()
+        return ev.stop_ms() / launches * 1e3
+
+    out = {}
+    grid, block, iters = 256, 512, 400
+    obuf, cyc = ca.Buffer(grid * block * 4), ca.Buffer(grid * (block // 64) * 16)
+    flop = grid * (block // 64) * iters * 32 * 16 * 16 * 32 * 2
+    for key, name in (("mfma_bf16_random_operands", "catena_calib_mfma_bf16"),
+                      ("mfma_bf16_lds_fed", "catena_calib_mfma_lds_bf16")):
+        go = launcher(kernel(name), grid, block,
+                      [vp(obuf.ptr), vp(cyc.ptr), ctypes.c_int(iters), ctypes.c_uint32(0x9E3779B9)])
+        us = time_us(go, 300, 100)
+        c = cyc.read(np.uint64).astype(np.float64).reshape(-1, 2)
+        clk = c[:, 0] / (c[:, 1] / 100e6) / 1e9
+        out[key] = {"TFLOP/s": round(flop / us / 1e6, 1), "frac_of_peak": round(flop / us / 1e6 / PEAK_BF16_TFLOPS, 4),
+                    "clock_GHz_median": round(float(np.median(clk)), 3), "us_per_launch": round(us, 2)}
+    nbytes = 2 << 30
+    src, flag = ca.Buffer(nbytes), ca.Buffer(64)
+    ca.fill_uniform_f32(src, nbytes // 4, 11, 0)
+    rgrid = 4096
+    go = launcher(kernel("catena_calib_read"), rgrid, 512,
+                  [vp(src.ptr), ctypes.c_uint64(nbytes // 16 // rgrid), vp(flag.ptr), ctypes.c_uint32(0x12345678)])
+    us = time_us(go, 5, 50)
+    out["hbm_read"] = {"GB/s": round(nbytes / us / 1e3, 1), "bytes": nbytes, "us_per_launch": round(us, 2)}
+    del src
+    cbytes = 4096 * 4096 * 2
+    cbuf = ca.Buffer(cbytes)
+    go = launcher(kernel("catena_calib_write_tile"), 256, 512, [vp(cbuf.ptr), ctypes.c_uint32(7)])
+    us = time_us(go, 50, 200)
+    out["c_store_4096sq_bf16"] = {"GB/s": round(cbytes / us / 1e3, 1), "bytes": cbytes, "us_per_launch": round(us, 2)}
+    ck(hip.hipModuleUnload(mod), "hipModuleUnload")
+    return out
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    # The first ~8 ms of back-to-back GEMMs cross a power-management
-    # transient (a trace shows launches 18-60 stretching from 108 us to 140
-    # us and back to 120 us); 100 warmup launches (~11 ms) put the timed
-    # region in the steady state (109 us per launch).
+    # Back-to-back GEMMs cross a power-management transient: in a trace the
+    # first ~15 launches take ~105 us, launches 20-40 129-133 us, decaying to
+    # 103-106 us by launch ~120; 100 warmup launches (~12 ms) put most of the
+    # timed region in the steady state.
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["gemm", "core", "decoder", "all"], default="all",
                     help="gemm: the headline GEMM only; core: + decode attention and decode "
                          "GEMMs; decoder: + the C5 decoder only; all: everything")
+    ap.add_argument("--no-ceilings", action="store_true",
+                    help="skip the measured ceilings (MFMA on random operands, LDS-fed MFMA, "
+                         "HBM read, C-store write), run after everything else")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also launch the plain copy kernel on 1 GiB (known traffic) three "
                          "times, for scaling FETCH_SIZE / WRITE_SIZE counter readings")
@@ -340,6 +417,9 @@ def main(argv=None) -> int:
         ca.synchronize()
         print(f"[bench] copy calibration: 3 x catena_copy_16b over {nbytes} B", file=sys.stderr,
               flush=True)
+    if not args.no_ceilings:
+        print("[bench] ceilings (calibrate.hip)", file=sys.stderr, flush=True)
+        extra["ceilings"] = bench_ceilings(ev)
     cpu = None
     if not args.no_cpu_baseline:
         threads = max(1, min(16, len(os.sched_getaffinity(0))))
