@@ -58,17 +58,21 @@ def _weights(dec, cfg):
 
 def _check_forward(dec, cfg, w, tokens, tq, cache_len):
     """Check the last forward (rows = B * tq, cache holding cache_len positions
-    after it) stage by stage; returns the GPU's next tokens."""
+    after it) stage by stage, through the last layer (whose input x is the
+    embedding with one layer, else the previous layer's residual stream,
+    checked through its RMSNorm); returns the GPU's next tokens."""
     d, F, B, H = cfg.d, cfg.F, cfg.B, cfg.H
     R = B * tq
+    lay = cfg.layers - 1
     lens = np.full(B, cache_len, np.int64)
-    rd = lambda which, dt, shape: dec.read(which, dt).reshape(shape)  # noqa: E731
+    rd = lambda which, dt, shape: dec.read(which, dt, layer=lay).reshape(shape)  # noqa: E731
     X = rd(ca.DEC_X, np.float32, (R, d))
-    _bitwise(X, as_f32(w["embed"][np.asarray(tokens, np.int64).ravel()]))
+    if lay == 0:
+        _bitwise(X, as_f32(w["embed"][np.asarray(tokens, np.int64).ravel()]))
     XN = rd(ca.DEC_XN, np.uint16, (R, d))
     _bitwise(XN, od.residual_rmsnorm_bf16(X)[1])
     QKV = rd(ca.DEC_QKV, np.float32, (R, 3 * d))
-    gemm_within_bound(XN, w["w_qkv"][0], QKV)
+    gemm_within_bound(XN, w["w_qkv"][lay], QKV)
     inv = dec.read(ca.DEC_INV_FREQ, np.float32)
     q, k, v, pos = od.rope_qkv(QKV, inv, lens, B, tq, H, D)
     Q = rd(ca.DEC_Q, np.uint16, (R, d))
@@ -82,18 +86,18 @@ def _check_forward(dec, cfg, w, tokens, tq, cache_len):
     o = od.attn_causal(Q, kc, vc, lens, B, tq, H, D, float(np.float32(1 / np.sqrt(D))))
     _bitwise(ATT, oracle.f32_to_bf16_bits_np(o))
     AP = rd(ca.DEC_ATTN_PROJ, np.float32, (R, d))
-    gemm_within_bound(ATT, w["w_o"][0], AP)
+    gemm_within_bound(ATT, w["w_o"][lay], AP)
     Hh = rd(ca.DEC_H, np.float32, (R, d))
     h, hn = od.residual_rmsnorm_bf16(X, AP)
     _bitwise(Hh, h)
     HN = rd(ca.DEC_HN, np.uint16, (R, d))
     _bitwise(HN, hn)
     GU = rd(ca.DEC_GU, np.float32, (R, 2 * F))
-    gemm_within_bound(HN, w["w_gu"][0], GU)
+    gemm_within_bound(HN, w["w_gu"][lay], GU)
     ACT = rd(ca.DEC_ACT, np.uint16, (R, F))
     _bitwise(ACT, od.silu_mul_bf16(GU, F, 64))
     FO = rd(ca.DEC_FFN_OUT, np.float32, (R, d))
-    gemm_within_bound(ACT, w["w_down"][0], FO)
+    gemm_within_bound(ACT, w["w_down"][lay], FO)
     last = np.arange(B) * tq + (tq - 1)
     fh, fxn = od.residual_rmsnorm_bf16(Hh[last], FO[last])
     _bitwise(rd(ca.DEC_FINAL_H, np.float32, (B, d)), fh)
@@ -158,6 +162,37 @@ def test_decoder_c5_width_decode_step_stagewise():
     dec.generate(1, out)
     want = _check_forward(dec, cfg, w, prev, 1, cfg.T + 1)
     assert np.array_equal(out.read(np.uint32), want)
+    dec.close()
+
+
+class Wide2L(Tiny):
+    H, F, V, T, L, layers = 16, 512, 512, 2, 6, 2
+    d = H * D
+
+
+@pytest.mark.parametrize("batch", [3, 16])
+def test_decoder_two_layers_decode_steps_stagewise(batch):
+    """Decode steps at d 2048 with two layers (the second layer's input is the
+    first one's residual stream, checked through its RMSNorm), stage by stage
+    as above, for a ragged batch and the largest batch the decode-GEMM
+    epilogues take (16 rows)."""
+    cfg = type("Wide2LBatch", (Wide2L,), {"B": batch})
+    dec = ca.Decoder(cfg.d, cfg.H, cfg.F, cfg.layers, cfg.V, cfg.B, cfg.L)
+    dec.init_weights(seed=13, std=0.02)
+    w = _weights(dec, cfg)
+    tokens = np.random.default_rng(4).integers(0, cfg.V, (cfg.B, cfg.T)).astype(np.uint32)
+    nxt = ca.Buffer(cfg.B * 4)
+    say(f"decoder prefill (d 2048, two layers, batch {batch})")
+    dec.prefill(ca.Buffer.from_array(tokens), cfg.B, cfg.T, nxt)
+    prev = nxt.read(np.uint32)
+    for s_ in range(2):
+        out = ca.Buffer(cfg.B * 4)
+        say(f"decoder step {s_} (d 2048, two layers, batch {batch})")
+        dec.generate(1, out)
+        want = _check_forward(dec, cfg, w, prev, 1, cfg.T + s_ + 1)
+        got = out.read(np.uint32)
+        assert np.array_equal(got, want)
+        prev = got
     dec.close()
 
 
