@@ -37,15 +37,6 @@ constexpr int ST = QB + 1;           // sT row stride (floats)
 constexpr int VBLK = 64;             // keys per V stage
 constexpr int VSTAGE = VBLK * D * 2; // bytes (bf16)
 
-CATENA_DEV int wave_max_i32(int v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const int o = __shfl_xor(v, off, 64);
-    v = o > v ? o : v;
-  }
-  return v;
-}
-
 CATENA_DEV FirstMax wave_first_max(FirstMax a) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
@@ -146,46 +137,123 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
   __syncthreads();
 
   // ---------------------------------------------------------------- max per query
-  for (int i = wave; i < QB; i += 4) {
-    const uint32_t len = qlen[i];
-    int lastnan = -1;
-    for (uint32_t t = lane; t < len; t += 64)
-      if (sT[t * ST + i] != sT[t * ST + i]) lastnan = (int)t;
-    const int J = wave_max_i32(lastnan);
-    FirstMax fm{__uint_as_float(0xFF800000u), 0xFFFFFFFFu};
-    for (uint32_t t = lane; t < len; t += 64)
-      if ((int)t > J) fm = first_max_combine(fm, FirstMax{sT[t * ST + i], t});
-    fm = wave_first_max(fm);
-    if (lane == 0) {
-      float mx;
-      if (len > 0 && J == (int)len - 1)
-        mx = sT[(len - 1) * ST + i];
-      else
-        mx = fm.i == 0xFFFFFFFFu ? __uint_as_float(0xFF800000u) : fm.v;
-      red[i] = mx;
+  // Wave w takes queries w, w + 4, w + 8, w + 12 in one pass over the
+  // scores: per lane and query, the last NaN position and the first max of
+  // every value the lane read (positions ascending).  Without a NaN in the
+  // query's prefix, the first-max combine of those over the lanes
+  // (associative and commutative) is the sequential fold's result, as in the
+  // two-pass form; a query with a NaN takes that form (first max after the
+  // last NaN, or the NaN itself when it is the last position).
+  {
+    uint32_t len4[4], lmx = 0;
+    int ln4[4];
+    FirstMax fm4[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      len4[u] = qlen[wave + 4 * u];
+      lmx = len4[u] > lmx ? len4[u] : lmx;
+      ln4[u] = -1;
+      fm4[u] = FirstMax{__uint_as_float(0xFF800000u), 0xFFFFFFFFu};
+    }
+    for (uint32_t t = lane; t < lmx; t += 64) {
+      const float* row = sT + t * ST + wave;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (t < len4[u]) {
+          const float sv = row[4 * u];
+          if (sv != sv) ln4[u] = (int)t;
+          fm4[u] = first_max_combine(fm4[u], FirstMax{sv, t});
+        }
+      }
+    }
+    // the four queries' butterflies interleaved (independent shuffle chains)
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int o = __shfl_xor(ln4[u], off, 64);
+        ln4[u] = o > ln4[u] ? o : ln4[u];
+        FirstMax b;
+        b.v = __shfl_xor(fm4[u].v, off, 64);
+        b.i = (uint32_t)__shfl_xor((int)fm4[u].i, off, 64);
+        fm4[u] = first_max_combine(fm4[u], b);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = wave + 4 * u;
+      const uint32_t len = len4[u];
+      const int J = ln4[u];
+      FirstMax fm;
+      if (J < 0) {
+        fm = fm4[u];
+      } else {
+        fm = FirstMax{__uint_as_float(0xFF800000u), 0xFFFFFFFFu};
+        for (uint32_t t = lane; t < len; t += 64)
+          if ((int)t > J) fm = first_max_combine(fm, FirstMax{sT[t * ST + i], t});
+        fm = wave_first_max(fm);
+      }
+      if (lane == 0) {
+        float mx;
+        if (len > 0 && J == (int)len - 1)
+          mx = sT[(len - 1) * ST + i];
+        else
+          mx = fm.i == 0xFFFFFFFFu ? __uint_as_float(0xFF800000u) : fm.v;
+        red[i] = mx;
+      }
     }
   }
   __syncthreads();
 
   // ---------------------------------------------------------------- exp~
-  for (uint32_t e = tid; e < lmax * QB; e += 256) {
-    const uint32_t t = e / QB, i = e % QB;
-    if (t < qlen[i]) {
-      const float shifted = sT[t * ST + i] - red[i];
-      sT[t * ST + i] = exp_approx(shifted);
+  // four elements per thread in flight (each element's arithmetic unchanged)
+  for (uint32_t e0 = tid; e0 < lmax * QB; e0 += 4 * 256) {
+    float sv[4], mv[4];
+    bool live[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t e = e0 + 256u * u, t = e / QB, i = e % QB;
+      live[u] = e < lmax * QB && t < qlen[i];
+      sv[u] = live[u] ? sT[t * ST + i] : 0.0f;
+      mv[u] = red[i];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t e = e0 + 256u * u, t = e / QB, i = e % QB;
+      if (live[u]) {
+        const float shifted = sv[u] - mv[u];
+        sT[t * ST + i] = exp_approx(shifted);
+      }
     }
   }
   __syncthreads();
 
   // ---------------------------------------------------------------- denominators
   if (tid < QB) {
-    // lane i: den_i = (((0 + e_0) + e_1) + ...), t ascending; the next 8
-    // values are read before the current 8 are added
+    // lane i: den_i = (((0 + e_0) + e_1) + ...), t ascending; the next 32
+    // (short prefixes: 8) values are read before the current ones are added
     const int i = tid;
     const uint32_t len = qlen[i];
     float den = __uint_as_float(0u);
     uint32_t t = 0;
-    if (len >= 16) {
+    if (len >= 64) {
+      float cur[32];
+#pragma unroll
+      for (int u = 0; u < 32; ++u) cur[u] = sT[u * ST + i];
+      for (t = 32; t + 32 <= len; t += 32) {
+        float nxt[32];
+#pragma unroll
+        for (int u = 0; u < 32; ++u) nxt[u] = sT[(t + u) * ST + i];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 32; ++u) den = den + cur[u];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 32; ++u) cur[u] = nxt[u];
+      }
+#pragma unroll
+      for (int u = 0; u < 32; ++u) den = den + cur[u];
+    } else if (len >= 16) {
       float cur[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) cur[u] = sT[u * ST + i];
@@ -207,9 +275,21 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
     red[QB + i] = den;
   }
   __syncthreads();
-  for (uint32_t e = tid; e < lmax * QB; e += 256) {
-    const uint32_t t = e / QB, i = e % QB;
-    if (t < qlen[i]) sT[t * ST + i] = sT[t * ST + i] / red[QB + i];
+  for (uint32_t e0 = tid; e0 < lmax * QB; e0 += 4 * 256) {
+    float sv[4], dv[4];
+    bool live[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t e = e0 + 256u * u, t = e / QB, i = e % QB;
+      live[u] = e < lmax * QB && t < qlen[i];
+      sv[u] = live[u] ? sT[t * ST + i] : 0.0f;
+      dv[u] = red[QB + i];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t e = e0 + 256u * u, t = e / QB, i = e % QB;
+      if (live[u]) sT[t * ST + i] = sv[u] / dv[u];
+    }
   }
   __syncthreads();
 

@@ -243,6 +243,32 @@ def test_attention_causal_matches_prefix_decode(B, Tq, H, L, lens):
     _bitwise(o16.read(np.uint16, (B * Tq, H * D)), oracle.f32_to_bf16_bits_np(want))
 
 
+def test_attention_causal_prefill_nan_inf_tie_scores():
+    """The 16-query prefill kernel (Tq >= 8) on scores with a NaN inside the
+    prefix (the max restarts after it), a NaN at exactly one query's last
+    position (that query's max is the NaN), an overflowing score, all-equal
+    (+0) scores, and a partial last block of queries (Tq = 20)."""
+    B, Tq, H, L, D = 2, 20, 4, 48, 128
+    lens = [48, 30]
+    rng = np.random.default_rng(21)
+    q16 = oracle.f32_to_bf16_bits_np(rng.normal(0, 1, (B * Tq * H * D,)).astype(np.float32))
+    k32 = rng.normal(0, 1, (B, H, L, D)).astype(np.float32)
+    k32[0, 0, 10, 5] = np.nan      # positions 11.. of every query of b 0 follow a NaN
+    k32[0, 1, 35, 0] = np.nan      # b 0, query 6 has 36 positions: its last one is NaN
+    k32[0, 2, 3, :] = 1e30         # overflowing score
+    k32[0, 3, :, :] = 0.0          # every score +0
+    k16 = oracle.f32_to_bf16_bits_np(k32)
+    v16 = oracle.f32_to_bf16_bits_np(rng.normal(0, 1, (B, H, L, D)).astype(np.float32))
+    q, k, v = ca.Buffer.from_array(q16), ca.Buffer.from_array(k16), ca.Buffer.from_array(v16)
+    lb = ca.Buffer.from_array(np.array(lens, np.uint32))
+    scale = 1.0 / math.sqrt(D)
+    o32 = ca.Buffer(B * Tq * H * D * 4)
+    say("causal prefill attention NaN / inf / tie scores")
+    ca.attn_causal_bf16(q, k, v, lb, o32, B, Tq, H, L, D, scale, out_f32=True)
+    want = od.attn_causal(q16, k16, v16, lens, B, Tq, H, D, scale)
+    _bitwise(o32.read(np.float32, (B * Tq, H * D)), want)
+
+
 def test_attention_causal_tq1_equals_decode_kernel():
     B, H, L, D = 4, 8, 1024, 128
     q, k, v = _attn_inputs(B, 1, H, L, 99)
