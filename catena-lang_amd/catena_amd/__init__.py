@@ -135,6 +135,7 @@ SIGNATURES = {
     "catena_mi355x_rope_inv_freq": (_int, [ctypes.POINTER(_f32), _u32, ctypes.c_double]),
     "catena_mi355x_rope_qkv_bf16": (_int, [_vp] * 6 + [_u32] * 5),
     "catena_mi355x_silu_mul_bf16": (_int, [_vp, _vp, _u64, _u32, _u32]),
+    "catena_mi355x_gemm_bf16_silu": (_int, [_vp, _vp, _vp, _u64, _u64, _u64]),
     "catena_mi355x_argmax_f32": (_int, [_vp, _vp, _u64, _u64]),
     "catena_mi355x_broadcast_f32": (_int, [_vp, _u64, _f32]),
     "catena_mi355x_arange_f32": (_int, [_vp, _u64]),
@@ -349,6 +350,12 @@ def rope_qkv_bf16(qkv, inv_freq, lens, q, k_cache, v_cache, batch: int, tq: int,
 
 def silu_mul_bf16(gu, out, rows: int, ffn: int, group: int = 0) -> None:
     check(lib().catena_mi355x_silu_mul_bf16(_p(gu), _p(out), rows, ffn, group))
+
+
+def gemm_bf16_silu(a, b, act, n: int, m: int, k: int) -> None:
+    """act[n][m/2] = bf16(silu(gate) * up) of A[n][k] x B[k][m] (gate / up in
+    groups of 64 columns), the GEMM and catena_mi355x_silu_mul_bf16 in one."""
+    check(lib().catena_mi355x_gemm_bf16_silu(_p(a), _p(b), _p(act), n, m, k))
 
 
 def argmax_f32(x, idx, rows: int, n: int) -> None:

@@ -169,6 +169,10 @@ int forward(catena_decoder& m, const uint32_t* tokens, uint32_t batch, uint32_t 
       DecodeEpiArgs e;
       e.act = ACT;
       TRY(gemm_bf16_decode(HN, wgu, GU, rows, 2 * f, d, DecodeEpilogue::Silu, e));
+    } else if (gemm_bf16_silu_fits(rows, 2 * f, d, HN, wgu, ACT)) {
+      // the SwiGLU gate in the GEMM's epilogue: the f32 gate / up product
+      // (4x the bytes of act) is never written
+      TRY(catena_mi355x_gemm_bf16_silu(HN, wgu, ACT, rows, 2 * f, d));
     } else {
       TRY(catena_mi355x_gemm_bf16(HN, wgu, GU, rows, 2 * f, d, 1));
       TRY(catena_mi355x_silu_mul_bf16(GU, ACT, rows, (uint32_t)f, 64));

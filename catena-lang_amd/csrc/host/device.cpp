@@ -78,6 +78,8 @@ const KernelSpec kKernels[] = {
     {KernelId::GemmBf16K32F32, "gemm_bf16_k32", "catena_gemm_bf16_k32_f32out"},
     {KernelId::GemmBf16K32N128Bf16, "gemm_bf16_k32", "catena_gemm_bf16_k32n128_bf16out"},
     {KernelId::GemmBf16K32N128F32, "gemm_bf16_k32", "catena_gemm_bf16_k32n128_f32out"},
+    {KernelId::GemmBf16K32Silu, "gemm_bf16_k32", "catena_gemm_bf16_k32_silu"},
+    {KernelId::GemmBf16K32N128Silu, "gemm_bf16_k32", "catena_gemm_bf16_k32n128_silu"},
     {KernelId::GemmBf16DecodeF32, "gemm_bf16_decode", "catena_gemm_bf16_decode_f32out"},
     {KernelId::GemmBf16DecodeBf16, "gemm_bf16_decode", "catena_gemm_bf16_decode_bf16out"},
     {KernelId::GemmBf16DecodeRope, "gemm_bf16_decode", "catena_gemm_bf16_decode_rope"},

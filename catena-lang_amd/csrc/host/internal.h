@@ -40,6 +40,8 @@ enum class KernelId : int {
   GemmBf16K32F32,
   GemmBf16K32N128Bf16,  // the same on 256 x 128 tiles
   GemmBf16K32N128F32,
+  GemmBf16K32Silu,  // variants 9 / 10 with the SwiGLU epilogue
+  GemmBf16K32N128Silu,
   GemmBf16DecodeF32,
   GemmBf16DecodeBf16,
   GemmBf16DecodeRope,
@@ -138,6 +140,10 @@ enum class DecodeEpilogue { StoreF32, StoreBf16, Rope, Silu, Argmax };
 // interleaved in 64-column groups, act[n][m/2]; Argmax: idx[n].
 int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, uint64_t m,
                      uint64_t k, DecodeEpilogue epi, const DecodeEpiArgs& ep);
+// Whether catena_mi355x_gemm_bf16_silu takes this shape (the 32-k tile
+// kernels: n % 256, m % 128, k % 128 == 0, aligned operands).
+bool gemm_bf16_silu_fits(uint64_t n, uint64_t m, uint64_t k, const void* a, const void* b,
+                         const void* act);
 // nn.rmsnorm rows whose input is an embedding gather (x = widen(table[tok]))
 // written to x_out, bf16 output.
 int embed_rmsnorm_bf16(const uint32_t* tokens, const uint16_t* table, uint32_t vocab,

@@ -176,6 +176,13 @@ int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, 
   return launch(id, dim3((unsigned)gx, (unsigned)S), dim3(256), lds, args);
 }
 
+bool gemm_bf16_silu_fits(uint64_t n, uint64_t m, uint64_t k, const void* a, const void* b,
+                         const void* act) {
+  return n % 256 == 0 && m % 128 == 0 && k % 128 == 0 && k > 0 && k <= (1ull << 22) &&
+         m <= (1ull << 24) && aligned16(a) && aligned16(b) && aligned16(act) &&
+         (n / 256) * (m / 128) <= 0x7FFFFFFFull;
+}
+
 }  // namespace catena
 
 extern "C" {
@@ -249,6 +256,30 @@ int catena_mi355x_gemm_bf16(const uint16_t* a, const uint16_t* b, void* c, uint6
   KernelId id = tile_ok ? (out_f32 ? KernelId::GemmBf16TileF32 : KernelId::GemmBf16TileBf16)
                         : (out_f32 ? KernelId::GemmBf16EdgeF32 : KernelId::GemmBf16EdgeBf16);
   return launch(id, dim3((unsigned)tiles), dim3(256), lds, args);
+}
+
+int catena_mi355x_gemm_bf16_silu(const uint16_t* a, const uint16_t* b, uint16_t* act, uint64_t n,
+                                 uint64_t m, uint64_t k) {
+  int st = ensure_init();
+  if (st) return st;
+  if (n == 0 || m == 0) return CATENA_OK;
+  if (!act || (k > 0 && (!a || !b))) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
+  if (!gemm_bf16_silu_fits(n, m, k, a, b, act))
+    return fail(CATENA_ERR_UNSUPPORTED,
+                "SwiGLU GEMM needs n %% 256 == 0, m %% 128 == 0, k %% 128 == 0 (k <= 2^22, m <= 2^24) "
+                "and 16-byte aligned pointers");
+  Device& d = device();
+  // the tile width the plain GEMM would take for this shape (same bits)
+  const bool narrow = m % 256 != 0 || prefer_n128(n, m, d.cu_count);
+  const size_t stages = narrow ? 4ull * (256 + 128) * 32 * sizeof(uint16_t)   // 98304 B
+                               : 4ull * (256 + 256) * 32 * sizeof(uint16_t);  // 131072 B
+  const size_t slots = 4ull * (narrow ? 64 : 128) * 68 * sizeof(float);        // up-column hand-over
+  const size_t lds = stages > slots ? stages : slots;
+  if (lds > d.max_lds) return fail(CATENA_ERR_UNSUPPORTED, "device LDS %zu < %zu", d.max_lds, lds);
+  const uint64_t grid = narrow ? (n / 256) * (m / 128) : (n / 256) * (m / 256);
+  void* args[] = {&a, &b, &act, &n, &m, &k};
+  return launch(narrow ? KernelId::GemmBf16K32N128Silu : KernelId::GemmBf16K32Silu, dim3((unsigned)grid),
+                dim3(512), lds, args);
 }
 
 int catena_mi355x_attn_decode_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,

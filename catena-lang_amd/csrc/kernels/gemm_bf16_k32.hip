@@ -83,7 +83,7 @@ CATENA_DEV void tile_of(uint32_t bid, uint32_t tiles_m, uint32_t tiles_n, uint32
 // buffer descriptor word 3 for raw (unswizzled, stride 0) 32-bit access
 constexpr int kRsrcWord3 = 0x00020000;
 
-template <bool OUT_BF16, int BN>
+template <bool OUT_BF16, int BN, bool SILU = false>
 CATENA_DEV void gemm_k32_body(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                               void* __restrict__ C, uint64_t M, uint64_t N, uint64_t K) {
   static_assert(BN == 256 || BN == 128, "tile widths 256 and 128");
@@ -272,7 +272,88 @@ CATENA_DEV void gemm_k32_body(const uint16_t* __restrict__ A, const uint16_t* __
   }
   CATENA_WAIT_VMCNT(0);  // no LDS writes outstanding past this point
 
-  if constexpr (OUT_BF16) {
+  if constexpr (SILU) {
+    // SwiGLU: B's columns come in groups of 64, gate and up alternating (a
+    // 128-column group holds matching gate and up columns), so a wave with
+    // even wn holds gate columns and wave wn + 1 the matching up columns.
+    // C is act [M][N / 2]: act[m][(n0 + 64 (wn & ~1)) / 2 + c] =
+    // bf16(silu~(gate) * up) of the f32 tile, as catena_silu_mul_bf16 with
+    // group 64.  Both waves of a pair work: the gate wave takes the first
+    // half of the rows, the up wave the second, each handing the other the
+    // half it needs through LDS (rows skewed by 16 bytes), so every SIMD
+    // carries two waves of the SiLU arithmetic.  Each wave then stages its
+    // act rows like the bf16 tile below and stores whole 128-byte rows.
+    constexpr int UP_LD = 68;                 // f32 row stride of a pair's slot
+    constexpr int SLOT = WI * 16 * UP_LD;     // floats per slot
+    constexpr int HB = WI / 2;                // row blocks per wave
+    float* slot = reinterpret_cast<float*>(smem) + (wm * (WAVES_N / 2) + (wn >> 1)) * SLOT;
+    const int half = wn & 1;                  // 0: gate wave, first rows; 1: up wave, last rows
+    // Each phase is instantiated for both halves so every acc index is a
+    // compile-time constant (a run-time index would put acc in scratch).
+    auto hand_over = [&](auto H) {
+      constexpr int h = decltype(H)::value;
+#pragma unroll
+      for (int ii = 0; ii < HB; ++ii) {
+        constexpr int base = (1 - h) * HB;    // the partner's row blocks
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          *reinterpret_cast<f32x4_t*>(slot + (16 * (base + ii) + s) * UP_LD + 16 * j + 4 * G) = acc[base + ii][j];
+      }
+    };
+    if (half)
+      hand_over(std::integral_constant<int, 1>{});
+    else
+      hand_over(std::integral_constant<int, 0>{});
+    __syncthreads();
+    uint2 act[HB][4];
+    auto swiglu = [&](auto H) {
+      constexpr int h = decltype(H)::value;
+#pragma unroll
+      for (int ii = 0; ii < HB; ++ii) {
+        constexpr int base = h * HB;          // this wave's row blocks
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const f32x4_t other =
+              *reinterpret_cast<const f32x4_t*>(slot + (16 * (base + ii) + s) * UP_LD + 16 * j + 4 * G);
+          float a[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float gate = h ? other[q] : acc[base + ii][j][q];
+            const float up = h ? acc[base + ii][j][q] : other[q];
+            const float sg = silu_approx(gate);
+            a[q] = sg * up;
+          }
+          act[ii][j].x = pack_bf16x2(a[0], a[1]);
+          act[ii][j].y = pack_bf16x2(a[2], a[3]);
+        }
+      }
+    };
+    if (half)
+      swiglu(std::integral_constant<int, 1>{});
+    else
+      swiglu(std::integral_constant<int, 0>{});
+    __syncthreads();  // the slots are read; every wave stages below
+    char* wt = reinterpret_cast<char*>(smem) + wave * (HB * 16 * 128);
+#pragma unroll
+    for (int ii = 0; ii < HB; ++ii) {
+      const uint32_t r = 16 * ii + s;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t c = (uint32_t)(2 * j + (G >> 1)) ^ ((r >> 1) & 7u);
+        *reinterpret_cast<uint2*>(wt + r * 128 + 16 * c + 8 * (G & 1)) = act[ii][j];
+      }
+    }
+    const uint64_t F = N / 2;
+    const uint32_t rr = (uint32_t)lane >> 3, cc = (uint32_t)lane & 7;
+#pragma unroll
+    for (int t = 0; t < WI; ++t) {
+      const uint32_t r = 8 * t + rr;
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(wt + r * 128 + 16 * (cc ^ ((r >> 1) & 7u)));
+      const uint64_t gr = m0 + wm * 16 * WI + half * HB * 16 + r;
+      const uint64_t gc = (n0 + (wn & ~1) * 64) / 2 + 8 * cc;
+      *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(C) + gr * F + gc) = v;
+    }
+  } else if constexpr (OUT_BF16) {
     // Stage the wave's (16 WI) x 64 bf16 tile in its own LDS (row r, 16-byte
     // chunk c at r * 128 + 16 * (c ^ ((r >> 1) & 7))), then store whole
     // 128-byte rows: 8 lanes per row, 8 rows per instruction.  The barrier
@@ -327,3 +408,14 @@ CATENA_GEMM_K32_KERNEL(catena_gemm_bf16_k32_bf16out, true, 256)
 CATENA_GEMM_K32_KERNEL(catena_gemm_bf16_k32_f32out, false, 256)
 CATENA_GEMM_K32_KERNEL(catena_gemm_bf16_k32n128_bf16out, true, 128)
 CATENA_GEMM_K32_KERNEL(catena_gemm_bf16_k32n128_f32out, false, 128)
+
+// SwiGLU-fused: C = act [M][N / 2] bf16 (N % 128 == 0), dynamic LDS the larger
+// of the stages and 4 up slots of 16 WI rows x 68 floats
+#define CATENA_GEMM_K32_SILU_KERNEL(NAME, BN_)                                            \
+  extern "C" __global__ __launch_bounds__(512) void NAME(                                 \
+      const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C, \
+      uint64_t M, uint64_t N, uint64_t K) {                                               \
+    gemm_k32_body<false, BN_, true>(A, B, C, M, N, K);                                    \
+  }
+CATENA_GEMM_K32_SILU_KERNEL(catena_gemm_bf16_k32_silu, 256)
+CATENA_GEMM_K32_SILU_KERNEL(catena_gemm_bf16_k32n128_silu, 128)

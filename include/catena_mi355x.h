@@ -194,6 +194,17 @@ int catena_mi355x_rope_qkv_bf16(const float *qkv, const float *inv_freq, const u
 int catena_mi355x_silu_mul_bf16(const float *gu, uint16_t *out, uint64_t rows, uint32_t ffn,
                                 uint32_t group);
 
+/* bf16 GEMM with the SwiGLU gate fused into its epilogue (the decoder's
+ * W_gu projection in prefill): act[n][m/2] = bf16(nn.silu(gate) * up) of the
+ * f32 product A[n][k] x B[k][m], whose columns are gate and up interleaved in
+ * groups of 64 (catena_mi355x_silu_mul_bf16 with group 64).  Bitwise the same
+ * as catena_mi355x_gemm_bf16(..., out_f32 = 1) followed by that call, without
+ * writing the f32 product.  Needs the 32-k tile kernels: n % 256 == 0, m % 128
+ * == 0, k % 128 == 0, k <= 2^22, m <= 2^24, 16-byte aligned pointers; other
+ * shapes return CATENA_ERR_UNSUPPORTED.  No reference counterpart. */
+int catena_mi355x_gemm_bf16_silu(const uint16_t *a, const uint16_t *b, uint16_t *act, uint64_t n,
+                                 uint64_t m, uint64_t k);
+
 /* tensor.argmax-f32 per row (catena-lang/stdlib/tensor.hex:204-227):
  * idx[r] = first index of the maximum with the reference's NaN behaviour;
  * n = 0 gives 0xFFFFFFFF (the reference asserts n != 0). */

@@ -208,3 +208,31 @@ def test_decode_register_path(monkeypatch):
     _check(a16, b16, g32, g16)
     ca.gemm_bf16(a, b, c16, mrows, n, k)
     assert np.array_equal(c16.read(np.uint16, (mrows, n)), g16)
+
+
+@pytest.mark.parametrize("n,m,k", [(256, 1024, 2048), (2048, 8192, 256), (512, 384, 128)])
+def test_gemm_swiglu_epilogue_equals_gemm_then_silu(n, m, k):
+    """The SwiGLU-fused tile GEMM (256 x 128 tiles for the first and third
+    shape, 256 x 256 for the second, as the plain GEMM would choose) gives
+    the bits of the f32 GEMM followed by catena_mi355x_silu_mul_bf16 with
+    group 64."""
+    a = dev_normal_bf16(n * k, 31 + n + k, 0, 1.0)
+    b = dev_normal_bf16(k * m, 31 + n + k, 1, 1.0)
+    say(f"bf16 GEMM + SwiGLU n={n} m={m} k={k}")
+    act = ca.Buffer(n * (m // 2) * 2)
+    ca.gemm_bf16_silu(a, b, act, n, m, k)
+    gu = ca.Buffer(n * m * 4)
+    ca.gemm_bf16(a, b, gu, n, m, k, out_f32=True)
+    want = ca.Buffer(n * (m // 2) * 2)
+    ca.silu_mul_bf16(gu, want, n, m // 2, 64)
+    assert np.array_equal(act.read(np.uint16), want.read(np.uint16))
+
+
+def test_gemm_swiglu_rejects_untiled_shapes():
+    a = dev_normal_bf16(256 * 256, 5, 0, 1.0)
+    b = dev_normal_bf16(256 * 256, 5, 1, 1.0)
+    act = ca.Buffer(256 * 128 * 2)
+    with pytest.raises(ca.CatenaError):
+        ca.gemm_bf16_silu(a, b, act, 100, 256, 256)
+    with pytest.raises(ca.CatenaError):
+        ca.gemm_bf16_silu(a, b, act, 256, 256, 96)

@@ -92,7 +92,16 @@ def _check_forward(dec, cfg, w, tokens, tq, cache_len):
     _bitwise(Hh, h)
     HN = rd(ca.DEC_HN, np.uint16, (R, d))
     _bitwise(HN, hn)
-    GU = rd(ca.DEC_GU, np.float32, (R, 2 * F))
+    if tq > 1 and R % 256 == 0 and d % 128 == 0 and (2 * F) % 128 == 0:
+        # prefill with the SwiGLU gate in W_gu's GEMM epilogue: the f32
+        # product is never written; the plain GEMM recomputes it (the same
+        # tile kernel's order, so the same bits) to check act against
+        gu = ca.Buffer(R * 2 * F * 4)
+        ca.gemm_bf16(ca.Buffer.from_array(HN), ca.Buffer.from_array(w["w_gu"][lay]), gu, R, 2 * F, d,
+                     out_f32=True)
+        GU = gu.read(np.float32, (R, 2 * F))
+    else:
+        GU = rd(ca.DEC_GU, np.float32, (R, 2 * F))
     gemm_within_bound(HN, w["w_gu"][lay], GU)
     ACT = rd(ca.DEC_ACT, np.uint16, (R, F))
     _bitwise(ACT, od.silu_mul_bf16(GU, F, 64))
@@ -193,6 +202,34 @@ def test_decoder_two_layers_decode_steps_stagewise(batch):
         got = out.read(np.uint32)
         assert np.array_equal(got, want)
         prev = got
+    dec.close()
+
+
+class Prefill256(Tiny):
+    H, F, V, B, T, L, layers = 2, 512, 512, 16, 16, 20, 1
+    d = H * D
+
+
+def test_decoder_prefill_fused_swiglu_stagewise():
+    """A prefill of 256 rows, where W_gu's GEMM carries the SwiGLU gate in
+    its epilogue (act only, no f32 product), then a decode step: stage by
+    stage as above."""
+    cfg = Prefill256
+    dec = ca.Decoder(cfg.d, cfg.H, cfg.F, cfg.layers, cfg.V, cfg.B, cfg.L)
+    dec.init_weights(seed=17, std=0.02)
+    w = _weights(dec, cfg)
+    tokens = np.random.default_rng(6).integers(0, cfg.V, (cfg.B, cfg.T)).astype(np.uint32)
+    nxt = ca.Buffer(cfg.B * 4)
+    say("decoder prefill of 256 rows (fused SwiGLU)")
+    dec.prefill(ca.Buffer.from_array(tokens), cfg.B, cfg.T, nxt)
+    want = _check_forward(dec, cfg, w, tokens, cfg.T, cfg.T)
+    got = nxt.read(np.uint32)
+    assert np.array_equal(got, want)
+    out = ca.Buffer(cfg.B * 4)
+    say("decoder step after the 256-row prefill")
+    dec.generate(1, out)
+    want = _check_forward(dec, cfg, w, got, 1, cfg.T + 1)
+    assert np.array_equal(out.read(np.uint32), want)
     dec.close()
 
 
