@@ -236,3 +236,30 @@ def test_gemm_swiglu_rejects_untiled_shapes():
         ca.gemm_bf16_silu(a, b, act, 100, 256, 256)
     with pytest.raises(ca.CatenaError):
         ca.gemm_bf16_silu(a, b, act, 256, 256, 96)
+
+
+def test_gemm_swiglu_special_values():
+    """NaN, +-inf and overflowing products in the gate and up columns: the
+    fused epilogue gives the bits of the f32 GEMM followed by silu_mul."""
+    n, m, k = 256, 512, 128
+    rng = np.random.default_rng(41)
+    a32 = rng.normal(0, 1, (n, k)).astype(np.float32)
+    a32[3, 7] = np.nan                  # row 3: NaN everywhere
+    a32[5, :] = 3e38                    # row 5: products overflow to +-inf
+    a32[9, 0] = np.inf                  # row 9: +-inf or NaN (inf * 0)
+    a32[11, :] = 0.0                    # row 11: exact zeros (silu(+0) * up)
+    b32 = rng.normal(0, 1, (k, m)).astype(np.float32)
+    b32[0, 64:128] = 0.0                # up columns of group 0 see inf * 0 = NaN on row 9
+    a = ca.Buffer.from_array(oracle.f32_to_bf16_bits_np(a32))
+    b = ca.Buffer.from_array(oracle.f32_to_bf16_bits_np(b32))
+    say("bf16 GEMM + SwiGLU special values")
+    act = ca.Buffer(n * (m // 2) * 2)
+    ca.gemm_bf16_silu(a, b, act, n, m, k)
+    gu = ca.Buffer(n * m * 4)
+    ca.gemm_bf16(a, b, gu, n, m, k, out_f32=True)
+    want = ca.Buffer(n * (m // 2) * 2)
+    ca.silu_mul_bf16(gu, want, n, m // 2, 64)
+    g16, w16 = act.read(np.uint16), want.read(np.uint16)
+    assert np.array_equal(g16, w16), int(np.sum(g16 != w16))
+    g = gu.read(np.float32, (n, m))
+    assert np.isnan(g[3]).all() and not np.isfinite(g[5]).all() and np.isnan(g[9, 64:128]).all()
