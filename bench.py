@@ -360,11 +360,12 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    # Back-to-back GEMMs cross a power-management transient: in a trace the
-    # first ~15 launches take ~105 us, launches 20-40 129-133 us, decaying to
-    # 103-106 us by launch ~120; 100 warmup launches (~12 ms) put most of the
-    # timed region in the steady state.
-    ap.add_argument("--warmup", type=int, default=100)
+    # Back-to-back GEMMs cross a power-management transient: in kernel traces
+    # the first ~15 launches take ~103-105 us, launches 20-50 122-133 us, and
+    # the durations decay to 104-107 us over launches 100-130 and settle at
+    # 101-103 us after ~150; 200 warmup launches (~23 ms) put the timed
+    # region in the steady state.  Every launch is the full GEMM.
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["gemm", "core", "decoder", "all"], default="all",
                     help="gemm: the headline GEMM only; core: + decode attention and decode "
