@@ -200,8 +200,9 @@ int catena_mi355x_silu_mul_bf16(const float *gu, uint16_t *out, uint64_t rows, u
  * groups of 64 (catena_mi355x_silu_mul_bf16 with group 64).  Bitwise the same
  * as catena_mi355x_gemm_bf16(..., out_f32 = 1) followed by that call, without
  * writing the f32 product.  Needs the 32-k tile kernels: n % 256 == 0, m % 128
- * == 0, k % 128 == 0, k <= 2^22, m <= 2^24, 16-byte aligned pointers; other
- * shapes return CATENA_ERR_UNSUPPORTED.  No reference counterpart. */
+ * == 0, k > 0 with k % 128 == 0, k <= 2^22, m <= 2^24, 16-byte aligned
+ * pointers; other shapes return CATENA_ERR_UNSUPPORTED (n == 0 or m == 0 is a
+ * no-op).  No reference counterpart. */
 int catena_mi355x_gemm_bf16_silu(const uint16_t *a, const uint16_t *b, uint16_t *act, uint64_t n,
                                  uint64_t m, uint64_t k);
 
