@@ -78,7 +78,8 @@ extern "C" __global__ __launch_bounds__(256) void catena_embed_rows_bf16(
 
 // One workgroup per output row.  h = x[src] (+ resid[src] when resid is
 // given: one f32 add per element); then nn.rmsnorm of h:
-//   sum_sq = fold_{i asc} from +0 of h_i * h_i   (one wave, serial_sum_wave)
+//   sum_sq = fold_{i asc} from +0 of h_i * h_i   (one wave, serial_sum_wave;
+//            serial_sum_wave_long for n >= 1024: same bits)
 //   rms    = math.sqrt(sum_sq / (f32)n + 0x3727C5AC)
 //   y_i    = h_i / rms
 // src = row_index ? row_index[row] : row.  Outputs (each optional): h_out
@@ -176,7 +177,7 @@ extern "C" __global__ __launch_bounds__(256) void catena_rmsnorm_rows(
   }
   __syncthreads();
   if (threadIdx.x < 64) {
-    const float sum_sq = serial_sum_wave(sq, n);
+    const float sum_sq = n >= 1024 ? serial_sum_wave_long(sq, n) : serial_sum_wave(sq, n);
     if (threadIdx.x == 0) {
       const float len_f = (float)(uint64_t)n;
       const float mean_sq = sum_sq / len_f;

@@ -42,7 +42,8 @@ def _rows(rows, n, seed, scale=1.0):
 
 
 @pytest.mark.parametrize("rows,n", [(1, 6), (3, 2048), (2, 4097), (5, 5632), (1, 1), (4, 12),
-                                    (2, 31), (2, 33), (3, 2049), (1, 6143), (1, 20000)])
+                                    (2, 31), (2, 33), (3, 2049), (1, 6143), (1, 20000),
+                                    (2, 1023), (2, 1024), (2, 1030)])
 def test_rmsnorm_f32(rows, n):
     say(f"rmsnorm rows={rows} n={n}")
     x = _rows(rows, n, rows * 31 + n, scale=3.0)
@@ -53,8 +54,8 @@ def test_rmsnorm_f32(rows, n):
     _bitwise(yb.read(np.float32, (rows, n)), oracle.rmsnorm_f32(x))
 
 
-def test_rmsnorm_specials():
-    n = 64
+@pytest.mark.parametrize("n", [64, 2048])
+def test_rmsnorm_specials(n):
     x = _rows(6, n, 5)
     x[0] = 0.0                      # sum 0: rms = sqrt(eps)
     x[1, 3] = np.nan                # NaN propagates through the fold
@@ -63,7 +64,7 @@ def test_rmsnorm_specials():
     x[4] = 1e-30                    # squares underflow (subnormal/zero)
     x[5, ::2] = -0.0
     xb, yb = ca.Buffer.from_array(x), ca.Buffer(x.nbytes)
-    say("rmsnorm specials")
+    say(f"rmsnorm specials n={n}")
     ca.rmsnorm_f32(xb, yb, 6, n)
     _bitwise(yb.read(np.float32, (6, n)), oracle.rmsnorm_f32(x))
 
