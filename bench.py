@@ -73,6 +73,12 @@ class HipEvents:
     def start(self):
         assert self.hip.hipEventRecord(self.a, self.stream) == 0
 
+    def close(self):
+        for e in (self.a, self.b):
+            if e:
+                self.hip.hipEventDestroy(e)
+        self.a = self.b = ctypes.c_void_p()
+
     def stop_ms(self) -> float:
         assert self.hip.hipEventRecord(self.b, self.stream) == 0
         assert self.hip.hipEventSynchronize(self.b) == 0
@@ -126,6 +132,56 @@ def output_hash(buf: ca.Buffer) -> str:
 
 
 # ------------------------------------------------------------------ workloads
+def bench_c1(steps: int, ev):
+    """configs[0] (C1): the 256^3 f32 GEMM, U[-1,1] inputs from seeds 1 and 2,
+    through the program ABI symbol program_matmul_2x2_via_mem called as the
+    reference's libffi executor calls a generated program (Mem by value,
+    output through a pointer; synchronous, the output allocated by the
+    callee and freed by the caller).  Times whole calls on the host clock
+    (allocation, launch, synchronisation) and, with HIP events, the kernel
+    alone; checks bitwise run to run."""
+    n = m = k = 256
+    a, b = ca.Buffer(n * k * 4), ca.Buffer(k * m * 4)
+    ca.fill_uniform_f32(a, n * k, 1, 0)
+    ca.fill_uniform_f32(b, k * m, 2, 0)
+    L = ca.lib()
+    hashes, got = set(), None
+
+    def call(i):
+        nonlocal got
+        out = ca.Mem()
+        L.program_matmul_2x2_via_mem(a.mem, b.mem, n, m, k, n * k, k * m, n * m, ctypes.byref(out))
+        if i < 10:
+            got = ca.mem_to_array(out, np.uint32).reshape(n, m)
+            hashes.add(output_hash_np(got))
+        ca.mem_free(out)
+
+    for i in range(10):
+        call(i)
+    t = []
+    for i in range(steps):
+        t0 = time.perf_counter()
+        call(10 + i)
+        t.append((time.perf_counter() - t0) * 1e6)
+    c = ca.Buffer(n * m * 4)
+    k_ms = timed(lambda i: ca.gemm_f32_exact(a, b, c, n, m, k), steps, 10, ev)
+    flop = 2.0 * n * m * k
+    return {"workload": "C1: f32 GEMM 256^3 as the program matmul-2x2-via-mem (program ABI, "
+                        "by-value Mem), U[-1,1] from seeds 1 / 2",
+            "us_per_program_call": round(float(np.median(t)), 2),
+            "kernel_us": round(k_ms * 1e3, 3),
+            "kernel_GFLOP/s": round(flop / (k_ms * 1e-3) / 1e9, 1),
+            "bitwise_run_to_run": len(hashes) == 1,
+            "roofline": None,
+            "bound": "neither (plumbing and parity: 33.5 Mflop, 786 KB)",
+            "inputs": (a.read(np.float32, (n, k)), b.read(np.float32, (k, m)), got)}
+
+
+def output_hash_np(arr) -> str:
+    import hashlib
+    return hashlib.sha256(np.ascontiguousarray(arr).tobytes()).hexdigest()[:16]
+
+
 def bench_gemm(steps, warmup, ev):
     n = m = k = 4096
     a, b, c = ca.Buffer(n * k * 2), ca.Buffer(k * m * 2), ca.Buffer(n * m * 2)
@@ -160,12 +216,23 @@ def bench_decode_gemm(steps, warmup, ev):
             ws.append(w)
         y = ca.Buffer(M * N * 2)
         call = lambda i: ca.gemm_bf16(x, ws[i % copies], y, M, N, K)  # noqa: E731
+        call(0)
+        h0 = output_hash(y)
         ms = timed(call, steps, warmup, ev)
+        call(0)
+        same = output_hash(y) == h0
         nbytes = 2.0 * N * K + 2.0 * M * K + 2.0 * M * N
-        res[f"N{N}_K{K}"] = {"us": ms * 1e3, "GB/s": nbytes / (ms * 1e-3) / 1e9,
-                             "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
-                             "bytes_per_launch": nbytes,
-                             "per_launch_us": per_launch_us(call, max(10, steps), ev)}
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        groups, _ = ca.gemm_bf16_decode_plan(M, N, K)
+        res[f"N{N}_K{K}"] = {"us": ms * 1e3, "GB/s": gbs, "frac_hbm": gbs / PEAK_HBM_GBS,
+                             "bytes_per_launch": nbytes, "k_groups": groups,
+                             "bitwise_run_to_run": same,
+                             "per_launch_us": per_launch_us(call, max(10, steps), ev),
+                             "roofline": {"bound": "hbm", "achieved": round(gbs, 1),
+                                          "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                          "frac": round(gbs / PEAK_HBM_GBS, 4),
+                                          "traffic": measured_traffic("catena_gemm_bf16_decode_bf16out")},
+                             "inputs": (x.read(np.uint16, (M, K)), ws[0].read(np.uint16, (K, N)))}
         del ws
     return res
 
@@ -221,6 +288,19 @@ def bench_decoder(reps: int, ev):
             gen.append(g_ms)
         hashes.add(output_hash(out))
     p_ms, g_ms = float(np.median(pre)), float(np.median(gen))
+    # state for the CPU baseline: host weights, and the caches of a prefill
+    dec.prefill(tb, B, T, nxt)
+    ca.synchronize()
+    w = {"embed": dec.read(ca.DEC_EMBED, np.uint16).reshape(V, d),
+         "w_lm": dec.read(ca.DEC_W_LM, np.uint16).reshape(d, V),
+         "w_qkv": [dec.read(ca.DEC_W_QKV, np.uint16).reshape(d, 3 * d)],
+         "w_o": [dec.read(ca.DEC_W_O, np.uint16).reshape(d, d)],
+         "w_gu": [dec.read(ca.DEC_W_GU, np.uint16).reshape(d, 2 * F)],
+         "w_down": [dec.read(ca.DEC_W_DOWN, np.uint16).reshape(F, d)]}
+    state = {"weights": w, "B": B, "T": T, "H": H, "F": F, "L": T + steps,
+             "kc": [dec.read(ca.DEC_K_CACHE, np.uint16).reshape(B, H, T + steps, 128)],
+             "vc": [dec.read(ca.DEC_V_CACHE, np.uint16).reshape(B, H, T + steps, 128)],
+             "next": nxt.read(np.uint32), "tokens": tokens}
     block_params = 4 * d * d + 3 * d * F
     head_params = 2 * V * d  # embedding + LM head
     prefill_flop = 2.0 * B * T * block_params + 2.0 * B * d * V
@@ -239,48 +319,156 @@ def bench_decoder(reps: int, ev):
         "decode_frac_hbm": step_bytes / (g_ms / steps * 1e-3) / 1e9 / PEAK_HBM_GBS,
         "params": {"block": block_params, "embedding_and_head": head_params},
         "bitwise_run_to_run": len(hashes) == 1,
+        "roofline_prefill": {"bound": "mfma", "achieved": round(prefill_flop / (p_ms * 1e-3) / 1e12, 1),
+                             "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                             "frac": round(prefill_flop / (p_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                             "traffic": None,
+                             "work": "GEMM flop of the prefill (block projections at 4096 rows + "
+                                     "LM head at 8 rows) over the whole prefill time"},
+        "roofline_decode": {"bound": "hbm", "achieved": round(step_bytes / (g_ms / steps * 1e-3) / 1e9, 1),
+                            "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                            "frac": round(step_bytes / (g_ms / steps * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                            "traffic": None,
+                            "work": "bf16 weights (block + LM head) + K/V read per step (average "
+                                    "cache length) over the step time"},
+        "state": state,
     }
     dec.close()
     return res
 
 
 # ------------------------------------------------------------------ CPU baseline
-def cpu_baseline_gemm(a_buf, b_buf, rows: int, threads: int):
+# The reference's arithmetic restated in C (oracle/, gcc -O2 -ffp-contract=off,
+# kind "port") timed on this host's cores on a bounded sample of each
+# workload: one warm-up call, then the median of CPU_RUNS timed calls, on all
+# visible cores (<= 16) and on one thread.
+CPU_RUNS = 5
+
+
+def cpu_median_s(fn, runs: int = CPU_RUNS) -> float:
+    fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def cpu_entry(value_fn, unit: str, threads: int, sample: str, single_sample: str,
+              all_fn, single_fn) -> dict:
+    """Median-of-CPU_RUNS timings of all_fn (on `threads` cores) and
+    single_fn (one thread); value_fn(seconds, single) converts a time to the
+    metric's unit for that sample."""
+    t_all = cpu_median_s(all_fn)
+    t_one = cpu_median_s(single_fn)
+    return {"value": value_fn(t_all, False), "unit": unit, "cores": threads, "kind": "port",
+            "sample": f"{sample}; median of {CPU_RUNS} runs {t_all:.3f} s",
+            "median_of": CPU_RUNS,
+            "single_thread": {"value": value_fn(t_one, True), "unit": unit, "cores": 1,
+                              "sample": f"{single_sample}; median of {CPU_RUNS} runs {t_one:.3f} s"}}
+
+
+def cpu_baseline_c1(a_host, b_host, got_bits, threads: int) -> dict:
+    import oracle
+    n, k = a_host.shape
+    m = b_host.shape[1]
+    want = oracle.matmul_f32(a_host, b_host, threads=threads)
+    flop = 2.0 * n * m * k
+    e = cpu_entry(lambda t, one: flop / t / 1e9, "GFLOP/s", threads,
+                  f"the whole {n}x{m}x{k} f32 GEMM (sequential k-ascending fold)",
+                  f"the whole {n}x{m}x{k} f32 GEMM",
+                  lambda: oracle.matmul_f32(a_host, b_host, threads=threads),
+                  lambda: oracle.matmul_f32(a_host, b_host, threads=1))
+    e["gpu_bitwise_equal"] = bool(np.array_equal(got_bits, want.view(np.uint32)))
+    return e
+
+
+def cpu_baseline_gemm(a_buf, b_buf, threads: int) -> dict:
     import oracle
     n = k = m = 4096
     a16 = a_buf.read(np.uint16, (n, k))
     b16 = b_buf.read(np.uint16, (k, m))
-    sel = np.arange(rows, dtype=np.uint64)
-    oracle.matmul_bf16(a16, b16, rows=sel[:1], threads=1)  # warm
-    t0 = time.perf_counter()
-    oracle.matmul_bf16(a16, b16, rows=sel, threads=threads)
-    dt = time.perf_counter() - t0
-    flop = 2.0 * rows * m * k
-    return {"value": flop / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"{rows} of 4096 output rows of the 4096^3 bf16 GEMM, sequential "
-                      f"k-ascending f32 fold (oracle/catena_oracle.c, gcc -O2 "
-                      f"-ffp-contract=off), {dt:.1f} s"}
+    rows_all, rows_one = 512, 16
+    sel_all = np.arange(rows_all, dtype=np.uint64)
+    sel_one = np.arange(rows_one, dtype=np.uint64)
+    return cpu_entry(lambda t, one: 2.0 * (rows_one if one else rows_all) * m * k / t / 1e12,
+                     "TFLOP/s", threads,
+                     f"{rows_all} of 4096 output rows of the 4096^3 bf16 GEMM, sequential "
+                     f"k-ascending f32 fold (oracle/catena_oracle.c)",
+                     f"{rows_one} of 4096 output rows",
+                     lambda: oracle.matmul_bf16(a16, b16, rows=sel_all, threads=threads),
+                     lambda: oracle.matmul_bf16(a16, b16, rows=sel_one, threads=1))
 
 
-def cpu_baseline_attention(q, k, v, heads: int, threads: int):
+def cpu_baseline_decode_gemm(x16, w16, threads: int) -> dict:
+    import oracle
+    M, K = x16.shape
+    N = w16.shape[1]
+    nbytes = 2.0 * N * K + 2.0 * M * K + 2.0 * M * N
+    rows_one = 4
+    sel = np.arange(rows_one, dtype=np.uint64)
+    # one thread on 4 of the 16 rows (the fold's cost is per output cell),
+    # scaled to the whole launch's bytes
+    return cpu_entry(lambda t, one: nbytes / (t * (M / rows_one if one else 1.0)) / 1e9, "GB/s",
+                     threads, f"the whole M={M} x N={N} x K={K} decode GEMM",
+                     f"{rows_one} of {M} rows, time scaled x{M // rows_one}",
+                     lambda: oracle.matmul_bf16(x16, w16, threads=threads),
+                     lambda: oracle.matmul_bf16(x16, w16, rows=sel, threads=1))
+
+
+def cpu_baseline_attention(q, k, v, threads: int) -> dict:
     import oracle
     B, H, L, D = 32, 32, 4096, 128
-    # read the first `heads` (b, h) slices only
-    hl = np.arange(heads, dtype=np.uint32)
     q16 = q.read(np.uint16, (B, H, D))
-    nbh = heads
-    kk = k.read(np.uint16, (nbh * L * D,)).reshape(1, nbh, L, D)
-    vv = v.read(np.uint16, (nbh * L * D,)).reshape(1, nbh, L, D)
-    qq = q16.reshape(1, B * H, D)[:, :nbh]
+    n_all, n_one = 1024, 32
+
+    def slices(nbh):
+        kk = k.read(np.uint16, (nbh * L * D,)).reshape(1, nbh, L, D)
+        vv = v.read(np.uint16, (nbh * L * D,)).reshape(1, nbh, L, D)
+        return q16.reshape(1, B * H, D)[:, :nbh], kk, vv
+
+    qa, ka, va = slices(n_all)
     lens = np.array([L], np.uint32)
     scale = float(np.float32(1.0 / math.sqrt(D)))
-    t0 = time.perf_counter()
-    oracle.attn_decode(qq, kk, vv, lens, scale, threads=threads)
-    dt = time.perf_counter() - t0
-    nbytes = nbh * (2.0 * L * D * 2 + D * 2 + D * 4)
-    del hl
-    return {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{nbh} of 1024 (batch, head) slices, {dt:.1f} s"}
+    per = 2.0 * L * D * 2 + D * 2 + D * 4
+    return cpu_entry(lambda t, one: (n_one if one else n_all) * per / t / 1e9, "GB/s", threads,
+                     f"{n_all} of 1024 (batch, head) slices (sequential folds)",
+                     f"{n_one} of 1024 slices",
+                     lambda: oracle.attn_decode(qa, ka, va, lens, scale, threads=threads),
+                     lambda: oracle.attn_decode(qa[:, :n_one], ka[:, :n_one], va[:, :n_one], lens,
+                                                scale, threads=1))
+
+
+def cpu_baseline_decoder(st: dict, threads: int) -> dict:
+    """C5 on the oracle's whole-model sequential forward with the GPU model's
+    weights: one greedy decode step at batch 8 from the GPU prefill's caches
+    (cache length 512 -> 513), and the prefill of 8 tokens of one sequence."""
+    from oracle import decoder as od
+    w, kc, vc, nxt, tokens = st["weights"], st["kc"], st["vc"], st["next"], st["tokens"]
+    B, T = st["B"], st["T"]
+    mk = lambda th: od.DecoderOracle(w, st["H"], 128, st["F"], st["L"], threads=th)  # noqa: E731
+
+    def step_fn(th, batch):
+        o = mk(th)
+        o.load_cache([c[:batch] for c in kc], [c[:batch] for c in vc], T)
+        # each call appends one position (513, 514, ...): the same work
+        return lambda: o.step(nxt[:batch], batch)
+
+    pre_t = 8
+
+    def prefill_fn(th):
+        o = mk(th)
+        return lambda: o.prefill(tokens[:1, :pre_t], 1, pre_t)
+
+    dec = cpu_entry(lambda t, one: (1 if one else B) / t, "tokens/s", threads,
+                    f"one decode step, batch {B}, cache length {T} -> {T + 1}",
+                    f"one decode step of one sequence (batch 1)", step_fn(threads, B),
+                    step_fn(1, 1))
+    pre = cpu_entry(lambda t, one: pre_t / t, "tokens/s", threads,
+                    f"prefill of {pre_t} tokens of one sequence", f"prefill of {pre_t} tokens",
+                    prefill_fn(threads), prefill_fn(1))
+    return {"decode": dec, "prefill": pre}
 
 
 def bench_ceilings(ev: HipEvents) -> dict:
@@ -389,11 +577,17 @@ def main(argv=None) -> int:
     g = bench_gemm(args.steps, args.warmup, ev)
     extra = {}
     core = args.only in ("core", "all")
+    dec = c1 = at = dg = None
     if args.only in ("decoder", "all"):
         print("[bench] decoder block C5 (prefill 8x512, 128 greedy steps)", file=sys.stderr,
               flush=True)
-        extra["decoder_c5"] = bench_decoder(3, ev)
+        dec = bench_decoder(3, ev)
+        extra["decoder_c5"] = {k_: v for k_, v in dec.items() if k_ != "state"}
     if core:
+        print("[bench] C1 f32 GEMM 256^3 through program_matmul_2x2_via_mem", file=sys.stderr,
+              flush=True)
+        c1 = bench_c1(max(20, args.steps // 5), ev)
+        extra["c1_f32_gemm_program"] = {k_: v for k_, v in c1.items() if k_ != "inputs"}
         print("[bench] decode attention B32 H32 L4096 D128", file=sys.stderr, flush=True)
         at = bench_attention(max(5, args.steps // 5), max(2, args.warmup // 5), ev)
         print("[bench] decode GEMMs M=16", file=sys.stderr, flush=True)
@@ -405,9 +599,10 @@ def main(argv=None) -> int:
                 "per_launch_us": at["per_launch_us"],
                 "roofline": {"bound": "hbm", "achieved": at["GB/s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                              "frac": at["frac_hbm"],
-                             "traffic": measured_traffic("catena_attn_decode_bf16_d128_kc")},
+                             "traffic": measured_traffic("catena_attn_decode_bf16_d128")},
                 "bytes_per_launch": at["bytes_per_launch"]},
-            "decode_gemm_m16": dg,
+            "decode_gemm_m16": {k_: {kk: vv for kk, vv in v.items() if kk != "inputs"}
+                                for k_, v in dg.items()},
         })
     if args.copy_calibration:
         nbytes = 1 << 30
@@ -421,18 +616,25 @@ def main(argv=None) -> int:
     if not args.no_ceilings:
         print("[bench] ceilings (calibrate.hip)", file=sys.stderr, flush=True)
         extra["ceilings"] = bench_ceilings(ev)
+    ev.close()
     cpu = None
     if not args.no_cpu_baseline:
         threads = max(1, min(16, len(os.sched_getaffinity(0))))
-        print(f"[bench] cpu baseline ({threads} threads)", file=sys.stderr, flush=True)
+        print(f"[bench] cpu baselines ({threads} threads and 1 thread, median of {CPU_RUNS})",
+              file=sys.stderr, flush=True)
         a, b = g["inputs"]
-        cpu = cpu_baseline_gemm(a, b, rows=4096, threads=threads)
-        single = cpu_baseline_gemm(a, b, rows=64, threads=1)
-        extra["cpu_baseline_single_thread"] = {k_: single[k_] for k_ in ("value", "unit", "cores", "kind", "sample")}
+        cpu = cpu_baseline_gemm(a, b, threads)
         extra["host_cpu"] = host_cpu()
         if core:
+            a1, b1, got1 = c1["inputs"]
+            extra["c1_f32_gemm_program"]["cpu_baseline"] = cpu_baseline_c1(a1, b1, got1, threads)
             q, k, v = at["inputs"]
-            extra["decode_attention"]["cpu_baseline"] = cpu_baseline_attention(q, k, v, 1024, threads)
+            extra["decode_attention"]["cpu_baseline"] = cpu_baseline_attention(q, k, v, threads)
+            for key, v_ in dg.items():
+                x16, w16 = v_["inputs"]
+                extra["decode_gemm_m16"][key]["cpu_baseline"] = cpu_baseline_decode_gemm(x16, w16, threads)
+        if dec is not None:
+            extra["decoder_c5"]["cpu_baseline"] = cpu_baseline_decoder(dec["state"], threads)
 
     tflops = g["tflops"]
     line = {
@@ -459,7 +661,8 @@ def main(argv=None) -> int:
         "cpu_baseline": cpu,
         "extra": extra,
     }
-    print(json.dumps(line))
+    print(json.dumps(line), flush=True)
+    ca.shutdown()
     return 0
 
 

@@ -75,6 +75,11 @@ def build(jobs: int = 8) -> list[str]:
         raise RuntimeError(f"hipcc not found at {HIPCC}")
     os.makedirs(OUT, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(KDIR, "*.hip")))
+    # code objects whose source is gone would otherwise linger in lib/
+    live = {os.path.splitext(os.path.basename(s))[0] for s in srcs}
+    for co in glob.glob(os.path.join(OUT, "*.co")):
+        if os.path.splitext(os.path.basename(co))[0] not in live:
+            os.remove(co)
     with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         futs = [ex.submit(build_kernel, s) for s in srcs]
         futs.append(ex.submit(build_host))

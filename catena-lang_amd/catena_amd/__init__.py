@@ -111,6 +111,7 @@ _int = ctypes.c_int
 # name -> (restype, argtypes); the list is the header's full export surface.
 SIGNATURES = {
     "catena_mi355x_init": (_int, [_int]),
+    "catena_mi355x_shutdown": (_int, []),
     "catena_mi355x_last_error": (ctypes.c_char_p, []),
     "catena_mi355x_stream": (_vp, []),
     "catena_mi355x_synchronize": (_int, []),
@@ -122,6 +123,8 @@ SIGNATURES = {
     "catena_pool_trim": (_int, []),
     "catena_mi355x_gemm_f32_exact": (_int, [_vp, _vp, _vp, _u64, _u64, _u64]),
     "catena_mi355x_gemm_bf16": (_int, [_vp, _vp, _vp, _u64, _u64, _u64, _int]),
+    "catena_mi355x_gemm_bf16_decode_plan": (_int, [_u64, _u64, _u64, ctypes.POINTER(_u32),
+                                                   ctypes.POINTER(_u64)]),
     "catena_mi355x_attn_decode_bf16": (_int, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _f32]),
     "catena_mi355x_softmax_f32": (_int, [_vp, _vp, _u64, _u64]),
     "catena_mi355x_exp_approx_f32": (_int, [_vp, _vp, _u64]),
@@ -207,8 +210,26 @@ def check(status: int) -> None:
         raise CatenaError(status, last_error())
 
 
+_atexit_registered = False
+
+
 def init(device: int = 0) -> None:
+    """Initialise the library on `device`; an orderly shutdown is registered
+    to run at interpreter exit (before the HIP runtime's own teardown)."""
+    global _atexit_registered
     check(lib().catena_mi355x_init(device))
+    if not _atexit_registered:
+        import atexit
+        atexit.register(shutdown)
+        _atexit_registered = True
+
+
+def shutdown() -> None:
+    """catena_mi355x_shutdown: wait for the library stream, release the
+    library's own device memory, unload its code objects, destroy the
+    stream."""
+    if _lib is not None:
+        check(_lib.catena_mi355x_shutdown())
 
 
 def synchronize() -> None:
@@ -286,6 +307,15 @@ def gemm_f32_exact(a, b, c, n: int, m: int, k: int) -> None:
 
 def gemm_bf16(a, b, c, n: int, m: int, k: int, out_f32: bool = False) -> None:
     check(lib().catena_mi355x_gemm_bf16(_p(a), _p(b), _p(c), n, m, k, 1 if out_f32 else 0))
+
+
+def gemm_bf16_decode_plan(n: int, m: int, k: int):
+    """(k groups, partials bytes) of the decode-shape GEMM for this shape;
+    needs no device."""
+    groups, nbytes = _u32(), _u64()
+    check(lib().catena_mi355x_gemm_bf16_decode_plan(n, m, k, ctypes.byref(groups),
+                                                    ctypes.byref(nbytes)))
+    return groups.value, nbytes.value
 
 
 def attn_decode_bf16(q, k, v, lens, o, batch: int, heads: int, max_len: int, head_dim: int,

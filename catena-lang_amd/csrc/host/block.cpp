@@ -35,10 +35,10 @@ int rmsnorm_launch(const float* x, const float* resid, const uint32_t* row_index
       return fail(CATENA_ERR_INVALID_ARGUMENT, "rmsnorm bf16 output must be 8-byte aligned");
   }
   const uint64_t n_pad = (n + 3) & ~3ull;
-  const size_t lds = 2 * n_pad * sizeof(float);
-  if (lds > device().max_lds)
+  const size_t lds = 2 * n_pad * sizeof(float);  // dynamic part
+  if (rmsnorm_lds_bytes(n) > device().max_lds)
     return fail(CATENA_ERR_UNSUPPORTED, "rmsnorm row of %llu needs %zu B of LDS",
-                (unsigned long long)n, lds);
+                (unsigned long long)n, rmsnorm_lds_bytes(n));
   uint32_t n32 = (uint32_t)n;
   void* args[] = {&x, &resid, &row_index, &h_out, &y_f32, &y_bf16, &n32, &tokens, &table, &vocab};
   return launch(KernelId::RmsnormRows, dim3((unsigned)rows), dim3(256), lds, args);
@@ -72,13 +72,10 @@ int catena_mi355x_attn_causal_bf16(const uint16_t* q, const uint16_t* k, const u
   if (blocks > 0x7FFFFFFFu) return fail(CATENA_ERR_UNSUPPORTED, "too many queries");
   // Many queries per sequence: the block-of-16-queries kernel, which reads
   // each K / V row once per block (its score buffer grows with max_len, so
-  // it is used while two workgroups still fit a CU).  CATENA_ATTN_PREFILL=0
-  // selects the one-query-per-workgroup kernel for comparison; both give the
-  // same bits.
+  // it is used while two workgroups still fit a CU); otherwise the
+  // one-query-per-workgroup kernel.  Both give the same bits.
   const size_t lds_pf = 16 * 128 * 4 + 64 * 128 * 2 + 3 * 16 * 4 + (size_t)max_len * 17 * 4;
-  const char* pf = getenv("CATENA_ATTN_PREFILL");
-  const bool prefill_ok = !(pf && strcmp(pf, "0") == 0);
-  if (prefill_ok && tq >= 8 && lds_pf <= 80 * 1024) {
+  if (tq >= 8 && lds_pf <= 80 * 1024) {
     const uint64_t nqb = ceil_div(tq, 16);
     const uint64_t grid = (uint64_t)batch * heads * nqb;
     if (grid > 0x7FFFFFFFu) return fail(CATENA_ERR_UNSUPPORTED, "too many query blocks");

@@ -34,6 +34,11 @@ struct catena_decoder {
   void* act[CATENA_DEC_TENSOR_COUNT] = {};
   void* final_rows = nullptr;  // [max_batch] u32: index of each sequence's last row
   void* cur_tok = nullptr;     // [max_batch] u32: next input token per sequence
+  // pinned host staging of final_rows; rows_copied marks the end of the last
+  // copy out of it, so it is not rewritten while a copy may still read it
+  uint32_t* rows_host = nullptr;
+  hipEvent_t rows_copied = nullptr;
+  bool rows_pending = false;
   uint32_t batch = 0, cur_len = 0, last_rows = 0;
 };
 
@@ -100,6 +105,10 @@ void release(catena_decoder* m) {
   }
   pool_free(m->final_rows);
   pool_free(m->cur_tok);
+  if (m->rows_copied) hipEventDestroy(m->rows_copied);
+  m->rows_copied = nullptr;
+  if (m->rows_host) hipHostFree(m->rows_host);
+  m->rows_host = nullptr;
 }
 
 #define TRY(expr)              \
@@ -221,6 +230,11 @@ int catena_mi355x_decoder_create(const catena_decoder_config_t* cfg, catena_deco
   if (attn_lds > device().max_lds)
     return fail(CATENA_ERR_UNSUPPORTED, "max_len %u exceeds the attention's LDS (%zu B > %zu B)",
                 c.max_len, attn_lds, device().max_lds);
+  // every RMSNorm holds a row of d_model values (and their squares) in LDS
+  const size_t norm_lds = rmsnorm_lds_bytes(c.d_model);
+  if (norm_lds > device().max_lds)
+    return fail(CATENA_ERR_UNSUPPORTED, "d_model %u exceeds the RMSNorm's LDS (%zu B > %zu B)",
+                c.d_model, norm_lds, device().max_lds);
   if (c.max_batch > 4096 || c.n_heads > 4096 || c.n_layers > 4096 || c.ffn_dim > (1u << 24) ||
       c.vocab > (1u << 26))
     return fail(CATENA_ERR_UNSUPPORTED,
@@ -265,6 +279,12 @@ int catena_mi355x_decoder_create(const catena_decoder_config_t* cfg, catena_deco
   if ((st = alloc(c.max_batch * 4, &m->act[CATENA_DEC_LENS]))) return fail_out(st);
   if ((st = alloc(c.max_batch * 4, &m->final_rows))) return fail_out(st);
   if ((st = alloc(c.max_batch * 4, &m->cur_tok))) return fail_out(st);
+  if ((st = hip_check(hipHostMalloc(reinterpret_cast<void**>(&m->rows_host), c.max_batch * 4),
+                      "hipHostMalloc(final rows)")))
+    return fail_out(st);
+  if ((st = hip_check(hipEventCreateWithFlags(&m->rows_copied, hipEventDisableTiming),
+                      "hipEventCreate(final rows)")))
+    return fail_out(st);
 
   // host-computed tables: RoPE frequencies and the uniform-length lens rows
   std::vector<float> inv;
@@ -356,13 +376,16 @@ int catena_mi355x_decoder_prefill(catena_decoder_t* dec, const uint32_t* tokens,
     return fail(CATENA_ERR_INVALID_ARGUMENT, "batch %u outside 1..%u", batch, c.max_batch);
   if (t == 0 || t > c.max_len)
     return fail(CATENA_ERR_INVALID_ARGUMENT, "prefill length %u outside 1..%u", t, c.max_len);
-  std::vector<uint32_t> rows(batch);
-  for (uint32_t b = 0; b < batch; ++b) rows[b] = b * t + (t - 1);
   Device& dv = device();
-  // pageable source: HIP stages it before the call returns
-  TRY(hip_check(hipMemcpyAsync(m.final_rows, rows.data(), batch * 4, hipMemcpyHostToDevice,
+  // the staging buffer is pinned, so the copy below reads it when the stream
+  // reaches it: wait for the previous prefill's copy before rewriting it
+  if (m.rows_pending) TRY(hip_check(hipEventSynchronize(m.rows_copied), "hipEventSynchronize"));
+  for (uint32_t b = 0; b < batch; ++b) m.rows_host[b] = b * t + (t - 1);
+  TRY(hip_check(hipMemcpyAsync(m.final_rows, m.rows_host, batch * 4, hipMemcpyHostToDevice,
                                dv.stream),
                 "hipMemcpyAsync(final rows)"));
+  TRY(hip_check(hipEventRecord(m.rows_copied, dv.stream), "hipEventRecord(final rows)"));
+  m.rows_pending = true;
   const uint32_t* lens = static_cast<const uint32_t*>(m.lens_table) + (uint64_t)t * c.max_batch;
   m.batch = batch;
   m.last_rows = batch * t;

@@ -52,28 +52,10 @@ struct KernelSpec {
 
 const KernelSpec kKernels[] = {
     {KernelId::GemmF32Exact, "gemm_f32_exact", "catena_gemm_f32_exact"},
-    {KernelId::GemmBf16TileBf16, "gemm_bf16", "catena_gemm_bf16_tile_bf16out"},
-    {KernelId::GemmBf16TileF32, "gemm_bf16", "catena_gemm_bf16_tile_f32out"},
     {KernelId::GemmBf16EdgeBf16, "gemm_bf16", "catena_gemm_bf16_edge_bf16out"},
     {KernelId::GemmBf16EdgeF32, "gemm_bf16", "catena_gemm_bf16_edge_f32out"},
-    {KernelId::GemmBf16LdsV0Bf16, "gemm_bf16_lds", "catena_gemm_bf16_lds_v0_bf16out"},
-    {KernelId::GemmBf16LdsV1Bf16, "gemm_bf16_lds", "catena_gemm_bf16_lds_v1_bf16out"},
-    {KernelId::GemmBf16LdsV2Bf16, "gemm_bf16_lds", "catena_gemm_bf16_lds_v2_bf16out"},
-    {KernelId::GemmBf16LdsV3Bf16, "gemm_bf16_lds", "catena_gemm_bf16_lds_v3_bf16out"},
-    {KernelId::GemmBf16LdsV4Bf16, "gemm_bf16_lds", "catena_gemm_bf16_lds_v4_bf16out"},
-    {KernelId::GemmBf16LdsV5Bf16, "gemm_bf16_lds", "catena_gemm_bf16_lds_v5_bf16out"},
-    {KernelId::GemmBf16LdsV7Bf16, "gemm_bf16_lds", "catena_gemm_bf16_lds_v7_bf16out"},
-    {KernelId::GemmBf16LdsV0F32, "gemm_bf16_lds", "catena_gemm_bf16_lds_v0_f32out"},
-    {KernelId::GemmBf16LdsV1F32, "gemm_bf16_lds", "catena_gemm_bf16_lds_v1_f32out"},
-    {KernelId::GemmBf16LdsV2F32, "gemm_bf16_lds", "catena_gemm_bf16_lds_v2_f32out"},
-    {KernelId::GemmBf16LdsV3F32, "gemm_bf16_lds", "catena_gemm_bf16_lds_v3_f32out"},
-    {KernelId::GemmBf16LdsV4F32, "gemm_bf16_lds", "catena_gemm_bf16_lds_v4_f32out"},
-    {KernelId::GemmBf16LdsV5F32, "gemm_bf16_lds", "catena_gemm_bf16_lds_v5_f32out"},
-    {KernelId::GemmBf16LdsV7F32, "gemm_bf16_lds", "catena_gemm_bf16_lds_v7_f32out"},
-    {KernelId::GemmBf16DeepBf16, "gemm_bf16_deep", "catena_gemm_bf16_deep4_bf16out"},
-    {KernelId::GemmBf16DeepF32, "gemm_bf16_deep", "catena_gemm_bf16_deep4_f32out"},
-    {KernelId::GemmBf16DeepFrontBf16, "gemm_bf16_deep", "catena_gemm_bf16_deep4f_bf16out"},
-    {KernelId::GemmBf16DeepFrontF32, "gemm_bf16_deep", "catena_gemm_bf16_deep4f_f32out"},
+    {KernelId::GemmBf16LdsBf16, "gemm_bf16_lds", "catena_gemm_bf16_lds_bf16out"},
+    {KernelId::GemmBf16LdsF32, "gemm_bf16_lds", "catena_gemm_bf16_lds_f32out"},
     {KernelId::GemmBf16K32Bf16, "gemm_bf16_k32", "catena_gemm_bf16_k32_bf16out"},
     {KernelId::GemmBf16K32F32, "gemm_bf16_k32", "catena_gemm_bf16_k32_f32out"},
     {KernelId::GemmBf16K32N128Bf16, "gemm_bf16_k32", "catena_gemm_bf16_k32n128_bf16out"},
@@ -86,7 +68,6 @@ const KernelSpec kKernels[] = {
     {KernelId::GemmBf16DecodeSilu, "gemm_bf16_decode", "catena_gemm_bf16_decode_silu"},
     {KernelId::GemmBf16DecodeArgmax, "gemm_bf16_decode", "catena_gemm_bf16_decode_argmax"},
     {KernelId::AttnDecodeD128, "attn_decode", "catena_attn_decode_bf16_d128"},
-    {KernelId::AttnDecodeD128KC, "attn_decode", "catena_attn_decode_bf16_d128_kc"},
     {KernelId::AttnCausalD128F32, "attn_decode", "catena_attn_causal_bf16_d128_f32out"},
     {KernelId::AttnCausalD128Bf16, "attn_decode", "catena_attn_causal_bf16_d128_bf16out"},
     {KernelId::AttnPrefillD128F32, "attn_prefill", "catena_attn_prefill_bf16_d128_f32out"},
@@ -266,24 +247,29 @@ using namespace catena;
 extern "C" {
 
 namespace {
-// Undo a partial init (stream, ticket block, loaded modules) so a later call
-// starts clean.
-int init_failed(int status, hipModule_t* mods, size_t n_mods) {
-  Device& d = device();
-  for (size_t i = 0; i < n_mods; ++i) hipModuleUnload(mods[i]);
+std::mutex g_init_mu;  // serialises init and shutdown
+
+// Release what init set up (loaded modules, ticket block, stream); used to
+// undo a partial init and by shutdown.
+void release_device(Device& d) {
+  for (int i = 0; i < d.n_modules; ++i) hipModuleUnload(d.modules[i]);
+  d.n_modules = 0;
   if (d.small) hipFree(d.small);
   d.small = nullptr;
   if (d.stream) hipStreamDestroy(d.stream);
   d.stream = nullptr;
   for (hipFunction_t& f : d.fn) f = nullptr;
+}
+
+int init_failed(int status) {
+  release_device(device());
   return status;
 }
 }  // namespace
 
 int catena_mi355x_init(int device_index) {
   Device& d = device();
-  static std::mutex init_mu;
-  std::lock_guard<std::mutex> g(init_mu);
+  std::lock_guard<std::mutex> g(g_init_mu);
   if (d.ready.load(std::memory_order_acquire)) return CATENA_OK;
   int count = 0;
   if (hipGetDeviceCount(&count) != hipSuccess || count == 0)
@@ -301,41 +287,59 @@ int catena_mi355x_init(int device_index) {
   d.max_lds = prop.sharedMemPerBlock;
   d.cu_count = prop.multiProcessorCount;
   st = hip_check(hipStreamCreateWithFlags(&d.stream, hipStreamNonBlocking), "hipStreamCreate");
-  if (st) return init_failed(st, nullptr, 0);
+  if (st) return init_failed(st);
   void* small = nullptr;
   st = hip_check(hipMalloc(&small, Device::kSmallBytes), "hipMalloc(tickets)");
-  if (st) return init_failed(st, nullptr, 0);
+  if (st) return init_failed(st);
   d.small = static_cast<unsigned char*>(small);
   st = hip_check(hipMemset(small, 0, Device::kSmallBytes), "hipMemset(tickets)");
-  if (st) return init_failed(st, nullptr, 0);
+  if (st) return init_failed(st);
   const std::string dir = library_dir();
   std::unordered_map<std::string, hipModule_t> modules;
-  std::vector<hipModule_t> loaded;
   for (const KernelSpec& k : kKernels) {
     auto it = modules.find(k.module);
     if (it == modules.end()) {
+      if (d.n_modules == Device::kMaxModules)
+        return init_failed(fail(CATENA_ERR_LOAD, "more than %d code objects", Device::kMaxModules));
       const std::string path = dir + "/" + k.module + ".co";
       hipModule_t m = nullptr;
       hipError_t e = hipModuleLoad(&m, path.c_str());
       if (e != hipSuccess)
         return init_failed(fail(CATENA_ERR_LOAD, "hipModuleLoad(%s): %s", path.c_str(),
-                                hipGetErrorString(e)),
-                           loaded.data(), loaded.size());
-      loaded.push_back(m);
+                                hipGetErrorString(e)));
+      d.modules[d.n_modules++] = m;
       it = modules.emplace(k.module, m).first;
     }
     hipFunction_t f = nullptr;
     hipError_t e = hipModuleGetFunction(&f, it->second, k.symbol);
     if (e != hipSuccess)
       return init_failed(fail(CATENA_ERR_LOAD, "hipModuleGetFunction(%s): %s", k.symbol,
-                              hipGetErrorString(e)),
-                         loaded.data(), loaded.size());
+                              hipGetErrorString(e)));
     d.fn[static_cast<int>(k.id)] = f;
   }
   d.device = device_index;
   d.ready.store(true, std::memory_order_release);
   clear_error();
   return CATENA_OK;
+}
+
+int catena_mi355x_shutdown(void) {
+  Device& d = device();
+  std::lock_guard<std::mutex> g(g_init_mu);
+  if (!d.ready.load(std::memory_order_acquire)) return CATENA_OK;
+  // every queued kernel has finished before anything it may use goes away
+  const int st = hip_check(hipStreamSynchronize(d.stream), "hipStreamSynchronize");
+  {
+    std::lock_guard<std::mutex> ws(d.ws_mu);
+    if (d.ws) pool_free(d.ws);
+    d.ws = nullptr;
+    d.ws_bytes = 0;
+  }
+  catena_pool_trim();  // cached blocks go back to the device
+  d.ready.store(false, std::memory_order_release);
+  release_device(d);
+  d.device = -1;
+  return st;
 }
 
 const char* catena_mi355x_last_error(void) { return last_error(); }

@@ -14,33 +14,15 @@ namespace catena {
 
 enum class KernelId : int {
   GemmF32Exact = 0,
-  GemmBf16TileBf16,
-  GemmBf16TileF32,
-  GemmBf16EdgeBf16,
+  GemmBf16EdgeBf16,  // general shapes, bounds-checked (gemm_bf16.hip)
   GemmBf16EdgeF32,
-  GemmBf16LdsV0Bf16,  // direct-to-LDS tile kernels, scheduling variants (see kernels.cpp)
-  GemmBf16LdsV1Bf16,
-  GemmBf16LdsV2Bf16,
-  GemmBf16LdsV3Bf16,
-  GemmBf16LdsV4Bf16,
-  GemmBf16LdsV5Bf16,
-  GemmBf16LdsV7Bf16,
-  GemmBf16LdsV0F32,
-  GemmBf16LdsV1F32,
-  GemmBf16LdsV2F32,
-  GemmBf16LdsV3F32,
-  GemmBf16LdsV4F32,
-  GemmBf16LdsV5F32,
-  GemmBf16LdsV7F32,
-  GemmBf16DeepBf16,
-  GemmBf16DeepF32,
-  GemmBf16DeepFrontBf16,
-  GemmBf16DeepFrontF32,
+  GemmBf16LdsBf16,  // aligned tiles with K % 128 != 0: two 64-k stages (gemm_bf16_lds.hip)
+  GemmBf16LdsF32,
   GemmBf16K32Bf16,  // four 32-k stages, spread buffer loads, LDS-staged epilogue (default)
   GemmBf16K32F32,
   GemmBf16K32N128Bf16,  // the same on 256 x 128 tiles
   GemmBf16K32N128F32,
-  GemmBf16K32Silu,  // variants 9 / 10 with the SwiGLU epilogue
+  GemmBf16K32Silu,  // the 32-k kernels with the SwiGLU epilogue
   GemmBf16K32N128Silu,
   GemmBf16DecodeF32,
   GemmBf16DecodeBf16,
@@ -48,7 +30,6 @@ enum class KernelId : int {
   GemmBf16DecodeSilu,
   GemmBf16DecodeArgmax,
   AttnDecodeD128,
-  AttnDecodeD128KC,
   AttnCausalD128F32,
   AttnCausalD128Bf16,
   AttnPrefillD128F32,
@@ -83,6 +64,10 @@ struct Device {
   size_t max_lds = 0;
   int cu_count = 0;
   hipFunction_t fn[static_cast<int>(KernelId::Count)] = {};
+  // code objects loaded at init (unloaded by catena_mi355x_shutdown)
+  static constexpr int kMaxModules = 32;
+  hipModule_t modules[kMaxModules] = {};
+  int n_modules = 0;
   void* ws = nullptr;  // split-K partials
   uint64_t ws_bytes = 0;
   // Zeroed once at init; kernels that take completion tickets return their
@@ -106,6 +91,14 @@ struct Device {
 // K / V staging area, reduction slots, then one f32 score per position.
 constexpr size_t kAttnLdsFixed = 128 * 4 + 16384 + 64;
 inline size_t attn_lds_bytes(uint32_t max_len) { return kAttnLdsFixed + (size_t)max_len * 4; }
+
+// LDS of catena_rmsnorm_rows (block.hip): its static __shared__ f32 (rounded
+// up to the 16-byte alignment of the dynamic area that follows it) plus the
+// dynamic row of h and of its squares, n rounded up to a multiple of 4.
+constexpr size_t kRmsnormLdsStatic = 16;
+inline size_t rmsnorm_lds_bytes(uint64_t n) {
+  return kRmsnormLdsStatic + 2 * ((n + 3) & ~3ull) * sizeof(float);
+}
 
 Device& device();
 int ensure_init();
@@ -137,9 +130,17 @@ struct DecodeEpiArgs {
 enum class DecodeEpilogue { StoreF32, StoreBf16, Rope, Silu, Argmax };
 // Decode-shape GEMM (n <= 16) with an epilogue; c is Y (f32, or bf16 for
 // StoreBf16).  Rope: m = 3 * heads * 128, one token per row; Silu: gate / up
-// interleaved in 64-column groups, act[n][m/2]; Argmax: idx[n].
+// interleaved in 64-column groups, act[n][m/2]; Argmax: idx[n].  The split-K
+// partials go to `scratch` (scratch_bytes long) when it is not NULL, else to
+// the library's pool-backed workspace.
 int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, uint64_t m,
-                     uint64_t k, DecodeEpilogue epi, const DecodeEpiArgs& ep);
+                     uint64_t k, DecodeEpilogue epi, const DecodeEpiArgs& ep,
+                     void* scratch = nullptr, uint64_t scratch_bytes = 0);
+// Bytes of split-K partials the decode GEMM needs for an (n x k) * (k x m)
+// product (0 when K is not split), and its number of k groups; a function of
+// the shape alone.
+uint64_t decode_partials_bytes(uint64_t n, uint64_t m, uint64_t k, uint32_t* k_groups);
+
 // Whether catena_mi355x_gemm_bf16_silu takes this shape (the 32-k tile
 // kernels: n % 256, m % 128, k % 128 == 0, aligned operands).
 bool gemm_bf16_silu_fits(uint64_t n, uint64_t m, uint64_t k, const void* a, const void* b,

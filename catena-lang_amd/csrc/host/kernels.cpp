@@ -1,4 +1,4 @@
-// Kernel ABI: shape checks, variant selection and launches.
+// Kernel ABI: shape checks, kernel selection and launches.
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
@@ -11,46 +11,6 @@ namespace {
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
-
-// Aligned-shape bf16 GEMM kernels.  All compute the same 256x256 tiles with
-// the same per-accumulator k32 order (bitwise identical outputs); they differ
-// in scheduling only.  CATENA_GEMM_VARIANT selects one for comparison.
-struct GemmVariant {
-  KernelId bf16, f32;
-  uint64_t min_k;  // K must be a multiple of 64 and at least this
-};
-const GemmVariant kGemmVariants[] = {
-    /* 0 two barriers per 64-k slab */
-    {KernelId::GemmBf16LdsV0Bf16, KernelId::GemmBf16LdsV0F32, 64},
-    /* 1 v0 + MFMA priority */
-    {KernelId::GemmBf16LdsV1Bf16, KernelId::GemmBf16LdsV1F32, 64},
-    /* 2 one barrier per slab, fragment double-buffering */
-    {KernelId::GemmBf16LdsV2Bf16, KernelId::GemmBf16LdsV2F32, 64},
-    /* 3 v2 + MFMA priority */
-    {KernelId::GemmBf16LdsV3Bf16, KernelId::GemmBf16LdsV3F32, 64},
-    /* 4 v2 with LDS reads interleaved 1:2 with MFMAs */
-    {KernelId::GemmBf16LdsV4Bf16, KernelId::GemmBf16LdsV4F32, 64},
-    /* 5 v4 + MFMA priority */
-    {KernelId::GemmBf16LdsV5Bf16, KernelId::GemmBf16LdsV5F32, 64},
-    /* 6 four 32-k stages, three slabs in flight (gemm_bf16_deep.hip) */
-    {KernelId::GemmBf16DeepBf16, KernelId::GemmBf16DeepF32, 128},
-    /* 7 v4 with reads front-loaded 1:1 */
-    {KernelId::GemmBf16LdsV7Bf16, KernelId::GemmBf16LdsV7F32, 64},
-    /* 8 v6 with reads front-loaded 1:1 */
-    {KernelId::GemmBf16DeepFrontBf16, KernelId::GemmBf16DeepFrontF32, 128},
-    /* 9 four 32-k stages through buffer loads spread over the MFMAs, LDS-staged
-       bf16 epilogue (gemm_bf16_k32.hip) */
-    {KernelId::GemmBf16K32Bf16, KernelId::GemmBf16K32F32, 128},
-    /* 10 variant 9 on 256 x 128 tiles (8 waves of 64 x 64) */
-    {KernelId::GemmBf16K32N128Bf16, KernelId::GemmBf16K32N128F32, 128},
-};
-constexpr int kGemmVariantCount = sizeof(kGemmVariants) / sizeof(kGemmVariants[0]);
-// Default: variant 9 when K % 128 == 0 (and its 32-bit buffer offsets hold),
-// else variant 7; variant 9 on 256 x 128 tiles (10) when that takes fewer
-// rounds of the chip (see prefer_n128).
-constexpr int kGemmDefaultVariant = 9;
-constexpr int kGemmFallbackVariant = 7;
-constexpr int kGemmN128Variant = 10;
 
 // 256 x 128 tiles instead of 256 x 256: measured on the box, a round of
 // 256 x 128 tiles (one per CU) takes ~0.6 of a round of 256 x 256 tiles at the
@@ -65,29 +25,31 @@ bool prefer_n128(uint64_t rows, uint64_t cols, int cu_count) {
   return 0.62 * r_narrow < r_wide;
 }
 
-// k per wave for the decode kernel, in whole 32-k MFMA steps.
-// Streaming path (K % 32 == 0, one 4-wave workgroup per CU for its 144 KiB
-// LDS ring; each wave keeps 36 KiB in flight): the fewest k groups that
-// still give every CU a workgroup, so one round of workgroups streams the
-// weight and few partials are added, but no fewer than 8 steps per wave,
-// or 2 when the weight is at most 16 MiB: such a kernel is bound by
-// latency, not by HBM, and more workgroups shorten each stream (measured:
-// 8 x 2048 x 2048 takes 7.5 us at 2 steps per wave against 9.4 us at 8;
-// the C3 shapes and the larger decoder projections are fastest at the
-// 8-step floor or within 0.5 us of it).  Register path: ~1500 waves.
-// CATENA_DECODE_KW overrides.
-uint32_t decode_kw(uint64_t n_cols, uint64_t k, int cu_count, bool regs_path) {
-  const char* env = getenv("CATENA_DECODE_KW");
-  if (env && *env) {
-    long v = strtol(env, nullptr, 10);
-    if (v >= 32 && v % 32 == 0) return (uint32_t)v;
-  }
+// Column blocks x k groups the decode kernel spreads a weight over: the
+// MI355X's 256 CUs, one 4-wave workgroup per CU.  A constant, not the
+// device's CU count: the k grouping fixes which partial sums are added
+// together, so it must depend on the shape alone for the bits to be the same
+// on every device (a partitioned MI355X shows fewer CUs).
+constexpr uint64_t kDecodeSpread = 256;
+
+// k per wave for the decode kernel, in whole 32-k MFMA steps, from (N, K)
+// only.  Streaming path (K % 32 == 0, one 4-wave workgroup per CU for its
+// 144 KiB LDS ring; each wave keeps 36 KiB in flight): the fewest k groups
+// that still give each of the 256 CUs a workgroup, so one round of
+// workgroups streams the weight and few partials are added, but no fewer
+// than 8 steps per wave, or 2 when the weight is at most 16 MiB: such a
+// kernel is bound by latency, not by HBM, and more workgroups shorten each
+// stream (measured: 8 x 2048 x 2048 takes 7.5 us at 2 steps per wave against
+// 9.4 us at 8; the C3 shapes and the larger decoder projections are fastest
+// at the 8-step floor or within 0.5 us of it).  Register path (K % 32 != 0):
+// ~1500 waves.
+uint32_t decode_kw(uint64_t n_cols, uint64_t k, bool regs_path) {
   const uint64_t blocks = ceil_div(n_cols, 128);
   uint64_t kw;
   if (!regs_path) {
     // at least 8 steps of 32 k per wave: shorter chunks pay the ring's fill
     // and the partials' reduction more often than they gain in spread
-    uint64_t groups = blocks >= (uint64_t)cu_count ? 1 : (uint64_t)cu_count / blocks;
+    const uint64_t groups = blocks >= kDecodeSpread ? 1 : kDecodeSpread / blocks;
     kw = ceil_div(k, 4 * groups);
     kw = ceil_div(kw, 32) * 32;
     const uint64_t min_kw = n_cols * k * 2 <= (16ull << 20) ? 64 : 256;
@@ -104,8 +66,16 @@ uint32_t decode_kw(uint64_t n_cols, uint64_t k, int cu_count, bool regs_path) {
 
 namespace catena {
 
+uint64_t decode_partials_bytes(uint64_t n, uint64_t m, uint64_t k, uint32_t* k_groups) {
+  const uint32_t kw = decode_kw(m, k, k % 32 != 0);
+  const uint64_t S = ceil_div(ceil_div(k, kw), 4);
+  if (k_groups) *k_groups = S > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)S;
+  return S > 1 ? S * n * m * sizeof(float) : 0;
+}
+
 int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, uint64_t m,
-                     uint64_t k, DecodeEpilogue epi, const DecodeEpiArgs& ep) {
+                     uint64_t k, DecodeEpilogue epi, const DecodeEpiArgs& ep, void* scratch,
+                     uint64_t scratch_bytes) {
   int st = ensure_init();
   if (st) return st;
   if (n == 0 || m == 0) return CATENA_OK;
@@ -114,9 +84,11 @@ int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, 
     return fail(CATENA_ERR_INVALID_ARGUMENT, "decode GEMM shape or alignment");
   Device& d = device();
   const uint32_t M = (uint32_t)n;
-  const char* dpath = getenv("CATENA_DECODE_PATH");
-  const bool regs_path = k % 32 != 0 || (dpath && strcmp(dpath, "regs") == 0);
-  const uint32_t kw = decode_kw(m, k, d.cu_count > 0 ? d.cu_count : 256, regs_path);
+  // streaming ring (4 waves x 4 stages x 9 KiB) when K % 32 == 0, else the
+  // register path with the reduction buffers only (3 x 8 KiB partials + the
+  // 16 x 132 f32 tile)
+  const bool regs_path = k % 32 != 0;
+  const uint32_t kw = decode_kw(m, k, regs_path);
   const uint64_t chunks = ceil_div(k, kw);
   const uint64_t S = ceil_div(chunks, 4);
   const uint64_t gx = ceil_div(m, 128);
@@ -152,24 +124,30 @@ int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, 
   if (S > 1) {
     // the partials are addressed through one buffer descriptor with 32-bit
     // byte offsets
-    if (S * M * m * sizeof(float) >= (1ull << 31))
+    const uint64_t pbytes = S * M * m * sizeof(float);
+    if (pbytes >= (1ull << 31))
       return fail(CATENA_ERR_UNSUPPORTED, "decode GEMM partials exceed 2 GiB (%llu k groups)",
                   (unsigned long long)S);
-    void* ws = nullptr;
-    st = workspace(S * M * m * sizeof(float), &ws);
-    if (st) return st;
-    P = static_cast<float*>(ws);
+    if (scratch) {
+      // caller-provided scratch (the allocation-free entry point)
+      if (pbytes > scratch_bytes)
+        return fail(CATENA_ERR_UNSUPPORTED,
+                    "decode GEMM partials need %llu B of scratch, more than the %llu B available",
+                    (unsigned long long)pbytes, (unsigned long long)scratch_bytes);
+      P = static_cast<float*>(scratch);
+    } else {
+      void* ws = nullptr;
+      st = workspace(pbytes, &ws);
+      if (st) return st;
+      P = static_cast<float*>(ws);
+    }
   }
   const uint16_t* X = a;
   const uint16_t* W = b;
   void* Y = c;
   uint64_t N = m, K = k;
   uint32_t* tickets = d.gemm_tickets();
-  // streaming ring (4 waves x 4 stages x 9 KiB) when K % 32 == 0, else the
-  // reduction buffers only (3 x 8 KiB partials + the 16 x 132 f32 tile);
-  // CATENA_DECODE_PATH=regs selects the register path for comparison
-  const char* path = getenv("CATENA_DECODE_PATH");
-  uint32_t stream_lds = (k % 32 == 0 && !(path && strcmp(path, "regs") == 0)) ? 1u : 0u;
+  uint32_t stream_lds = regs_path ? 0u : 1u;
   const size_t lds = stream_lds ? 4 * 4 * 9216 : 3 * 8 * 64 * 16 + 16 * 132 * 4;
   void* args[] = {&X, &W, &Y, &P, &tickets, (void*)&M, &N, &K, (void*)&kw, &stream_lds, &e};
   if (lds > d.max_lds) return fail(CATENA_ERR_UNSUPPORTED, "decode GEMM needs %zu B of LDS", lds);
@@ -212,12 +190,12 @@ int catena_mi355x_gemm_bf16(const uint16_t* a, const uint16_t* b, void* c, uint6
       aligned16(c))
     return gemm_bf16_decode(a, b, c, n, m, k,
                             out_f32 ? DecodeEpilogue::StoreF32 : DecodeEpilogue::StoreBf16,
-                            DecodeEpiArgs{});
+                            DecodeEpiArgs{}, nullptr, 0);
 
   const bool ptr_ok = aligned16(a) && aligned16(b) && aligned16(c);
   const bool tile_ok = n % 256 == 0 && m % 256 == 0 && k % 64 == 0 && k > 0 && ptr_ok;
   // the 32-k stage kernels need K % 128 == 0 (whole groups of 4 stages);
-  // variants 9 and 10 address A's 256-row tile and B's 32-row slab with
+  // they address A's 256-row tile and B's 32-row slab with
   // 32-bit buffer offsets
   const bool k32_ok = k % 128 == 0 && k > 0 && k <= (1ull << 22) && m <= (1ull << 24);
   const bool n128_ok = n % 256 == 0 && m % 128 == 0 && k32_ok && ptr_ok;
@@ -225,37 +203,35 @@ int catena_mi355x_gemm_bf16(const uint16_t* a, const uint16_t* b, void* c, uint6
   if (ceil_div(n, 256) * ceil_div(m, 128) > 0x7FFFFFFFu)
     return fail(CATENA_ERR_UNSUPPORTED, "matrix too large");
   void* args[] = {&a, &b, &c, &n, &m, &k};
-  // Aligned shapes: direct-to-LDS kernels (8 waves).  The older
-  // register-staged tile kernel stays selectable with CATENA_GEMM_TILE=regs
-  // for comparison; it computes in the same order per output tile.
-  const char* sel = getenv("CATENA_GEMM_TILE");
-  const bool use_regs = sel && strcmp(sel, "regs") == 0;
-  if ((tile_ok || n128_ok) && !use_regs) {
-    int variant = kGemmDefaultVariant;
-    const char* v = getenv("CATENA_GEMM_VARIANT");
-    const bool forced = v && *v;
-    if (forced) {
-      const long x = strtol(v, nullptr, 10);
-      if (x >= 0 && x < kGemmVariantCount) variant = (int)x;
+  // Aligned shapes: direct-to-LDS kernels (8 waves), all with the same
+  // per-accumulator k32 order, so the choice between them never changes the
+  // bits: the four-stage 32-k kernel on 256 x 256 tiles, or on 256 x 128
+  // tiles when N % 256 == 128 or when that takes fewer rounds of the chip;
+  // the two-stage 64-k kernel when K % 128 != 0.
+  if (tile_ok || n128_ok) {
+    KernelId id;
+    size_t lds;
+    uint64_t grid;
+    if (k32_ok && (!tile_ok || prefer_n128(n, m, d.cu_count))) {
+      id = out_f32 ? KernelId::GemmBf16K32N128F32 : KernelId::GemmBf16K32N128Bf16;
+      lds = 4ull * (256 + 128) * 32 * sizeof(uint16_t);  // 98304 B
+      grid = (n / 256) * (m / 128);
+    } else if (k32_ok) {
+      id = out_f32 ? KernelId::GemmBf16K32F32 : KernelId::GemmBf16K32Bf16;
+      lds = 4ull * (256 + 256) * 32 * sizeof(uint16_t);  // 131072 B
+      grid = tiles;
+    } else {
+      id = out_f32 ? KernelId::GemmBf16LdsF32 : KernelId::GemmBf16LdsBf16;
+      lds = 2ull * (256 * 64 + 64 * 256) * sizeof(uint16_t);  // 131072 B
+      grid = tiles;
     }
-    if (!tile_ok || (!forced && n128_ok && prefer_n128(n, m, d.cu_count))) variant = kGemmN128Variant;
-    if (variant == kGemmN128Variant && !n128_ok) variant = kGemmDefaultVariant;
-    if (k < kGemmVariants[variant].min_k || (kGemmVariants[variant].min_k == 128 && !k32_ok))
-      variant = kGemmFallbackVariant;
-    const GemmVariant& gv = kGemmVariants[variant];
-    const bool narrow = variant == kGemmN128Variant;
-    // two-stage kernels: 2 x (A 256x64 + B 64x256); four-stage: 4 x (A 256x32 + B 32xBN)
-    const size_t lds = narrow ? 4ull * (256 + 128) * 32 * sizeof(uint16_t)   // 98304 B
-                              : 2ull * (256 * 64 + 64 * 256) * sizeof(uint16_t);  // 131072 B
     if (lds > d.max_lds) return fail(CATENA_ERR_UNSUPPORTED, "device LDS %zu < %zu", d.max_lds, lds);
-    const uint64_t grid = narrow ? (n / 256) * (m / 128) : tiles;
-    return launch(out_f32 ? gv.f32 : gv.bf16, dim3((unsigned)grid), dim3(512), lds, args);
+    return launch(id, dim3((unsigned)grid), dim3(512), lds, args);
   }
   const size_t lds = 2ull * 2 * 256 * 72 * sizeof(uint16_t);  // 147456 B
   if (lds > d.max_lds) return fail(CATENA_ERR_UNSUPPORTED, "device LDS %zu < %zu", d.max_lds, lds);
-  KernelId id = tile_ok ? (out_f32 ? KernelId::GemmBf16TileF32 : KernelId::GemmBf16TileBf16)
-                        : (out_f32 ? KernelId::GemmBf16EdgeF32 : KernelId::GemmBf16EdgeBf16);
-  return launch(id, dim3((unsigned)tiles), dim3(256), lds, args);
+  return launch(out_f32 ? KernelId::GemmBf16EdgeF32 : KernelId::GemmBf16EdgeBf16,
+                dim3((unsigned)tiles), dim3(256), lds, args);
 }
 
 int catena_mi355x_gemm_bf16_silu(const uint16_t* a, const uint16_t* b, uint16_t* act, uint64_t n,
@@ -302,13 +278,7 @@ int catena_mi355x_attn_decode_bf16(const uint16_t* q, const uint16_t* k, const u
     return fail(CATENA_ERR_UNSUPPORTED, "max_len %u needs %zu B of LDS (device has %zu)", max_len,
                 lds, d.max_lds);
   void* args[] = {&q, &k, &v, &lens, &o, &heads, &max_len, &scale};
-  // K-pass cache policy: plain loads by default (each 128-byte line of K is
-  // read as two halves by consecutive steps and must stay in L2 between
-  // them); CATENA_ATTN_K=nt selects the non-temporal form for comparison.
-  const char* kp = getenv("CATENA_ATTN_K");
-  const bool k_cached = !(kp && strcmp(kp, "nt") == 0);
-  return launch(k_cached ? KernelId::AttnDecodeD128KC : KernelId::AttnDecodeD128, dim3((unsigned)bh),
-                dim3(256), lds, args);
+  return launch(KernelId::AttnDecodeD128, dim3((unsigned)bh), dim3(256), lds, args);
 }
 
 int catena_mi355x_softmax_f32(const float* x, float* y, uint64_t rows, uint64_t n) {
@@ -354,6 +324,18 @@ int catena_mi355x_fill_uniform_f32(float* out, uint64_t n, uint64_t seed, uint64
   if (g > 0x7FFFFFFFull) return fail(CATENA_ERR_UNSUPPORTED, "too many elements");
   void* args[] = {&out, &n, &seed, &stream};
   return launch(KernelId::FillUniformF32, dim3((unsigned)g), dim3(256), 0, args);
+}
+
+int catena_mi355x_gemm_bf16_decode_plan(uint64_t n, uint64_t m, uint64_t k, uint32_t* k_groups,
+                                        uint64_t* partials_bytes) {
+  if (!k_groups || !partials_bytes) return fail(CATENA_ERR_INVALID_ARGUMENT, "null output");
+  *k_groups = 0;
+  *partials_bytes = 0;
+  if (n == 0 || n > 16 || m == 0 || k == 0 || m % 8 != 0 || k % 8 != 0)
+    return fail(CATENA_ERR_INVALID_ARGUMENT,
+                "not a decode-GEMM shape (1 <= n <= 16, m %% 8 == 0, k %% 8 == 0, k > 0)");
+  *partials_bytes = decode_partials_bytes(n, m, k, k_groups);
+  return CATENA_OK;
 }
 
 int catena_mi355x_copy_bytes(void* dst, const void* src, uint64_t n) {

@@ -69,12 +69,16 @@ int catena_mi355x_copy_f32(float* dst, const float* src, uint64_t n) {
   return launch(KernelId::CopyF32, dim3(stride_grid(n)), dim3(256), 0, args);
 }
 
+// Longest f32 sum row: the one-wave serial fold walks a row in 32-bit
+// 2048-value chunks (chunk base and lane offsets must not wrap).
+constexpr uint64_t kSumMaxN = 0xFFFFF800ull;
+
 static int sum_launch(const float* x, float* out, uint64_t rows, uint64_t n, uint32_t mean) {
-  int st = ensure_init();
-  if (st) return st;
-  if (rows == 0) return CATENA_OK;
+  if (rows == 0) return ensure_init();
   if (!out || (n > 0 && !x)) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
-  st = rows_ok(rows, n, 0xFFFFFFFFull, "sum-f32");
+  int st = rows_ok(rows, n, kSumMaxN, "sum-f32");
+  if (st) return st;
+  st = ensure_init();
   if (st) return st;
   void* args[] = {&x, &out, &n, &mean};
   return launch(KernelId::SumRowsF32, dim3((unsigned)rows), dim3(64), 0, args);

@@ -76,10 +76,10 @@ CATENA_DEV FirstMax wave_first_max(FirstMax a) {
 }
 }  // namespace
 
-// K_NT: K-pass loads carry the non-temporal hint.  Each 128-byte line of K
-// is read as two 64-byte halves by consecutive steps, so the hint can cost a
-// second fetch of the line; both forms are kept and the host picks one.
-template <bool K_NT, bool OUT_BF16>
+// K-pass loads are plain (cached): each 128-byte line of K is read as two
+// 64-byte halves by consecutive steps, so the line must stay in L2 between
+// them (a non-temporal hint measured slower).
+template <bool OUT_BF16>
 CATENA_DEV void attn_body(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                           const uint16_t* __restrict__ v, const uint32_t* __restrict__ lens,
                           void* __restrict__ o, uint32_t H, uint32_t L, uint32_t Tq,
@@ -124,7 +124,7 @@ CATENA_DEV void attn_body(const uint16_t* __restrict__ q, const uint16_t* __rest
         const u32x4_t* src =
             reinterpret_cast<const u32x4_t*>(kb + (uint64_t)t * D + seg * 32 + lchunk * 8);
         if (t < len)
-          r[i] = K_NT ? __builtin_nontemporal_load(src) : *src;
+          r[i] = *src;
         else
           r[i] = u32x4_t{0u, 0u, 0u, 0u};
       }
@@ -292,14 +292,7 @@ extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
 catena_attn_decode_bf16_d128(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                              const uint16_t* __restrict__ v, const uint32_t* __restrict__ lens,
                              float* __restrict__ o, uint32_t H, uint32_t L, float scale) {
-  attn_body<true, false>(q, k, v, lens, o, H, L, 1u, scale);
-}
-
-extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void
-catena_attn_decode_bf16_d128_kc(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-                                const uint16_t* __restrict__ v, const uint32_t* __restrict__ lens,
-                                float* __restrict__ o, uint32_t H, uint32_t L, float scale) {
-  attn_body<false, false>(q, k, v, lens, o, H, L, 1u, scale);
+  attn_body<false>(q, k, v, lens, o, H, L, 1u, scale);
 }
 
 // Tq causal queries per sequence (prefill and multi-token steps).
@@ -308,7 +301,7 @@ catena_attn_causal_bf16_d128_f32out(const uint16_t* __restrict__ q, const uint16
                                     const uint16_t* __restrict__ v,
                                     const uint32_t* __restrict__ lens, float* __restrict__ o,
                                     uint32_t H, uint32_t L, uint32_t Tq, float scale) {
-  attn_body<false, false>(q, k, v, lens, o, H, L, Tq, scale);
+  attn_body<false>(q, k, v, lens, o, H, L, Tq, scale);
 }
 
 extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void
@@ -316,5 +309,5 @@ catena_attn_causal_bf16_d128_bf16out(const uint16_t* __restrict__ q, const uint1
                                      const uint16_t* __restrict__ v,
                                      const uint32_t* __restrict__ lens, uint16_t* __restrict__ o,
                                      uint32_t H, uint32_t L, uint32_t Tq, float scale) {
-  attn_body<false, true>(q, k, v, lens, o, H, L, Tq, scale);
+  attn_body<true>(q, k, v, lens, o, H, L, Tq, scale);
 }

@@ -345,23 +345,28 @@ CATENA_DEV uint32_t load_coherent(const uint32_t* p) {
 // of one output tile).  Each workgroup calls it once, with all its threads,
 // after writing its partials with store_coherent; it returns true in
 // exactly one of them, the last to arrive, which then reads every partial of
-// the group with load_coherent.  Each thread waits for its own stores to
-// complete before the barrier, so all of the workgroup's partials are in
-// place before thread 0 takes the ticket.  The last workgroup returns the
-// counter to zero, so counters need clearing only once, when allocated.
-// Which workgroup reduces depends on timing; what it computes does not.
+// the group with load_coherent.  Ordering: each thread waits for its own
+// stores to complete before the barrier, thread 0 takes the ticket with an
+// agent-scope release (so the workgroup's partials are visible before the
+// ticket moves), and the last workgroup's threads take an agent-scope acquire
+// before they read, so no load of a partial is served from a stale cache
+// line.  The last workgroup returns the counter to zero, so counters need
+// clearing only once, when allocated.  Which workgroup reduces depends on
+// timing; what it computes does not.
 CATENA_DEV bool last_arrival(uint32_t* counter, uint32_t group_size, uint32_t* lds_flag) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
     const uint32_t t =
-        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
     const uint32_t last = t == group_size - 1 ? 1u : 0u;
     if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *lds_flag = last;
   }
   __syncthreads();
-  return *lds_flag != 0u;
+  const bool last = *lds_flag != 0u;
+  if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  return last;
 }
 
 // Exact parallel form of the f32.max-env fold (catena-lang/stdlib/

@@ -1,4 +1,8 @@
-// bf16 GEMM on gfx950 MFMA with a fixed, data-independent reduction order.
+// bf16 GEMM on gfx950 MFMA with a fixed, data-independent reduction order:
+// the general-shape (edge) kernel, for shapes the aligned tile kernels do not
+// take (M or N not a multiple of 256, K not a multiple of 64, unaligned
+// pointers).  Every load and store is bounds-checked; out-of-range A and B
+// elements read as +0.
 //
 // Semantics: the reference's f32.matmul.row-major.materialize contraction
 // (catena-lang/stdlib/matrix.hex:236-327; NN, both operands row-major:
@@ -48,10 +52,8 @@ CATENA_DEV void tile_of(uint32_t bid, uint32_t tiles_m, uint32_t tiles_n, uint32
   tn = r / gsize;
 }
 
-template <bool EDGE>
 CATENA_DEV u32x4_t load_a_chunk(const uint16_t* __restrict__ A, uint64_t M, uint64_t K,
                                 uint64_t row, uint64_t col) {
-  if (!EDGE) return *reinterpret_cast<const u32x4_t*>(A + row * K + col);
   uint32_t w[4];
 #pragma unroll
   for (int h = 0; h < 4; ++h) {
@@ -63,10 +65,8 @@ CATENA_DEV u32x4_t load_a_chunk(const uint16_t* __restrict__ A, uint64_t M, uint
   return u32x4_t{w[0], w[1], w[2], w[3]};
 }
 
-template <bool EDGE>
 CATENA_DEV u32x4_t load_b_chunk(const uint16_t* __restrict__ B, uint64_t K, uint64_t N,
                                 uint64_t row, uint64_t col) {
-  if (!EDGE) return *reinterpret_cast<const u32x4_t*>(B + row * N + col);
   uint32_t w[4];
 #pragma unroll
   for (int h = 0; h < 4; ++h) {
@@ -93,7 +93,7 @@ CATENA_DEV void transpose8x8(const u32x4_t in[8], u32x4_t out[8]) {
   }
 }
 
-template <bool EDGE, bool OUT_BF16>
+template <bool OUT_BF16>
 CATENA_DEV void gemm_bf16_body(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                                void* __restrict__ C, uint64_t M, uint64_t N, uint64_t K) {
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
@@ -120,10 +120,10 @@ CATENA_DEV void gemm_bf16_body(const uint16_t* __restrict__ A, const uint16_t* _
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       int idx = tid + 256 * e;
-      ra[e] = load_a_chunk<EDGE>(A, M, K, m0 + (idx >> 3), k0 + (idx & 7) * 8);
+      ra[e] = load_a_chunk(A, M, K, m0 + (idx >> 3), k0 + (idx & 7) * 8);
     }
 #pragma unroll
-    for (int r = 0; r < 8; ++r) rb[r] = load_b_chunk<EDGE>(B, K, N, k0 + kb * 8 + r, n0 + nb * 8);
+    for (int r = 0; r < 8; ++r) rb[r] = load_b_chunk(B, K, N, k0 + kb * 8 + r, n0 + nb * 8);
   };
   auto lstore = [&](int buf) {
     uint16_t* as = As + buf * TILE_ELEMS;
@@ -187,7 +187,7 @@ CATENA_DEV void gemm_bf16_body(const uint16_t* __restrict__ A, const uint16_t* _
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const uint64_t gr = m0 + wm * 128 + i * 16 + crow + q;
-        if (EDGE && (gr >= M || gc >= N)) continue;
+        if (gr >= M || gc >= N) continue;
         if (OUT_BF16)
           static_cast<uint16_t*>(C)[gr * N + gc] = (uint16_t)f32_to_bf16_bits(acc[i][j][q]);
         else
@@ -198,14 +198,12 @@ CATENA_DEV void gemm_bf16_body(const uint16_t* __restrict__ A, const uint16_t* _
 }
 }  // namespace
 
-#define CATENA_GEMM_BF16_KERNEL(NAME, EDGE, OUTB)                                      \
+#define CATENA_GEMM_BF16_KERNEL(NAME, OUTB)                                            \
   extern "C" __global__ __launch_bounds__(256) void NAME(                            \
       const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C, \
       uint64_t M, uint64_t N, uint64_t K) {                                          \
-    gemm_bf16_body<EDGE, OUTB>(A, B, C, M, N, K);                                    \
+    gemm_bf16_body<OUTB>(A, B, C, M, N, K);                                          \
   }
 
-CATENA_GEMM_BF16_KERNEL(catena_gemm_bf16_tile_bf16out, false, true)
-CATENA_GEMM_BF16_KERNEL(catena_gemm_bf16_tile_f32out, false, false)
-CATENA_GEMM_BF16_KERNEL(catena_gemm_bf16_edge_bf16out, true, true)
-CATENA_GEMM_BF16_KERNEL(catena_gemm_bf16_edge_f32out, true, false)
+CATENA_GEMM_BF16_KERNEL(catena_gemm_bf16_edge_bf16out, true)
+CATENA_GEMM_BF16_KERNEL(catena_gemm_bf16_edge_f32out, false)

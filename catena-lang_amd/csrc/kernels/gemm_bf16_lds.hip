@@ -33,7 +33,11 @@
 // the second wave on each SIMD can issue while the first waits on LDS.
 // Pipeline: two LDS stages (2 x 64 KiB); slab t+1's loads are in flight while
 // slab t is multiplied; a stage is refilled only after a barrier that follows
-// the last read of it.
+// the last read of it.  One barrier per slab; the fragments of the next k32
+// step are read from LDS during the current step's MFMAs, one read per MFMA
+// over the first 16 of its 32 MFMAs.  This kernel serves aligned tiles with
+// K % 128 != 0 (the four-stage k32 kernels need whole groups of four 32-k
+// slabs).
 #include "common.h"
 
 namespace {
@@ -72,7 +76,7 @@ CATENA_DEV void tile_of(uint32_t bid, uint32_t tiles_m, uint32_t tiles_n, uint32
 #define CATENA_WAIT_VMCNT(n) \
   __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | 0x0070 | 0x0F00)
 
-template <bool OUT_BF16, bool PIPE, bool PRIO, bool ILV, bool FRONT>
+template <bool OUT_BF16>
 CATENA_DEV void gemm_lds_body(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                               void* __restrict__ C, uint64_t M, uint64_t N, uint64_t K) {
   extern __shared__ __attribute__((aligned(1024))) uint16_t smem[];
@@ -168,27 +172,24 @@ CATENA_DEV void gemm_lds_body(const uint16_t* __restrict__ A, const uint16_t* __
     }
   };
   auto mma = [&](const Frags& f) {
-    if (PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.b[j], f.a[i], acc[i][j], 0, 0, 0);
-    if (PRIO) __builtin_amdgcn_s_setprio(0);
   };
 
   // LDS reads of `next` interleaved with the MFMAs of `cur`, pinned with
   // scheduling barriers so that few reads are outstanding when an MFMA
   // issues (the LDS counter tracks only 15 operations, so a block of 16
-  // reads ahead of the MFMAs forces a full wait).  FRONT: one read per MFMA
-  // over the first 16 MFMAs, then 16 MFMAs with no reads (the reads have
-  // landed by the next barrier); otherwise one read per two MFMAs.
+  // reads ahead of the MFMAs forces a full wait): one read per MFMA over the
+  // first 16 MFMAs, then 16 MFMAs with no reads (the reads have landed by
+  // the next barrier).
   auto load_mma = [&](int stage, int kk, Frags& next, const Frags& cur) {
     const char* as = reinterpret_cast<const char*>(As + stage * A_STAGE);
     const char* bs = reinterpret_cast<const char*>(Bs + stage * B_STAGE);
     const uint32_t a_off = kk == 0 ? a_lds : (a_lds ^ (4u * 16u));
     i16x4_t blo[4], bhi[4];
-    if (PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int g = 0; g < 16; ++g) {
       if (g < 8) {
@@ -202,115 +203,51 @@ CATENA_DEV void gemm_lds_body(const uint16_t* __restrict__ A, const uint16_t* __
         else
           bhi[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 4 * BN * 2));
       }
-      if (FRONT) {
-        const int j = g >> 3, i = g & 7;
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.b[j], cur.a[i], acc[i][j], 0, 0, 0);
-      } else {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int m = 2 * g + t, j = m >> 3, i = m & 7;
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.b[j], cur.a[i], acc[i][j], 0, 0, 0);
-        }
-      }
+      const int j = g >> 3, i = g & 7;
+      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.b[j], cur.a[i], acc[i][j], 0, 0, 0);
     }
-    if (FRONT) {
 #pragma unroll
-      for (int m = 16; m < 32; ++m) {
-        const int j = m >> 3, i = m & 7;
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.b[j], cur.a[i], acc[i][j], 0, 0, 0);
-      }
-#pragma unroll
-      for (int g = 0; g < 16; ++g) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);   // sixteen MFMAs
-    } else {
-#pragma unroll
-      for (int g = 0; g < 16; ++g) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // two MFMAs
-      }
+    for (int m = 16; m < 32; ++m) {
+      const int j = m >> 3, i = m & 7;
+      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.b[j], cur.a[i], acc[i][j], 0, 0, 0);
     }
-    if (PRIO) __builtin_amdgcn_s_setprio(0);
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);   // sixteen MFMAs
 #pragma unroll
     for (int j = 0; j < 4; ++j) next.b[j] = cat_bf16(blo[j], bhi[j]);
   };
 
-  if (!PIPE) {
-    // two barriers per slab: wait + barrier before reading, barrier before refill
-    for (uint64_t it = 0; it < nk; ++it) {
-      const int stage = (int)(it & 1);
-      asm volatile("" ::: "memory");
-      if (it + 1 < nk) {
-        CATENA_WAIT_VMCNT(8);
-      } else {
-        CATENA_WAIT_VMCNT(0);
-      }
-      __builtin_amdgcn_s_barrier();
-      asm volatile("" ::: "memory");
-#pragma unroll
-      for (int kk = 0; kk < BK; kk += 32) {
-        Frags f;
-        load_frags(stage, kk, f);
-        mma(f);
-      }
-      if (it + 2 < nk) {
-        // every wave's reads of this stage have landed before it is refilled
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        issue(it + 2, stage);
-      }
-    }
+  // one barrier per slab; the fragments of the next k32 step are read from
+  // LDS while the current step's MFMAs run:
+  //   read F1 (2nd half of slab it) | MFMA F0 | wait: F1 landed, my slab it+1
+  //   loads landed | barrier | refill this stage with slab it+2 | read F0 (1st
+  //   half of slab it+1) | MFMA F1
+  if (nk > 1) {
+    CATENA_WAIT_VMCNT(8);
   } else {
-    // one barrier per slab; the fragments of the next k32 step are read from
-    // LDS while the current step's MFMAs run:
-    //   read F1 (2nd half of slab it) | MFMA F0 | wait: F1 landed, my slab it+1
-    //   loads landed | barrier | refill this stage with slab it+2 | read F0 (1st
-    //   half of slab it+1) | MFMA F1
-    if (nk > 1) {
-      CATENA_WAIT_VMCNT(8);
-    } else {
-      CATENA_WAIT_VMCNT(0);
-    }
+    CATENA_WAIT_VMCNT(0);
+  }
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  Frags f0, f1;
+  load_frags(0, 0, f0);
+  for (uint64_t it = 0; it + 1 < nk; ++it) {
+    const int stage = (int)(it & 1);
+    load_mma(stage, 32, f1, f0);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): f1 has landed
+    CATENA_WAIT_VMCNT(0);                // this wave's slab it+1 has landed
+    asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    Frags f0, f1;
-    load_frags(0, 0, f0);
-    if (!ILV) {
-      for (uint64_t it = 0; it < nk; ++it) {
-        const int stage = (int)(it & 1);
-        load_frags(stage, 32, f1);
-        mma(f0);
-        if (it + 1 < nk) {
-          __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): f1 has landed
-          CATENA_WAIT_VMCNT(0);                // this wave's slab it+1 has landed
-          asm volatile("" ::: "memory");
-          __builtin_amdgcn_s_barrier();
-          asm volatile("" ::: "memory");
-          if (it + 2 < nk) issue(it + 2, stage);
-          load_frags(stage ^ 1, 0, f0);
-        }
-        mma(f1);
-      }
-    } else {
-      for (uint64_t it = 0; it + 1 < nk; ++it) {
-        const int stage = (int)(it & 1);
-        load_mma(stage, 32, f1, f0);
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): f1 has landed
-        CATENA_WAIT_VMCNT(0);                // this wave's slab it+1 has landed
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        if (it + 2 < nk) issue(it + 2, stage);
-        load_mma(stage ^ 1, 0, f0, f1);
-      }
-      load_mma((int)((nk - 1) & 1), 32, f1, f0);
-      mma(f1);
-    }
+    if (it + 2 < nk) issue(it + 2, stage);
+    load_mma(stage ^ 1, 0, f0, f1);
   }
+  load_mma((int)((nk - 1) & 1), 32, f1, f0);
+  mma(f1);
 
   // acc[i][j] lane (G, s) holds C[row = 16 i + s][cols 16 j + 4G .. +3] of
   // the wave's 128 x 64 block.
@@ -334,29 +271,12 @@ CATENA_DEV void gemm_lds_body(const uint16_t* __restrict__ A, const uint16_t* __
 }
 }  // namespace
 
-#define CATENA_GEMM_LDS_KERNEL(NAME, OUTB, PIPE, PRIO, ILV, FRONT)                        \
+#define CATENA_GEMM_LDS_KERNEL(NAME, OUTB)                                                \
   extern "C" __global__ __launch_bounds__(512) void NAME(                                 \
       const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C, \
       uint64_t M, uint64_t N, uint64_t K) {                                               \
-    gemm_lds_body<OUTB, PIPE, PRIO, ILV, FRONT>(A, B, C, M, N, K);                        \
+    gemm_lds_body<OUTB>(A, B, C, M, N, K);                                                \
   }
 
-// Scheduling variants (same arithmetic and order; selected by the host):
-//   v0 two barriers per slab; v1 = v0 + MFMA priority; v2 one barrier per
-//   slab with fragment double-buffering; v3 = v2 + MFMA priority; v4 = v2
-//   with LDS reads interleaved 1:2 with MFMAs; v5 = v4 + MFMA priority;
-//   v7 = v4 with the reads front-loaded 1:1 into the first 16 MFMAs.
-CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v0_bf16out, true, false, false, false, false)
-CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v1_bf16out, true, false, true, false, false)
-CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v2_bf16out, true, true, false, false, false)
-CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v3_bf16out, true, true, true, false, false)
-CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v4_bf16out, true, true, false, true, false)
-CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v5_bf16out, true, true, true, true, false)
-CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v7_bf16out, true, true, false, true, true)
-CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v0_f32out, false, false, false, false, false)
-CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v1_f32out, false, false, true, false, false)
-CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v2_f32out, false, true, false, false, false)
-CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v3_f32out, false, true, true, false, false)
-CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v4_f32out, false, true, false, true, false)
-CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v5_f32out, false, true, true, true, false)
-CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_v7_f32out, false, true, false, true, true)
+CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_bf16out, true)
+CATENA_GEMM_LDS_KERNEL(catena_gemm_bf16_lds_f32out, false)

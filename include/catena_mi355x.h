@@ -64,6 +64,15 @@ typedef enum catena_status {
  * Replaces GpuRuntime::load (catena-lang/src/runtime/mem.rs:134-150) and the
  * per-Runtime hipcc + dlopen of catena-lang/src/runtime/artifact.rs:44-103. */
 int catena_mi355x_init(int device);
+/* Orderly teardown before the process exits: waits for the library
+ * stream, returns the library's own device memory (split-K workspace,
+ * completion counters, cached pool blocks), unloads the code objects and
+ * destroys the stream.  Buffers the caller still holds stay allocated and
+ * may still be freed with catena_mem_free.  A later call re-initialises on
+ * demand.  The reference instead keeps its generated library resident for
+ * the process lifetime (RTLD_NODELETE, catena-lang/src/runtime/runtime.rs:
+ * 249-263); here nothing is left for the runtime's own exit to tear down. */
+int catena_mi355x_shutdown(void);
 /* Message of the last failing call on this thread ("" if none). */
 const char *catena_mi355x_last_error(void);
 /* The hipStream_t every launch goes to (for events / interop). */
@@ -108,6 +117,15 @@ int catena_mi355x_gemm_f32_exact(const float *a, const float *b, float *c, uint6
  * n <= 16 (decode shape) uses the weight-streaming kernel (both outputs). */
 int catena_mi355x_gemm_bf16(const uint16_t *a, const uint16_t *b, void *c, uint64_t n,
                             uint64_t m, uint64_t k, int out_f32);
+
+/* The k split of the decode-shape GEMM (1 <= n <= 16, m % 8 == 0, k % 8 ==
+ * 0): the number of k groups whose f32 partials are added in ascending
+ * order, and the bytes of those partials (0 when k is not split).  A function
+ * of (n, m, k) alone -- never of the device -- so the decode GEMM's bits
+ * depend only on the shape and the inputs.  Needs no device.  No reference
+ * counterpart (the reference's fold is one sequential chain per cell). */
+int catena_mi355x_gemm_bf16_decode_plan(uint64_t n, uint64_t m, uint64_t k, uint32_t *k_groups,
+                                        uint64_t *partials_bytes);
 
 /* Decode attention, one query per (batch, head): q[B][H][D], k/v[B][H][L][D]
  * bf16, lens[B] (device u32, each <= L), o[B][H][D] f32.  Bitwise the
@@ -223,7 +241,8 @@ int catena_mi355x_arange_f32(float *out, uint64_t n);
 int catena_mi355x_copy_f32(float *dst, const float *src, uint64_t n);
 /* sum-f32 / mean-f32 / max-f32 per row (catena-lang/stdlib/sum.hex:29-101):
  * the reference's sequential folds (sum from +0, max-env from -inf),
- * bitwise.  n < 2^32 (max: n < 2^31). */
+ * bitwise.  sum / mean: n <= 0xFFFFF800 (longer rows return
+ * CATENA_ERR_UNSUPPORTED); max: n < 2^31. */
 int catena_mi355x_sum_f32(const float *x, float *out, uint64_t rows, uint64_t n);
 int catena_mi355x_mean_f32(const float *x, float *out, uint64_t rows, uint64_t n);
 int catena_mi355x_max_f32(const float *x, float *out, uint64_t rows, uint64_t n);
@@ -310,11 +329,14 @@ typedef struct catena_decoder_config {
   uint32_t vocab;
   uint32_t max_batch; /* <= 4096 */
   uint32_t max_len;   /* cache positions per sequence; the attention holds one
-                         f32 score per position in LDS: <= 36,720 on gfx950 */
+                         f32 score per position in LDS: <= 36,720 on gfx950
+                         ((163,840 - 16,960) / 4) */
   float rope_base;
 } catena_decoder_config_t;
 /* create() rejects (CATENA_ERR_UNSUPPORTED) n_heads or n_layers > 4096,
- * ffn_dim > 2^24, vocab > 2^26 and the limits above. */
+ * ffn_dim > 2^24, vocab > 2^26, d_model > 20,476 (the RMSNorm holds a row
+ * and its squares in LDS: 16 + 8 * d_model <= 163,840 B on gfx950) and the
+ * limits above. */
 
 typedef enum catena_decoder_tensor {
   CATENA_DEC_EMBED = 0, /* [vocab][d] bf16 */

@@ -84,6 +84,14 @@ def lib():
         L.or_rope_inv_freq.restype = None
         L.or_rope_f32.argtypes = [_f32p, ctypes.c_uint32, _f32p, ctypes.c_uint32]
         L.or_rope_f32.restype = None
+        L.or_silu_mul_rows.argtypes = [_f32p, _u16p, ctypes.c_uint64, ctypes.c_uint32,
+                                       ctypes.c_uint32]
+        L.or_silu_mul_rows.restype = None
+        L.or_rope_qkv_rows.argtypes = [_f32p, _f32p, _u32p, _u16p, _u16p, _u16p, ctypes.c_uint64,
+                                       ctypes.c_uint32, ctypes.c_uint32]
+        L.or_rope_qkv_rows.restype = None
+        L.or_rmsnorm_rows.argtypes = [_f32p, _f32p, ctypes.c_uint64, ctypes.c_uint64]
+        L.or_rmsnorm_rows.restype = None
         _lib = L
     return _lib
 
@@ -208,10 +216,8 @@ def rmsnorm_f32(x: np.ndarray) -> np.ndarray:
     """nn.rmsnorm per row of a 1-D or 2-D array."""
     x = np.ascontiguousarray(x, np.float32)
     y = np.empty_like(x)
-    rows = x.reshape(-1, x.shape[-1])
-    out = y.reshape(-1, x.shape[-1])
-    for r in range(rows.shape[0]):
-        lib().or_rmsnorm_f32(_p(rows[r], _f32p), _p(out[r], _f32p), rows.shape[1])
+    n = x.shape[-1]
+    lib().or_rmsnorm_rows(_p(x, _f32p), _p(y, _f32p), x.size // n if n else 0, n)
     return y
 
 

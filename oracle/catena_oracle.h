@@ -95,6 +95,13 @@ void or_rmsnorm_f32(const float *x, float *y, uint64_t n);   /* nn.rmsnorm */
 uint64_t or_argmax_f32(const float *x, uint64_t n);           /* tensor.argmax-f32 */
 void or_rope_inv_freq(float *inv_freq, uint32_t d, double base);
 void or_rope_f32(float *x, uint32_t pos, const float *inv_freq, uint32_t d);
+/* whole-activation forms of the decoder stages (row by row, same bits) */
+void or_silu_mul_rows(const float *gu, uint16_t *out, uint64_t rows, uint32_t ffn,
+                      uint32_t group);
+void or_rope_qkv_rows(const float *qkv, const float *inv_freq, const uint32_t *pos,
+                      uint16_t *q, uint16_t *k, uint16_t *v, uint64_t rows, uint32_t heads,
+                      uint32_t d);
+void or_rmsnorm_rows(const float *x, float *y, uint64_t rows, uint64_t n);
 
 #ifdef __cplusplus
 }

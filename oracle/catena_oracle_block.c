@@ -174,3 +174,61 @@ void or_rope_f32(float *x, uint32_t pos, const float *inv_freq, uint32_t d) {
     x[i + h] = t3 + t4;
   }
 }
+
+/* Whole-activation forms of the two elementwise decoder stages, row by row
+ * through the functions above (checkers for full-size activations).
+ *
+ * SwiGLU gate: out[r][i] = bf16(nn.silu(gate) * up) with one f32 rounding of
+ * the product; group = 0: gate = gu[r][i], up = gu[r][ffn + i]; group = G:
+ * gate and up interleaved in blocks of G columns (gate i at G-block i/G,
+ * offset i%G; up G columns after it). */
+void or_silu_mul_rows(const float *gu, uint16_t *out, uint64_t rows, uint32_t ffn,
+                      uint32_t group) {
+  for (uint64_t r = 0; r < rows; ++r) {
+    const float *row = gu + r * 2ull * ffn;
+    for (uint32_t i = 0; i < ffn; ++i) {
+      uint64_t gi, ui;
+      if (group == 0) {
+        gi = i;
+        ui = (uint64_t)ffn + i;
+      } else {
+        const uint64_t blk = i / group, j = i % group;
+        gi = blk * 2ull * group + j;
+        ui = gi + group;
+      }
+      const float s = or_silu(row[gi]);
+      const float p = s * row[ui];
+      out[r * ffn + i] = or_f32_to_bf16(p);
+    }
+  }
+}
+
+/* RoPE + split of a fused projection row qkv[r][3 * heads * d] (q heads |
+ * k heads | v heads) at position pos[r]: q and k heads rotated by
+ * or_rope_f32, v copied; all three rounded to bf16.  q[r][heads * d],
+ * k / v[r][heads][d]. */
+void or_rope_qkv_rows(const float *qkv, const float *inv_freq, const uint32_t *pos,
+                      uint16_t *q, uint16_t *k, uint16_t *v, uint64_t rows, uint32_t heads,
+                      uint32_t d) {
+  float buf[1024];
+  const uint64_t hd = (uint64_t)heads * d;
+  if (d > 1024) return;
+  for (uint64_t r = 0; r < rows; ++r) {
+    const float *row = qkv + r * 3 * hd;
+    for (uint32_t h = 0; h < heads; ++h) {
+      memcpy(buf, row + (uint64_t)h * d, d * sizeof(float));
+      or_rope_f32(buf, pos[r], inv_freq, d);
+      for (uint32_t i = 0; i < d; ++i) q[r * hd + (uint64_t)h * d + i] = or_f32_to_bf16(buf[i]);
+      memcpy(buf, row + hd + (uint64_t)h * d, d * sizeof(float));
+      or_rope_f32(buf, pos[r], inv_freq, d);
+      for (uint32_t i = 0; i < d; ++i) k[r * hd + (uint64_t)h * d + i] = or_f32_to_bf16(buf[i]);
+      for (uint32_t i = 0; i < d; ++i)
+        v[r * hd + (uint64_t)h * d + i] = or_f32_to_bf16(row[2 * hd + (uint64_t)h * d + i]);
+    }
+  }
+}
+
+/* nn.rmsnorm of each of `rows` contiguous rows of length n. */
+void or_rmsnorm_rows(const float *x, float *y, uint64_t rows, uint64_t n) {
+  for (uint64_t r = 0; r < rows; ++r) or_rmsnorm_f32(x + r * n, y + r * n, n);
+}

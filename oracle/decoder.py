@@ -26,8 +26,14 @@ from __future__ import annotations
 
 import numpy as np
 
+import ctypes
+
 from . import (argmax_f32, attn_decode, bf16_bits_to_f32, f32_to_bf16_bits_np, lib,
                matmul_bf16, rmsnorm_f32, rope_f32)
+
+
+def _ptr(arr, ctype):
+    return arr.ctypes.data_as(ctypes.POINTER(ctype))
 
 
 def residual_rmsnorm_bf16(x, r=None):
@@ -40,6 +46,17 @@ def residual_rmsnorm_bf16(x, r=None):
 def silu_mul_bf16(gu, ffn: int, group: int = 0):
     """group = 0: columns gate | up; group = G: interleaved in groups of G."""
     gu = np.ascontiguousarray(gu, np.float32)
+    rows = gu.shape[0]
+    assert gu.shape[1] == 2 * ffn and (group == 0 or ffn % group == 0)
+    out = np.empty((rows, ffn), np.uint16)
+    lib().or_silu_mul_rows(_ptr(gu, ctypes.c_float), _ptr(out, ctypes.c_uint16), rows, ffn, group)
+    return out
+
+
+def silu_mul_bf16_elementwise(gu, ffn: int, group: int = 0):
+    """The same stage element by element through or_silu (Python loop; small
+    inputs only): the composition the row form must equal."""
+    gu = np.ascontiguousarray(gu, np.float32)
     if group:
         blocks = gu.reshape(gu.shape[0], ffn // group, 2, group)
         g = np.ascontiguousarray(blocks[:, :, 0, :].reshape(gu.shape[0], ffn))
@@ -51,19 +68,44 @@ def silu_mul_bf16(gu, ffn: int, group: int = 0):
     return f32_to_bf16_bits_np((s * u).astype(np.float32))
 
 
+def _rope_positions(lens, batch: int, tq: int):
+    pos = np.empty(batch * tq, np.int64)
+    for r in range(batch * tq):
+        b, t = divmod(r, tq)
+        pos[r] = int(lens[b]) - tq + t
+    return pos
+
+
 def rope_qkv(qkv, inv_freq, lens, batch: int, tq: int, heads: int, head_dim: int):
     """-> (q bf16 [R][H*D], k bf16 [R][H][D], v bf16 [R][H][D], pos [R])."""
+    qkv = np.ascontiguousarray(qkv, np.float32)
+    R = batch * tq
+    HD = heads * head_dim
+    assert qkv.shape == (R, 3 * HD)
+    pos = _rope_positions(lens, batch, tq)
+    p32 = np.maximum(pos, 0).astype(np.uint32)
+    inv = np.ascontiguousarray(inv_freq, np.float32)
+    q = np.empty((R, HD), np.uint16)
+    k = np.empty((R, heads, head_dim), np.uint16)
+    v = np.empty((R, heads, head_dim), np.uint16)
+    lib().or_rope_qkv_rows(_ptr(qkv, ctypes.c_float), _ptr(inv, ctypes.c_float),
+                           _ptr(p32, ctypes.c_uint32), _ptr(q, ctypes.c_uint16),
+                           _ptr(k, ctypes.c_uint16), _ptr(v, ctypes.c_uint16), R, heads, head_dim)
+    return q, k, v, pos
+
+
+def rope_qkv_per_head(qkv, inv_freq, lens, batch: int, tq: int, heads: int, head_dim: int):
+    """The same stage head by head through or_rope_f32 (small inputs only):
+    the composition the row form must equal."""
     qkv = np.ascontiguousarray(qkv, np.float32)
     R = batch * tq
     HD = heads * head_dim
     q = np.empty((R, HD), np.uint16)
     k = np.empty((R, heads, head_dim), np.uint16)
     v = np.empty((R, heads, head_dim), np.uint16)
-    pos = np.empty(R, np.int64)
+    pos = _rope_positions(lens, batch, tq)
     for r in range(R):
-        b, t = divmod(r, tq)
-        p = int(lens[b]) - tq + t
-        pos[r] = p
+        p = int(pos[r])
         for h in range(heads):
             qs = qkv[r, h * head_dim:(h + 1) * head_dim]
             ks = qkv[r, HD + h * head_dim:HD + (h + 1) * head_dim]
@@ -73,20 +115,21 @@ def rope_qkv(qkv, inv_freq, lens, batch: int, tq: int, heads: int, head_dim: int
     return q, k, v, pos
 
 
-def attn_causal(q, kc, vc, lens, batch: int, tq: int, heads: int, head_dim: int, scale: float):
+def attn_causal(q, kc, vc, lens, batch: int, tq: int, heads: int, head_dim: int, scale: float,
+                threads=None):
     """q bf16 [B*Tq][H*D], caches [B][H][L][D] -> o f32 [B*Tq][H*D]."""
     q = np.asarray(q, np.uint16).reshape(batch, tq, heads, head_dim)
     lens = np.asarray(lens, np.int64)
     o = np.empty((batch, tq, heads, head_dim), np.float32)
     for t in range(tq):
         ln = np.maximum(lens - (tq - 1 - t), 0).astype(np.uint32)
-        o[:, t] = attn_decode(np.ascontiguousarray(q[:, t]), kc, vc, ln, scale)
+        o[:, t] = attn_decode(np.ascontiguousarray(q[:, t]), kc, vc, ln, scale, threads=threads)
     return o.reshape(batch * tq, heads * head_dim)
 
 
-def gemm(a16, b16):
+def gemm(a16, b16, threads=None):
     """Sequential-order bf16 GEMM: (f32, bf16 bits)."""
-    return matmul_bf16(a16, b16)
+    return matmul_bf16(a16, b16, threads=threads)
 
 
 class DecoderOracle:
@@ -96,8 +139,9 @@ class DecoderOracle:
     interleaved by 64 columns, w_down [L][F][d], embed [V][d], w_lm [d][V])."""
 
     def __init__(self, weights: dict, n_heads: int, head_dim: int, ffn: int, max_len: int,
-                 rope_base: float = 10000.0):
+                 rope_base: float = 10000.0, threads=None):
         self.w = weights
+        self.threads = threads  # None: the oracle's default (all visible cores, <= 16)
         self.H, self.D, self.F, self.L = n_heads, head_dim, ffn, max_len
         self.d = n_heads * head_dim
         self.layers = len(weights["w_qkv"])
@@ -118,21 +162,22 @@ class DecoderOracle:
                 _, xn = residual_rmsnorm_bf16(x)
             else:
                 x, xn = residual_rmsnorm_bf16(h, ffn_out)
-            qkv, _ = gemm(xn, self.w["w_qkv"][l])
+            qkv, _ = gemm(xn, self.w["w_qkv"][l], self.threads)
             q, k, v, pos = rope_qkv(qkv, self.inv, lens, batch, tq, H, D)
             for r in range(batch * tq):
                 b = r // tq
                 self.kc[l][b, :, pos[r]] = k[r]
                 self.vc[l][b, :, pos[r]] = v[r]
-            o = attn_causal(q, self.kc[l], self.vc[l], lens, batch, tq, H, D, self.scale)
-            ap, _ = gemm(f32_to_bf16_bits_np(o), self.w["w_o"][l])
+            o = attn_causal(q, self.kc[l], self.vc[l], lens, batch, tq, H, D, self.scale,
+                            self.threads)
+            ap, _ = gemm(f32_to_bf16_bits_np(o), self.w["w_o"][l], self.threads)
             h, hn = residual_rmsnorm_bf16(x, ap)
-            gu, _ = gemm(hn, self.w["w_gu"][l])
+            gu, _ = gemm(hn, self.w["w_gu"][l], self.threads)
             act = silu_mul_bf16(gu, F, 64)
-            ffn_out, _ = gemm(act, self.w["w_down"][l])
+            ffn_out, _ = gemm(act, self.w["w_down"][l], self.threads)
         last = np.arange(batch) * tq + (tq - 1)
         _, fxn = residual_rmsnorm_bf16(h[last], ffn_out[last])
-        logits, _ = gemm(fxn, self.w["w_lm"])
+        logits, _ = gemm(fxn, self.w["w_lm"], self.threads)
         nxt = np.array([argmax_f32(logits[b]) for b in range(batch)], np.uint32)
         self.len += tq
         return logits, nxt
@@ -145,3 +190,10 @@ class DecoderOracle:
 
     def step(self, tokens, batch: int):
         return self._forward(tokens, batch, 1)
+
+    def load_cache(self, kc, vc, length: int):
+        """Start from caches filled elsewhere (e.g. by a GPU prefill):
+        kc / vc per layer [batch][H][L][D] bf16, `length` positions valid."""
+        self.kc = [np.array(k, np.uint16, copy=True) for k in kc]
+        self.vc = [np.array(v, np.uint16, copy=True) for v in vc]
+        self.len = length

@@ -34,7 +34,7 @@ def test_library_exports_every_header_symbol():
 
 def test_code_objects_present_and_gfx950():
     objdump = "/opt/rocm/llvm/bin/llvm-readelf"
-    for name in ["gemm_f32_exact", "gemm_bf16", "gemm_bf16_lds", "gemm_bf16_deep", "gemm_bf16_k32", "gemm_bf16_decode",
+    for name in ["gemm_f32_exact", "gemm_bf16", "gemm_bf16_lds", "gemm_bf16_k32", "gemm_bf16_decode",
                  "attn_decode", "attn_prefill", "block", "tensor", "softmax", "fill"]:
         path = os.path.join(ca.LIB_DIR, name + ".co")
         assert os.path.exists(path), path

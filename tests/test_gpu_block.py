@@ -54,6 +54,21 @@ def test_rmsnorm_f32(rows, n):
     _bitwise(yb.read(np.float32, (rows, n)), oracle.rmsnorm_f32(x))
 
 
+def test_rmsnorm_row_limit():
+    """The row and its squares sit in LDS beside the kernel's static f32:
+    16 + 8 n <= 163,840 B, so 20,476 elements run and 20,480 are refused
+    with CATENA_ERR_UNSUPPORTED before any launch."""
+    x = _rows(1, 20480, 3)
+    xb, yb = ca.Buffer.from_array(x), ca.Buffer(x.nbytes)
+    say("rmsnorm n=20480 (refused)")
+    with pytest.raises(ca.CatenaError) as e:
+        ca.rmsnorm_f32(xb, yb, 1, 20480)
+    assert e.value.status == 2
+    say("rmsnorm n=20476")
+    ca.rmsnorm_f32(xb, yb, 1, 20476)
+    _bitwise(yb.read(np.float32, (1, 20480))[:, :20476], oracle.rmsnorm_f32(x[:, :20476]))
+
+
 @pytest.mark.parametrize("n", [64, 2048])
 def test_rmsnorm_specials(n):
     x = _rows(6, n, 5)
@@ -322,25 +337,34 @@ def test_argmax_chunked_nan_and_tie_patterns():
 
 
 @pytest.mark.parametrize("B,Tq,H,L,lens", [(2, 37, 3, 200, [200, 37]), (1, 512, 2, 640, [512]),
-                                           (3, 8, 2, 96, [96, 8, 30]), (2, 100, 1, 700, [700, 120])])
-def test_attention_prefill_kernel_equals_per_query_kernel(monkeypatch, B, Tq, H, L, lens):
-    """The 16-query-block kernel against the one-query-per-workgroup kernel
-    (same bits by construction), including cached prefixes (lens > Tq),
-    partial last blocks and sequences shorter than Tq."""
+                                           (3, 8, 2, 96, [96, 8, 30]), (2, 100, 1, 700, [700, 120]),
+                                           (1, 12, 2, 1000, [1000])])
+def test_attention_prefill_kernel_equals_per_query_kernel(B, Tq, H, L, lens):
+    """The causal attention (the 16-query-block kernel for Tq >= 8 while its
+    score buffer fits, L <= ~830; the one-query kernel beyond, as in the last
+    case) against the decode kernel run once per query on that query's
+    prefix (same bits by construction), including cached prefixes
+    (lens > Tq), partial last blocks and sequences shorter than Tq."""
     D = 128
     q, k, v = _attn_inputs(B, Tq, H, L, B * 7 + Tq)
     lb = ca.Buffer.from_array(np.array(lens, np.uint32))
     scale = 1.0 / math.sqrt(D)
-    a32, b32 = ca.Buffer(B * Tq * H * D * 4), ca.Buffer(B * Tq * H * D * 4)
-    a16, b16 = ca.Buffer(B * Tq * H * D * 2), ca.Buffer(B * Tq * H * D * 2)
+    a32 = ca.Buffer(B * Tq * H * D * 4)
+    a16 = ca.Buffer(B * Tq * H * D * 2)
     say(f"prefill attention B={B} Tq={Tq} H={H} L={L} lens={lens}")
     ca.attn_causal_bf16(q, k, v, lb, a32, B, Tq, H, L, D, scale, out_f32=True)
     ca.attn_causal_bf16(q, k, v, lb, a16, B, Tq, H, L, D, scale, out_f32=False)
-    monkeypatch.setenv("CATENA_ATTN_PREFILL", "0")
-    ca.attn_causal_bf16(q, k, v, lb, b32, B, Tq, H, L, D, scale, out_f32=True)
-    ca.attn_causal_bf16(q, k, v, lb, b16, B, Tq, H, L, D, scale, out_f32=False)
-    assert np.array_equal(a32.read(np.uint32), b32.read(np.uint32))
-    assert np.array_equal(a16.read(np.uint16), b16.read(np.uint16))
+    got = a32.read(np.float32, (B, Tq, H, D))
+    assert np.array_equal(a16.read(np.uint16, (B, Tq, H, D)),
+                          oracle.f32_to_bf16_bits_np(got))
+    q_host = q.read(np.uint16, (B, Tq, H, D))
+    ob = ca.Buffer(B * H * D * 4)
+    for t in range(Tq):
+        qt = ca.Buffer.from_array(np.ascontiguousarray(q_host[:, t]))
+        ln = ca.Buffer.from_array(np.maximum(np.array(lens, np.int64) - (Tq - 1 - t), 0)
+                                  .astype(np.uint32))
+        ca.attn_decode_bf16(qt, k, v, ln, ob, B, H, L, D, scale)
+        assert np.array_equal(got[:, t].view(np.uint32), ob.read(np.uint32, (B, H, D))), t
     if B * Tq * H <= 4096:
         want = od.attn_causal(q.read(np.uint16), k.read(np.uint16, (B, H, L, D)),
                               v.read(np.uint16, (B, H, L, D)), lens, B, Tq, H, D, scale)

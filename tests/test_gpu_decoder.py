@@ -293,3 +293,47 @@ def test_decoder_two_layers_against_sequential_oracle_and_run_to_run():
         if not np.all(clear) or step == 4:
             break
         ol, on = ora.step(toks[step], cfg.B)
+
+
+class C5:
+    """d 2048, 16 heads of 128, SwiGLU 5632, vocab 32000,
+    one block, batch 8, a 512-token prefill then 128 greedy steps (the cache
+    holds 640 positions after the last one)."""
+    H, F, V, B, T, layers = 16, 5632, 32000, 8, 512, 1
+    d = H * D
+    steps = 128
+    L = T + steps
+
+
+def test_decoder_c5_full_workload_stagewise():
+    """The C5 workload as bench.py runs it (same seeds): the 4096-row prefill
+    (the 256-row-tile GEMMs, the SwiGLU-fused W_gu GEMM, the 16-query-block
+    prefill attention over 512 positions) checked stage by stage; all 128
+    greedy steps run on the device, and the last one (cache length 640)
+    checked stage by stage, its tokens equal to the oracle's argmax of the
+    GPU logits."""
+    cfg = C5
+    say("C5 decoder: create + init weights")
+    dec = ca.Decoder(cfg.d, cfg.H, cfg.F, cfg.layers, cfg.V, cfg.B, cfg.L)
+    dec.init_weights(seed=51, std=0.02)
+    w = _weights(dec, cfg)
+    tokens = np.random.default_rng(51).integers(0, cfg.V, (cfg.B, cfg.T)).astype(np.uint32)
+    tb = ca.Buffer.from_array(tokens)
+    nxt = ca.Buffer(cfg.B * 4)
+    say("C5 decoder: prefill 8 x 512")
+    dec.prefill(tb, cfg.B, cfg.T, nxt)
+    say("C5 decoder: prefill stagewise check")
+    want = _check_forward(dec, cfg, w, tokens, cfg.T, cfg.T)
+    first = nxt.read(np.uint32)
+    assert np.array_equal(first, want)
+    out = ca.Buffer((cfg.steps - 1) * cfg.B * 4)
+    say("C5 decoder: 127 greedy steps")
+    dec.generate(cfg.steps - 1, out)
+    toks = out.read(np.uint32, (cfg.steps - 1, cfg.B))
+    assert toks.max() < cfg.V
+    last = ca.Buffer(cfg.B * 4)
+    say("C5 decoder: step 128 (cache length 640)")
+    dec.generate(1, last)
+    want = _check_forward(dec, cfg, w, toks[-1], 1, cfg.L)
+    assert np.array_equal(last.read(np.uint32), want)
+    dec.close()

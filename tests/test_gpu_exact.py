@@ -187,3 +187,32 @@ def test_pool_reuses_blocks():
         b = ca.Buffer(1 << 20)
         b.close()
     assert ca.pool_stats()["device_allocs"] - before <= 1
+
+
+def test_program_matmul_via_mem_c1_by_value():
+    """C1: the 256^3 f32 GEMM through the program ABI symbol itself,
+    program_matmul_2x2_via_mem, called the way the reference's libffi
+    executor calls a generated program (catena-lang/src/runtime/
+    executor.rs:88-106: each Mem argument by value as a 16-byte struct, the
+    u64 sizes by value, one pointer per output), on U[-1,1] inputs from seeds
+    1 and 2: bitwise equal to the oracle, and bitwise run to run."""
+    import ctypes
+    n = m = k = 256
+    a, b = ca.Buffer(n * k * 4), ca.Buffer(k * m * 4)
+    ca.fill_uniform_f32(a, n * k, 1, 0)
+    ca.fill_uniform_f32(b, k * m, 2, 0)
+    a_host, b_host = a.read(np.float32, (n, k)), b.read(np.float32, (k, m))
+    assert a_host.min() >= -1 and a_host.max() <= 1 and np.unique(a_host).size > 60000
+    want = oracle.matmul_f32(a_host, b_host).view(np.uint32)
+    L = ca.lib()
+    hashes = set()
+    for i in range(5):
+        out = ca.Mem()
+        say(f"program_matmul_2x2_via_mem 256^3 by value, call {i}")
+        L.program_matmul_2x2_via_mem(a.mem, b.mem, n, m, k, n * k, k * m, n * m, ctypes.byref(out))
+        assert out.len == n * m * 4 and out.data
+        got = ca.mem_to_array(out, np.uint32).reshape(n, m)
+        assert np.array_equal(got, want)
+        hashes.add(hash_bits(got))
+        ca.mem_free(out)
+    assert len(hashes) == 1

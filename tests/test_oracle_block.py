@@ -123,3 +123,37 @@ def test_silu_mul_group_layout():
     inter = np.concatenate([np.concatenate([g[:, i:i + G], u[:, i:i + G]], axis=1)
                             for i in range(0, F, G)], axis=1)
     assert np.array_equal(od.silu_mul_bf16(halves, F), od.silu_mul_bf16(inter, F, G))
+
+
+def test_row_forms_equal_the_elementwise_composition():
+    """The whole-activation oracle forms (or_silu_mul_rows, or_rope_qkv_rows,
+    or_rmsnorm_rows) equal the pinned per-element / per-head / per-row
+    functions they are built from, on both SwiGLU layouts, with specials in
+    the gate / up columns and with positions that clamp at 0: a wrong gate /
+    up index, head offset, position or row stride fails here."""
+    from oracle import decoder as od
+    rng = np.random.default_rng(9)
+    rows, F = 5, 192
+    gu = rng.standard_normal((rows, 2 * F)).astype(np.float32) * 4
+    gu[0, 3] = np.nan
+    gu[1, 70] = np.inf
+    gu[2, 200] = -np.inf
+    gu[3, :] = 0.0
+    gu[4, 100] = 95.0   # exp~ of -95: the garbage range of the reference's exp
+    for group in (0, 64, 32):
+        a = od.silu_mul_bf16(gu, F, group)
+        b = od.silu_mul_bf16_elementwise(gu, F, group)
+        assert a.shape == (rows, F)
+        an, bn = (a & 0x7FFF) > 0x7F80, (b & 0x7FFF) > 0x7F80
+        assert np.array_equal(an, bn) and np.array_equal(a[~an], b[~bn]), group
+    B, tq, H, Dh = 2, 3, 3, 128
+    inv = oracle.rope_inv_freq(Dh, 10000.0)
+    qkv = rng.standard_normal((B * tq, 3 * H * Dh)).astype(np.float32)
+    for lens in ([3, 700], [1, 2]):   # the second: positions below 0 clamp to 0
+        fast = od.rope_qkv(qkv, inv, lens, B, tq, H, Dh)
+        slow = od.rope_qkv_per_head(qkv, inv, lens, B, tq, H, Dh)
+        for x, y in zip(fast, slow):
+            assert np.array_equal(x, y)
+    x = rng.standard_normal((4, 300)).astype(np.float32)
+    want = np.stack([oracle.rmsnorm_f32(r) for r in x])
+    assert np.array_equal(oracle.rmsnorm_f32(x).view(np.uint32), want.view(np.uint32))
