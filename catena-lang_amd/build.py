@@ -60,12 +60,29 @@ def build_kernel(src: str) -> str:
     return out
 
 
+# Host-side HIP sources (csrc/host/*.hip) hold device globals the library
+# addresses from the host (hipGetSymbolAddress): compiled by hipcc for the
+# host and gfx950 into one object each, then linked into the library.
+HOST_HIP_FLAGS = [
+    "-x", "hip", "--offload-arch=gfx950", "-O2", "-std=c++17", "-fPIC",
+    "-ffp-contract=off", "-fno-fast-math",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", f"-I{os.path.join(ROOT, 'include')}",
+]
+
+
 def build_host() -> str:
     srcs = sorted(glob.glob(os.path.join(HDIR, "*.cpp")))
+    objs = []
+    os.makedirs(os.path.join(OUT, "obj"), exist_ok=True)
+    for hs in sorted(glob.glob(os.path.join(HDIR, "*.hip"))):
+        obj = os.path.join(OUT, "obj", os.path.splitext(os.path.basename(hs))[0] + ".o")
+        _run([HIPCC, *HOST_HIP_FLAGS, "-c", hs, "-o", obj])
+        objs.append(obj)
     out = os.path.join(OUT, LIB_NAME)
     tmp = out + ".tmp"
     cxx = os.environ.get("CXX", "g++")
-    _run([cxx, *HOST_FLAGS, *srcs, "-o", tmp, *HOST_LIBS])
+    _run([cxx, *HOST_FLAGS, *srcs, *objs, "-o", tmp, *HOST_LIBS])
     os.replace(tmp, out)
     return out
 

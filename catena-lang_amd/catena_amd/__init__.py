@@ -125,6 +125,7 @@ SIGNATURES = {
     "catena_mi355x_gemm_bf16": (_int, [_vp, _vp, _vp, _u64, _u64, _u64, _int]),
     "catena_mi355x_gemm_bf16_decode_plan": (_int, [_u64, _u64, _u64, ctypes.POINTER(_u32),
                                                    ctypes.POINTER(_u64)]),
+    "catena_mi355x_gemm_bf16_decode_noalloc": (_int, [_vp, _vp, _vp, _u64, _u64, _u64, _int]),
     "catena_mi355x_attn_decode_bf16": (_int, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _f32]),
     "catena_mi355x_softmax_f32": (_int, [_vp, _vp, _u64, _u64]),
     "catena_mi355x_exp_approx_f32": (_int, [_vp, _vp, _u64]),
@@ -307,6 +308,13 @@ def gemm_f32_exact(a, b, c, n: int, m: int, k: int) -> None:
 
 def gemm_bf16(a, b, c, n: int, m: int, k: int, out_f32: bool = False) -> None:
     check(lib().catena_mi355x_gemm_bf16(_p(a), _p(b), _p(c), n, m, k, 1 if out_f32 else 0))
+
+
+def gemm_bf16_decode_noalloc(a, b, c, n: int, m: int, k: int, out_f32: bool = False) -> None:
+    """Allocation-free decode-shape GEMM (partials in the library's fixed
+    device scratch)."""
+    check(lib().catena_mi355x_gemm_bf16_decode_noalloc(_p(a), _p(b), _p(c), n, m, k,
+                                                       1 if out_f32 else 0))
 
 
 def gemm_bf16_decode_plan(n: int, m: int, k: int):

@@ -317,6 +317,9 @@ int catena_mi355x_init(int device_index) {
                               hipGetErrorString(e)));
     d.fn[static_cast<int>(k.id)] = f;
   }
+  // the allocation-free entry point's scratch: its address on this device
+  st = noalloc_setup(device_index);
+  if (st) return init_failed(st);
   d.device = device_index;
   d.ready.store(true, std::memory_order_release);
   clear_error();

@@ -140,6 +140,12 @@ int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, 
 // product (0 when K is not split), and its number of k groups; a function of
 // the shape alone.
 uint64_t decode_partials_bytes(uint64_t n, uint64_t m, uint64_t k, uint32_t* k_groups);
+// Scratch of the allocation-free decode GEMM (noalloc.hip): its device
+// address, looked up once per device at init (noalloc_setup, with that
+// device current), and its size.
+int noalloc_setup(int device);
+void* noalloc_scratch(int device);
+uint64_t noalloc_scratch_bytes();
 
 // Whether catena_mi355x_gemm_bf16_silu takes this shape (the 32-k tile
 // kernels: n % 256, m % 128, k % 128 == 0, aligned operands).

@@ -127,6 +127,20 @@ int catena_mi355x_gemm_bf16(const uint16_t *a, const uint16_t *b, void *c, uint6
 int catena_mi355x_gemm_bf16_decode_plan(uint64_t n, uint64_t m, uint64_t k, uint32_t *k_groups,
                                         uint64_t *partials_bytes);
 
+/* Allocation-free form of catena_mi355x_gemm_bf16 for decode shapes
+ * (1 <= n <= 16, m % 8 == 0, k % 8 == 0, k > 0; 16-byte aligned pointers):
+ * the same kernels and the same bits, with the split-K partials in a fixed
+ * 4 MiB device array the library holds on each device from load to exit,
+ * instead of a workspace it grows with hipMalloc.  No reference counterpart:
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc).  Needs a prior
+ * catena_mi355x_init (returns CATENA_ERR_NOT_INITIALIZED otherwise; it never
+ * initialises, since init allocates); shapes whose partials exceed 4 MiB
+ * (see catena_mi355x_gemm_bf16_decode_plan) return CATENA_ERR_UNSUPPORTED.
+ * Calls share the device's array: calls that overlap on one device race. */
+int catena_mi355x_gemm_bf16_decode_noalloc(const uint16_t *a, const uint16_t *b, void *c,
+                                           uint64_t n, uint64_t m, uint64_t k, int out_f32);
+
 /* Decode attention, one query per (batch, head): q[B][H][D], k/v[B][H][L][D]
  * bf16, lens[B] (device u32, each <= L), o[B][H][D] f32.  Bitwise the
  * sequential composition of cell-dot, nn.softmax and cell-dot

@@ -1,0 +1,71 @@
+"""The allocation-free decode GEMM (catena_mi355x_gemm_bf16_decode_noalloc)
+against catena_mi355x_gemm_bf16, through the C ABI: the same bits on two
+calls in a row (the second smaller, so it runs on the scratch the first
+left behind), no device allocation by the call, and the size limit."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import catena_amd as ca
+from gpu_util import dev_normal_bf16, say
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _init():
+    say("init device 0")
+    ca.init(0)
+
+
+def _pair(m, n, k, seed):
+    x = dev_normal_bf16(m * k, seed, 0, 1.0)
+    w = dev_normal_bf16(k * n, seed, 1, 0.02)
+    return x, w
+
+
+def test_noalloc_decode_gemm_equals_the_allocating_entry_point():
+    L = ca.lib()
+    # two calls in a row, the second with a smaller input; both split K
+    # (8 and 2 k groups), so both write partials into the scratch
+    for (m, n, k, seed) in [(16, 4096, 11008, 61), (5, 1024, 2048, 62)]:
+        groups, pbytes = ca.gemm_bf16_decode_plan(m, n, k)
+        assert groups > 1 and 0 < pbytes <= 4 << 20
+        x, w = _pair(m, n, k, seed)
+        for out_f32, dt, es in ((False, np.uint16, 2), (True, np.uint32, 4)):
+            want, got = ca.Buffer(m * n * es), ca.Buffer(m * n * es)
+            say(f"decode GEMM M={m} N={n} K={k} out_f32={out_f32}: allocating entry point")
+            ca.gemm_bf16(x, w, want, m, n, k, out_f32=out_f32)
+            ca.synchronize()
+            allocs = ca.pool_stats()["device_allocs"]
+            say(f"decode GEMM M={m} N={n} K={k} out_f32={out_f32}: allocation-free entry point")
+            st = L.catena_mi355x_gemm_bf16_decode_noalloc(x.ptr, w.ptr, got.ptr, m, n, k,
+                                                          1 if out_f32 else 0)
+            assert st == 0, ca.last_error()
+            ca.synchronize()
+            assert ca.pool_stats()["device_allocs"] == allocs
+            assert np.array_equal(got.read(dt), want.read(dt)), (m, n, k, out_f32)
+
+
+def test_noalloc_decode_gemm_limits():
+    L = ca.lib()
+    # partials of 3 k groups x 16 x 24224 f32 = 4.4 MiB: beyond the 4 MiB scratch
+    groups, pbytes = ca.gemm_bf16_decode_plan(16, 24224, 2056)
+    assert pbytes > 4 << 20
+    x, w = _pair(16, 24224, 2056, 63)
+    y = ca.Buffer(16 * 24224 * 2)
+    say("allocation-free decode GEMM beyond its scratch (refused before launch)")
+    st = L.catena_mi355x_gemm_bf16_decode_noalloc(x.ptr, w.ptr, y.ptr, 16, 24224, 2056, 0)
+    assert st == 2 and "scratch" in ca.last_error()
+    # not a decode shape
+    st = L.catena_mi355x_gemm_bf16_decode_noalloc(x.ptr, w.ptr, y.ptr, 17, 128, 128, 0)
+    assert st == 1
+    # a shape that does not split K needs no scratch at all
+    x2, w2 = _pair(8, 32000, 2048, 64)
+    assert ca.gemm_bf16_decode_plan(8, 32000, 2048) == (1, 0)
+    a, b = ca.Buffer(8 * 32000 * 2), ca.Buffer(8 * 32000 * 2)
+    say("allocation-free decode GEMM without a k split")
+    ca.gemm_bf16(x2, w2, a, 8, 32000, 2048)
+    assert L.catena_mi355x_gemm_bf16_decode_noalloc(x2.ptr, w2.ptr, b.ptr, 8, 32000, 2048, 0) == 0
+    assert np.array_equal(a.read(np.uint16), b.read(np.uint16))
