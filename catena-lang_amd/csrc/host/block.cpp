@@ -87,6 +87,9 @@ int catena_mi355x_attn_causal_bf16(const uint16_t* q, const uint16_t* k, const u
   if (lds > device().max_lds)
     return fail(CATENA_ERR_UNSUPPORTED, "max_len %u needs %zu B of LDS (device has %zu)", max_len,
                 lds, device().max_lds);
+  // few (query, head) pairs: the eight-wave kernel spreads each over a CU
+  int split = attn_few_launch(q, k, v, lens, o, batch, tq, heads, max_len, scale, out_f32 != 0);
+  if (split >= 0) return split;
   void* args[] = {&q, &k, &v, &lens, &o, &heads, &max_len, &tq, &scale};
   return launch(out_f32 ? KernelId::AttnCausalD128F32 : KernelId::AttnCausalD128Bf16,
                 dim3((unsigned)blocks), dim3(256), lds, args);

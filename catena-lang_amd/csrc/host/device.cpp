@@ -68,6 +68,8 @@ const KernelSpec kKernels[] = {
     {KernelId::GemmBf16DecodeSilu, "gemm_bf16_decode", "catena_gemm_bf16_decode_silu"},
     {KernelId::GemmBf16DecodeArgmax, "gemm_bf16_decode", "catena_gemm_bf16_decode_argmax"},
     {KernelId::AttnDecodeD128, "attn_decode", "catena_attn_decode_bf16_d128"},
+    {KernelId::AttnFewD128F32, "attn_few", "catena_attn_few_bf16_d128_f32out"},
+    {KernelId::AttnFewD128Bf16, "attn_few", "catena_attn_few_bf16_d128_bf16out"},
     {KernelId::AttnCausalD128F32, "attn_decode", "catena_attn_causal_bf16_d128_f32out"},
     {KernelId::AttnCausalD128Bf16, "attn_decode", "catena_attn_causal_bf16_d128_bf16out"},
     {KernelId::AttnPrefillD128F32, "attn_prefill", "catena_attn_prefill_bf16_d128_f32out"},

@@ -30,6 +30,8 @@ enum class KernelId : int {
   GemmBf16DecodeSilu,
   GemmBf16DecodeArgmax,
   AttnDecodeD128,
+  AttnFewD128F32,  // eight waves per pair for few pairs (attn_few.hip)
+  AttnFewD128Bf16,
   AttnCausalD128F32,
   AttnCausalD128Bf16,
   AttnPrefillD128F32,
@@ -91,6 +93,22 @@ struct Device {
 // K / V staging area, reduction slots, then one f32 score per position.
 constexpr size_t kAttnLdsFixed = 128 * 4 + 16384 + 64;
 inline size_t attn_lds_bytes(uint32_t max_len) { return kAttnLdsFixed + (size_t)max_len * 4; }
+
+// The eight-wave attention (attn_few.hip) for few (query, head) pairs, where
+// the four-wave kernel leaves CUs idle or underfed: one workgroup per pair,
+// at most one per CU.  LDS: six q copies and the max words, six 4 KiB K
+// stages and two 48 KiB V rings (124 KiB), then 64 f32 scores per 64-row
+// block.
+constexpr uint64_t kAttnFewMaxQueries = 256;
+constexpr size_t kAttnFewFixed = 4096 + 6 * 4096 + 2 * 6 * 8192;
+inline size_t attn_few_lds_bytes(uint32_t max_len) {
+  return kAttnFewFixed + (size_t)((max_len + 63) / 64) * (64 * 4);
+}
+// Launch the eight-wave attention when it applies; returns -1 (nothing
+// launched) when it does not.
+int attn_few_launch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint32_t* lens,
+                    void* o, uint32_t batch, uint32_t tq, uint32_t heads, uint32_t max_len,
+                    float scale, bool out_f32);
 
 // LDS of catena_rmsnorm_rows (block.hip): its static __shared__ f32 (rounded
 // up to the 16-byte alignment of the dynamic area that follows it) plus the

@@ -154,6 +154,19 @@ int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, 
   return launch(id, dim3((unsigned)gx, (unsigned)S), dim3(256), lds, args);
 }
 
+int attn_few_launch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint32_t* lens,
+                    void* o, uint32_t batch, uint32_t tq, uint32_t heads, uint32_t max_len,
+                    float scale, bool out_f32) {
+  const uint64_t nq = (uint64_t)batch * tq * heads;
+  Device& d = device();
+  if (nq == 0 || nq > kAttnFewMaxQueries || tq >= 8 || max_len < 64 ||
+      attn_few_lds_bytes(max_len) > d.max_lds)
+    return -1;
+  void* args[] = {&q, &k, &v, &lens, &o, &heads, &max_len, &tq, &scale};
+  return launch(out_f32 ? KernelId::AttnFewD128F32 : KernelId::AttnFewD128Bf16, dim3((unsigned)nq),
+                dim3(512), attn_few_lds_bytes(max_len), args);
+}
+
 bool gemm_bf16_silu_fits(uint64_t n, uint64_t m, uint64_t k, const void* a, const void* b,
                          const void* act) {
   return n % 256 == 0 && m % 128 == 0 && k % 128 == 0 && k > 0 && k <= (1ull << 22) &&
@@ -277,6 +290,9 @@ int catena_mi355x_attn_decode_bf16(const uint16_t* q, const uint16_t* k, const u
   if (lds > d.max_lds)
     return fail(CATENA_ERR_UNSUPPORTED, "max_len %u needs %zu B of LDS (device has %zu)", max_len,
                 lds, d.max_lds);
+  // few (batch, head) pairs: the eight-wave kernel spreads each over a CU
+  st = attn_few_launch(q, k, v, lens, o, batch, 1, heads, max_len, scale, true);
+  if (st >= 0) return st;
   void* args[] = {&q, &k, &v, &lens, &o, &heads, &max_len, &scale};
   return launch(KernelId::AttnDecodeD128, dim3((unsigned)bh), dim3(256), lds, args);
 }

@@ -1,0 +1,418 @@
+// KV-cache attention for few (query, head) pairs -- the decode step of a
+// small batch -- in one kernel of eight waves per pair, so that each pair's
+// positions and output columns spread over more of its CU than the
+// four-wave kernel of attn_decode.hip manages.  Same definition and fold
+// orders as attn_decode.hip, so the same bits:
+//   s_t = (fold_{d asc} from +0 of q_d * k_{t,d}) * scale
+//         -- f32.matmul.cell-dot order, catena-lang/stdlib/matrix.hex:236-256
+//   m   = f32.max-env fold from -inf        (catena-lang/stdlib/sum.hex:73-84)
+//   den = f32.add-env fold from +0 of exp~(s_t - m)  (catena-lang/stdlib/nn.hex:93-114)
+//   p_t = exp~(s_t - m) / den                (catena-lang/stdlib/nn.hex:75-90)
+//   o_d = fold_{t asc} from +0 of p_t * v_{t,d}
+//
+// Layouts as attn_decode.hip: q[B][Tq][H][128], k/v[B][H][L][128] bf16,
+// lens[B], o[B][Tq][H][128] f32 or bf16; workgroup qi = (b * Tq + tq) * H + h
+// attends to the first lens[b] - (Tq - 1 - tq) positions (clamped to L).
+//
+// Waves 0-5 score: each first requests its own copy of q, then all four
+// 32-wide d segments of its first two 64-row blocks (blocks w, w+6, ...;
+// coalesced 16-byte loads, 4 lanes per 64-byte row segment), and folds each
+// segment through its LDS slice with lane l owning row l (one d-ascending
+// chain of v_mul_f32 + v_add_f32 per score).  The max fold is reduced with
+// one LDS atomic per wave and block for each of the last NaN position and a
+// 64-bit key whose maximum is the first maximal score (see max_key).  When a NaN precedes the
+// last position the key is taken again over the positions after it.  Then
+// every score wave computes exp~ for its share of positions, wave 0 runs the
+// denominator (the one sequential chain), and the score waves divide their
+// shares.
+// Waves 6 and 7 own output columns 0-63 and 64-127.  Once the score waves
+// have requested their K rows (so that K, which is needed first, is ahead
+// of V in the memory queues) they stream their V rows (128 bytes per row)
+// straight into private LDS rings of 64-row batches, and once p is ready
+// fold their columns (lane = column) t ascending: each half batch is read
+// into registers while the previous one is folded, and a slot is refilled as
+// soon as its batch is in registers.
+//
+// Cost (measured on MI355X at 2.4 GHz): one wave issues a VALU op about
+// every 4.1 cycles and a chain of dependent v_add_f32 runs at about 4.5
+// cycles per add, so the V fold (unpack, multiply, add per position and
+// column) is issue-bound at about 12.5 cycles per position.
+#include "common.h"
+
+namespace {
+constexpr int D = 128;
+constexpr int KWAVES = 6;
+constexpr int KSTAGE_ROW = 64;                // bytes per staged row segment
+constexpr int KSTAGE_WAVE = 64 * KSTAGE_ROW;  // 4096 B per wave
+CATENA_DEV uint32_t kswz(uint32_t row, uint32_t chunk) { return 16u * (chunk ^ ((row >> 2) & 3u)); }
+
+constexpr int VB_ROWS = 64;              // rows per V batch
+constexpr int VB_BYTES = VB_ROWS * 128;  // 64 rows x 64 columns bf16
+constexpr int VRING = 6;                 // batches in flight per V wave (8 loads each)
+
+// LDS: q copies [6][128] f32 | den, last score, last NaN, max keys |
+// K stages [6][4 KiB] | V rings [2][VRING][8 KiB] | scores sp[64 * ceil(L/64)]
+constexpr uint32_t kOffDen = KWAVES * 512;
+constexpr uint32_t kOffK = 4096;
+constexpr uint32_t kOffV = kOffK + KWAVES * KSTAGE_WAVE;
+constexpr uint32_t kOffState = kOffV + 2 * VRING * VB_BYTES;
+
+CATENA_DEV void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS
+// operations, not for its global loads (the V waves' requests stay in
+// flight through the barriers).
+CATENA_DEV void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// s_waitcnt on vmcnt only (gfx9 encoding: vmcnt[3:0], vmcnt[5:4] at 15:14)
+#define FEW_WAIT_VMCNT(n) \
+  __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | 0x0070 | 0x0F00)
+
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) unsigned char lds_u8;
+typedef __attribute__((address_space(3))) f32x4_t lds_f32x4;
+
+// The f32.max-env fold (acc = (acc >= x) ? acc : x from -inf, ascending)
+// returns, without NaNs, the first score equal to the maximum (+0 and -0
+// compare equal, so the earlier of them wins).  max_key orders (score,
+// position) so that the largest key is exactly that score: the score's bits
+// made monotone (with -0 taken as +0) above the complemented position, and
+// the sign bit at the bottom so that the score's exact bits come back
+// (key_score).  0 is below every key (no score).  A NaN resets the fold:
+// the result is then the last NaN if it is the final score, otherwise the
+// first maximum of the scores after the last NaN.
+CATENA_DEV uint32_t mono_bits(uint32_t bits) {
+  const uint32_t canon = bits == 0x80000000u ? 0u : bits;
+  return (canon & 0x80000000u) ? ~canon : (canon | 0x80000000u);
+}
+CATENA_DEV uint64_t make_key(uint32_t mono, uint32_t t, uint32_t bits) {
+  return ((uint64_t)mono << 32) | ((0x7FFFFFFFu - t) << 1) | (bits >> 31);
+}
+CATENA_DEV uint64_t max_key(float v, uint32_t t) {
+  const uint32_t bits = __float_as_uint(v);
+  return make_key(mono_bits(bits), t, bits);
+}
+
+// Maximum over the wave of an unsigned value (0 is the identity): inclusive
+// max scans within rows of 16 lanes (row_shr 1, 2, 4, 8), rows joined
+// through row_bcast 15 and 31, lane 63's result returned uniformly.
+CATENA_DEV uint32_t wave_umax(uint32_t x) {
+#define FEW_DPP_MAX(ctrl, rows) \
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, (ctrl), (rows), 0xF, false))
+  FEW_DPP_MAX(0x111, 0xF);
+  FEW_DPP_MAX(0x112, 0xF);
+  FEW_DPP_MAX(0x114, 0xF);
+  FEW_DPP_MAX(0x118, 0xF);
+  FEW_DPP_MAX(0x142, 0xA);
+  FEW_DPP_MAX(0x143, 0xC);
+#undef FEW_DPP_MAX
+  return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+}
+CATENA_DEV float key_score(uint64_t key) {
+  const uint32_t mono = (uint32_t)(key >> 32);
+  const uint32_t canon = (mono & 0x80000000u) ? (mono & 0x7FFFFFFFu) : ~mono;
+  return __uint_as_float(canon == 0u ? ((uint32_t)key & 1u) << 31 : canon);
+}
+
+template <bool OUT_BF16>
+CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                              const uint16_t* __restrict__ v, const uint32_t* __restrict__ lens,
+                              void* __restrict__ o, uint32_t H, uint32_t L, uint32_t Tq, float scale) {
+  extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
+  float* den_slot = reinterpret_cast<float*>(smem + kOffDen);
+  float* last_slot = den_slot + 1;                                          // score at len - 1
+  uint32_t* nan_word = reinterpret_cast<uint32_t*>(smem + kOffDen + 8);     // last NaN + 1
+  uint64_t* key_word = reinterpret_cast<uint64_t*>(smem + kOffDen + 16);    // [2] max keys
+  float* sp = reinterpret_cast<float*>(smem + kOffState);  // 16-byte aligned
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t qi = blockIdx.x;
+  const uint32_t row = qi / H, h = qi % H;
+  const uint32_t b = row / Tq, tq = row % Tq;
+  uint32_t len = lens[b];
+  if (len > L) len = L;
+  const uint32_t later = Tq - 1 - tq;
+  len = len > later ? len - later : 0u;
+  const uint64_t bh = (uint64_t)b * H + h;
+  const uint16_t* kb = k + bh * (uint64_t)L * D;
+  const uint16_t* vb = v + bh * (uint64_t)L * D;
+  const uint32_t nblk = (len + 63u) / 64u;
+
+  if (wave >= KWAVES) {
+    // ---------------------------------------------------------- V waves
+    const uint32_t vw = (uint32_t)wave - KWAVES;  // column half
+    const uint32_t colbase = 64u * vw;
+    // the ring's LDS offset, uniform across the wave (so M0 is set from a
+    // scalar register)
+    const uint32_t ring_off = __builtin_amdgcn_readfirstlane(kOffV + vw * (VRING * VB_BYTES));
+    // batch bt -> slot bt % VRING: 8 direct-to-LDS loads of 1 KiB (8 rows x
+    // 128 bytes; lane l: row l / 8, chunk l % 8).  In the last batch rows
+    // past len read row 0 instead (in bounds, never folded), so every batch
+    // is exactly 8 loads and the waits below are exact.
+    const uint32_t vr = (uint32_t)lane >> 3, vc = (uint32_t)lane & 7u;
+    const uint16_t* vlane = vb + (uint64_t)vr * D + colbase + 8 * vc;
+    auto issue = [&](uint32_t bt) {
+      unsigned char* slot = smem + ring_off + (bt % VRING) * VB_BYTES;
+      if ((bt + 1) * VB_ROWS <= len) {
+        const uint16_t* src = vlane + (uint64_t)bt * VB_ROWS * D;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          __builtin_amdgcn_global_load_lds(src + 8 * i * D, (lds_void*)(slot + 1024 * i), 16, 0, 0);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          uint32_t t = bt * VB_ROWS + 8 * i + vr;
+          if (t >= len) t = 0;
+          __builtin_amdgcn_global_load_lds(vb + (uint64_t)t * D + colbase + 8 * vc,
+                                           (lds_void*)(slot + 1024 * i), 16, 0, 0);
+        }
+      }
+    };
+    __builtin_amdgcn_s_barrier();  // (0) K requested, max words cleared
+    const uint32_t pre = nblk < (uint32_t)VRING ? nblk : (uint32_t)VRING;
+    for (uint32_t bt = 0; bt < pre; ++bt) issue(bt);
+    lds_barrier();  // (1) scores, last NaN and first key written
+    const uint32_t jn = *nan_word;
+    if (jn != 0u && jn < len) lds_barrier();  // (1a) key after the last NaN
+    __builtin_amdgcn_s_barrier();  // (2) exp~ written
+    __builtin_amdgcn_s_barrier();  // (3) den written
+    __builtin_amdgcn_s_barrier();  // (4) p written
+    asm volatile("" ::: "memory");
+
+    // batch bt's data has landed once the loads of the batches issued after
+    // it (bt+1 .. min(bt+VRING-1, nblk-1), 8 each) are all that is left
+    auto wait_batch = [&](uint32_t bt) {
+      const uint32_t after = nblk - 1 - bt < (uint32_t)(VRING - 1) ? nblk - 1 - bt : (uint32_t)(VRING - 1);
+      switch (after) {
+        case 0: FEW_WAIT_VMCNT(0); break;
+        case 1: FEW_WAIT_VMCNT(8); break;
+        case 2: FEW_WAIT_VMCNT(16); break;
+        case 3: FEW_WAIT_VMCNT(24); break;
+        case 4: FEW_WAIT_VMCNT(32); break;
+        default: FEW_WAIT_VMCNT(40); break;
+      }
+      asm volatile("" ::: "memory");
+    };
+    // half a batch (32 rows) into registers: four rows of this lane's
+    // column per transposing read (lane 4j + a of a 16-lane group addresses
+    // row 4u + j, columns 16g + 4a .. +3, and lane i receives column 16g + i
+    // of rows 4u .. 4u+3), p four at a time.  The bases are opaque 32-bit
+    // LDS addresses so that the eight reads of each kind share one base
+    // register and differ only in their immediate offsets.
+    const uint32_t tr_off = (4u * (((uint32_t)lane & 15u) >> 2)) * 32u +
+                            2u * (16u * ((uint32_t)lane >> 4) + 4u * ((uint32_t)lane & 3u));
+    auto read_half = [&](uint32_t bt, int half, f32x4_t p4[8], i16x4_t v4[8]) {
+      uint32_t vbase = ring_off + (bt % VRING) * VB_BYTES + half * 32 * 128 + tr_off;
+      uint32_t pbase = kOffState + (bt * VB_ROWS + half * 32) * 4;
+      asm volatile("" : "+v"(vbase), "+v"(pbase));
+      const lds_u8* vp = (const lds_u8*)smem + vbase;
+      const lds_u8* pp = (const lds_u8*)smem + pbase;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        p4[u] = *(const lds_f32x4*)(pp + 16 * u);
+        v4[u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vp + 512 * u));
+      }
+    };
+    float acc = __uint_as_float(0u);
+    // once a batch's reads are done its slot takes batch bt + VRING; the
+    // empty asm on acc keeps the fold issued before it in front of the wait
+    auto refill = [&](uint32_t bt) {
+      asm volatile("" ::"v"(acc));
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      asm volatile("" ::: "memory");
+      if (bt + VRING < nblk) issue(bt + VRING);
+    };
+    // products first (independent of acc), then the t-ascending chain
+    auto fold_regs = [&](const f32x4_t p4[8], const i16x4_t v4[8]) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        float prod[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) prod[e] = p4[u][e] * bf16_to_f32((uint16_t)v4[u][e]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc = acc + prod[e];
+      }
+    };
+    // full batches: each half is read while the one before it folds
+    const uint32_t nfull = len / VB_ROWS;
+    f32x4_t pa[8], pb[8];
+    i16x4_t va[8], vb8[8];
+    if (nfull > 0) {
+      wait_batch(0);
+      read_half(0, 0, pa, va);
+    }
+    uint32_t bt = 0;
+    for (; bt < nfull; ++bt) {
+      read_half(bt, 1, pb, vb8);
+      fold_regs(pa, va);
+      refill(bt);
+      if (bt + 1 < nfull) {
+        wait_batch(bt + 1);
+        read_half(bt + 1, 0, pa, va);
+      }
+      fold_regs(pb, vb8);
+    }
+    if (bt < nblk) {
+      // the last, partial batch
+      wait_batch(bt);
+      const uint16_t* st16 = reinterpret_cast<const uint16_t*>(smem + ring_off + (bt % VRING) * VB_BYTES);
+      const uint32_t t0 = bt * VB_ROWS;
+      for (uint32_t rr = 0; rr < len - t0; ++rr) {
+        const float prod = sp[t0 + rr] * bf16_to_f32(st16[rr * 64 + lane]);
+        acc = acc + prod;
+      }
+    }
+    if (OUT_BF16)
+      static_cast<uint16_t*>(o)[(uint64_t)qi * D + colbase + lane] = (uint16_t)f32_to_bf16_bits(acc);
+    else
+      static_cast<float*>(o)[(uint64_t)qi * D + colbase + lane] = acc;
+    return;
+  }
+
+  // ------------------------------------------------------------ K waves
+  // this wave's q, requested ahead of its K rows so it lands first
+  const uint16_t q_lo = q[(uint64_t)qi * D + 2 * lane];
+  const uint16_t q_hi = q[(uint64_t)qi * D + 2 * lane + 1];
+  const int lrow = lane >> 2, lchunk = lane & 3;
+  unsigned char* st = smem + kOffK + wave * KSTAGE_WAVE;
+  float* qf = reinterpret_cast<float*>(smem + wave * 512);
+  auto gload = [&](uint32_t blk, u32x4_t r[16]) {
+#pragma unroll
+    for (int seg = 0; seg < 4; ++seg)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t t = blk * 64 + lrow + 16 * i;
+        if (t >= len) t = 0;  // in bounds; such a score is never read
+        r[4 * seg + i] = *reinterpret_cast<const u32x4_t*>(kb + (uint64_t)t * D + seg * 32 + lchunk * 8);
+      }
+  };
+  // one block: its 64 scores into sp, its max-fold state into the block
+  // state arrays
+  auto fold = [&](uint32_t blk, const u32x4_t r[16]) {
+    float acc = __uint_as_float(0u);
+#pragma unroll
+    for (int seg = 0; seg < 4; ++seg) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<u32x4_t*>(st + (lrow + 16 * i) * KSTAGE_ROW + kswz(lrow, lchunk)) = r[4 * seg + i];
+      wave_sync();
+      const unsigned char* myrow = st + lane * KSTAGE_ROW;
+#pragma unroll
+      for (int ch = 0; ch < 4; ++ch) {
+        const u32x4_t kv = *reinterpret_cast<const u32x4_t*>(myrow + kswz(lane, ch));
+        const f32x4_t q0 = *reinterpret_cast<const f32x4_t*>(qf + seg * 32 + ch * 8);
+        const f32x4_t q1 = *reinterpret_cast<const f32x4_t*>(qf + seg * 32 + ch * 8 + 4);
+        float p;
+        p = q0[0] * bf16lo(kv[0]); acc = acc + p;
+        p = q0[1] * bf16hi(kv[0]); acc = acc + p;
+        p = q0[2] * bf16lo(kv[1]); acc = acc + p;
+        p = q0[3] * bf16hi(kv[1]); acc = acc + p;
+        p = q1[0] * bf16lo(kv[2]); acc = acc + p;
+        p = q1[1] * bf16hi(kv[2]); acc = acc + p;
+        p = q1[2] * bf16lo(kv[3]); acc = acc + p;
+        p = q1[3] * bf16hi(kv[3]); acc = acc + p;
+      }
+      wave_sync();  // the slice is rewritten by the next segment
+    }
+    // stored unconditionally (sp holds whole blocks; entries past len are
+    // never read), so the dot product stays where its operands arrive
+    // instead of sinking into a branch that keeps them all live
+    const uint32_t t = blk * 64 + (uint32_t)lane;
+    const float sv = acc * scale;
+    sp[t] = sv;
+    if (t + 1 == len) *last_slot = sv;  // read by every score wave below
+    // one LDS atomic per wave and block: the block's last NaN, and the key
+    // of its first maximal score (the wave's largest monotone bits, then
+    // the lowest lane holding them)
+    const bool in = t < len, nan = sv != sv;
+    const uint64_t nans = __builtin_amdgcn_ballot_w64(in && nan);
+    if (nans != 0u && lane == 0)
+      __hip_atomic_fetch_max(nan_word, blk * 64 + (63u - (uint32_t)__builtin_clzll(nans)) + 1u, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_WORKGROUP);
+    const uint32_t bits = __float_as_uint(sv);
+    const uint32_t mono = (in && !nan) ? mono_bits(bits) : 0u;
+    const uint32_t m = wave_umax(mono);
+    if (m != 0u) {
+      const uint32_t wl = (uint32_t)__builtin_ctzll(__builtin_amdgcn_ballot_w64(mono == m));
+      const uint32_t wbits = (uint32_t)__builtin_amdgcn_readlane((int)bits, (int)wl);
+      if (lane == 0)
+        __hip_atomic_fetch_max(&key_word[0], make_key(m, blk * 64 + wl, wbits), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  };
+  // (loads are unconditional: rows past len read row 0, so no copies of
+  // the register blocks are needed to merge loaded and not-loaded paths)
+  u32x4_t ra[16], rb[16];
+  const uint32_t b0 = (uint32_t)wave;
+  gload(b0, ra);
+  gload(b0 + KWAVES, rb);
+  if (wave == 0 && lane == 0) {
+    *nan_word = 0u;
+    key_word[0] = 0u;
+    key_word[1] = 0u;
+  }
+  lds_barrier();  // (0) K requested (V follows it), max words cleared
+  qf[2 * lane] = bf16_to_f32(q_lo);
+  qf[2 * lane + 1] = bf16_to_f32(q_hi);
+  wave_sync();
+  for (uint32_t bk = b0; bk < nblk; bk += 2 * KWAVES) {
+    fold(bk, ra);
+    gload(bk + 2 * KWAVES, ra);
+    if (bk + KWAVES < nblk) fold(bk + KWAVES, rb);
+    gload(bk + 3 * KWAVES, rb);
+  }
+  lds_barrier();  // (1) scores, last NaN and first key written
+  const uint32_t stride = 64u * KWAVES;
+  const uint32_t jn = *nan_word;  // last NaN position + 1, 0 if none
+  uint64_t key = key_word[0];
+  if (jn != 0u && jn < len) {
+    // the first maximum of the scores after the last NaN
+    for (uint32_t t = jn + (uint32_t)(wave * 64 + lane); t < len; t += stride)
+      __hip_atomic_fetch_max(&key_word[1], max_key(sp[t], t), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    lds_barrier();  // (1a)
+    key = key_word[1];
+  }
+  float mx;
+  if (jn != 0u && jn == len)
+    mx = *last_slot;  // the final score is NaN: the fold returns it
+  else
+    mx = key == 0u ? __uint_as_float(0xFF800000u) : key_score(key);
+  for (uint32_t t = (uint32_t)(wave * 64 + lane); t < len; t += stride) sp[t] = exp_approx(sp[t] - mx);
+  lds_barrier();  // (2) exp~ written
+  if (wave == 0) {
+    // the one sequential fold den = (((0 + e_0) + e_1) + ...) in ascending t
+    const float den = len >= 1024 ? serial_sum_wave_long(sp, len) : serial_sum_wave(sp, len);
+    if (lane == 0) *den_slot = den;
+  }
+  lds_barrier();  // (3) den written
+  const float den = *den_slot;
+  for (uint32_t t = (uint32_t)(wave * 64 + lane); t < len; t += stride) sp[t] = sp[t] / den;
+  lds_barrier();  // (4) p written
+}
+
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(512) void catena_attn_few_bf16_d128_f32out(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const uint32_t* __restrict__ lens, float* __restrict__ o, uint32_t H, uint32_t L, uint32_t Tq,
+    float scale) {
+  attn_few_body<false>(q, k, v, lens, o, H, L, Tq, scale);
+}
+
+extern "C" __global__ __launch_bounds__(512) void catena_attn_few_bf16_d128_bf16out(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const uint32_t* __restrict__ lens, uint16_t* __restrict__ o, uint32_t H, uint32_t L, uint32_t Tq,
+    float scale) {
+  attn_few_body<true>(q, k, v, lens, o, H, L, Tq, scale);
+}

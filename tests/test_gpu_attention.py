@@ -110,3 +110,59 @@ def test_attention_program_abi():
     got = ca.mem_to_array(res.get(), np.float32).reshape(B, H, D)
     _bitwise(got, oracle.attn_decode(q16, k16, v16, lens, 0.125))
     ca.mem_free(res.get())
+
+
+@pytest.mark.parametrize("L,lens", [(640, [513, 640, 600, 577, 64, 65, 1, 0]),
+                                    (2000, [2000, 1999, 1025, 256, 257, 255, 1024, 1500]),
+                                    (600, [600, 384, 385, 383, 448, 63, 2, 599])])
+def test_few_pairs_form_equals_many_pairs_form(L, lens):
+    """Eight sequences x 16 heads (128 pairs) take the eight-wave kernel; the
+    same sequences inside a batch of 40 (640 pairs) take the four-wave
+    kernel: per (b, h) the outputs are the same bits, and both equal the
+    oracle.  Lengths cross the 64-row blocks and the six score waves'
+    rotation (384 rows), down to 1 and 0, around the 1024 switch of the
+    denominator's chain, with ceil(L / 64) not a multiple of 4."""
+    H = 16
+    Bs, Bl = 8, 40
+    seed = 77 + L
+    q = dev_normal_bf16(Bl * H * D, seed, 0)
+    k = dev_normal_bf16(Bl * H * L * D, seed, 1)
+    v = dev_normal_bf16(Bl * H * L * D, seed, 2)
+    scale = float(np.float32(1.0 / math.sqrt(D)))
+    lens_l = list(lens) + [L] * (Bl - Bs)
+    say(f"attention eight-wave form B={Bs} H={H} L={L}")
+    small = _run(q, k, v, lens, Bs, H, L, scale)
+    say(f"attention four-wave form B={Bl} H={H} L={L}")
+    large = _run(q, k, v, lens_l, Bl, H, L, scale)
+    assert np.array_equal(small.view(np.uint32), large[:Bs].view(np.uint32))
+    want = oracle.attn_decode(q.read(np.uint16, (Bl, H, D))[:Bs], k.read(np.uint16, (Bl, H, L, D))[:Bs],
+                              v.read(np.uint16, (Bl, H, L, D))[:Bs], np.array(lens, np.uint32), scale)
+    _bitwise(small, want)
+
+
+def test_few_pairs_form_nan_at_block_boundaries():
+    """NaN and infinite scores at 64-row block boundaries (63 / 64, and 383 /
+    384 where the six score waves' rotation wraps), several NaNs in one head
+    with larger scores after the last, and a NaN at the last position,
+    through the eight-wave kernel: bitwise the oracle."""
+    B, H, L = 1, 6, 600
+    rng = np.random.default_rng(18)
+    q16 = oracle.f32_to_bf16_bits_np(rng.normal(0, 1, (B, H, D)).astype(np.float32))
+    k32 = rng.normal(0, 1, (B, H, L, D)).astype(np.float32)
+    k32[0, 0, 63, 3] = np.nan
+    k32[0, 1, 64, 0] = np.nan
+    k32[0, 1, 300, :] = 1e30
+    k32[0, 2, L - 1, 7] = np.nan
+    k32[0, 3, 383, :] = 1e30
+    k32[0, 3, 384, :] = 1e30   # two equal +inf scores: the first one wins the max
+    k32[0, 4, 10, 1] = np.nan
+    k32[0, 4, 200, 2] = np.nan
+    k32[0, 4, 450, :] = 1e30   # after the last NaN: the max restarts there
+    k32[0, 5, 0, 5] = np.nan
+    k16 = oracle.f32_to_bf16_bits_np(k32)
+    v16 = oracle.f32_to_bf16_bits_np(rng.normal(0, 1, (B, H, L, D)).astype(np.float32))
+    qb, kb, vb = ca.Buffer.from_array(q16), ca.Buffer.from_array(k16), ca.Buffer.from_array(v16)
+    say("attention eight-wave form NaN / inf at block boundaries")
+    got = _run(qb, kb, vb, [L], B, H, L, 0.088388)
+    want = oracle.attn_decode(q16, k16, v16, np.array([L], np.uint32), 0.088388)
+    _bitwise(got, want)
