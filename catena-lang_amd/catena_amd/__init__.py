@@ -443,7 +443,7 @@ class DecoderConfig(ctypes.Structure):
 # catena_decoder_tensor_t
 (DEC_EMBED, DEC_W_QKV, DEC_W_O, DEC_W_GU, DEC_W_DOWN, DEC_W_LM, DEC_K_CACHE, DEC_V_CACHE,
  DEC_INV_FREQ, DEC_X, DEC_XN, DEC_QKV, DEC_Q, DEC_ATTN, DEC_ATTN_PROJ, DEC_H, DEC_HN, DEC_GU,
- DEC_ACT, DEC_FFN_OUT, DEC_FINAL_H, DEC_FINAL_XN, DEC_LOGITS, DEC_LENS) = range(24)
+ DEC_ACT, DEC_FFN_OUT, DEC_FINAL_H, DEC_FINAL_XN, DEC_LOGITS, DEC_LENS, DEC_EMBED_NORM) = range(25)
 
 
 class Decoder:
@@ -557,6 +557,12 @@ def mem_to_array(m: Mem, dtype) -> np.ndarray:
     out = np.empty(m.len // dtype.itemsize, dtype)
     check(lib().catena_mem_read(m, 0, out.ctypes.data_as(_vp), out.nbytes))
     return out
+
+
+def mem_write(m: Mem, arr: np.ndarray, offset: int = 0) -> None:
+    """Host -> device copy into a runtime Mem (catena_mem_write)."""
+    arr = np.ascontiguousarray(arr)
+    check(lib().catena_mem_write(m, offset, arr.ctypes.data_as(_vp), arr.nbytes))
 
 
 def mem_free(m: Mem) -> None:

@@ -21,8 +21,10 @@ int rmsnorm_launch(const float* x, const float* resid, const uint32_t* row_index
   int st = ensure_init();
   if (st) return st;
   if (rows == 0 || n == 0) return CATENA_OK;
-  if ((!x && !tokens) || (!y_f32 && !y_bf16)) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
-  if (tokens && (!table || (n % 4 == 0 && (reinterpret_cast<uintptr_t>(table) & 7u))))
+  // input rows: x, or the embedding gather (tokens into table), or the
+  // table's own rows (neither x nor tokens)
+  if ((!x && !table) || (!y_f32 && !y_bf16)) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
+  if ((tokens || !x) && (!table || (n % 4 == 0 && (reinterpret_cast<uintptr_t>(table) & 7u))))
     return fail(CATENA_ERR_INVALID_ARGUMENT, "embedding table missing or misaligned");
   if (rows > 0x7FFFFFFFull || n > 0xFFFFFFFFull)
     return fail(CATENA_ERR_UNSUPPORTED, "rmsnorm shape too large");
@@ -50,6 +52,19 @@ int embed_rmsnorm_bf16(const uint32_t* tokens, const uint16_t* table, uint32_t v
                        float* x_out, uint16_t* y, uint64_t rows, uint64_t n) {
   if (!tokens || !y) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
   return rmsnorm_launch(nullptr, nullptr, nullptr, x_out, nullptr, y, rows, n, tokens, table, vocab);
+}
+
+int embed_residual_rmsnorm_bf16(const uint32_t* tokens, const uint16_t* table, uint32_t vocab,
+                                const float* resid, float* h_out, uint16_t* y, uint64_t rows,
+                                uint64_t n) {
+  if (!tokens || !resid || !y) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
+  return rmsnorm_launch(nullptr, resid, nullptr, h_out, nullptr, y, rows, n, tokens, table, vocab);
+}
+
+int embed_norm_table_bf16(const uint16_t* table, uint32_t vocab, uint16_t* y, uint64_t n) {
+  if (!table || !y) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
+  return rmsnorm_launch(nullptr, nullptr, nullptr, nullptr, nullptr, y, (uint64_t)vocab + 1, n, nullptr,
+                        table, vocab);
 }
 }  // namespace catena
 

@@ -25,6 +25,10 @@ struct catena_decoder {
   uint64_t d = 0, f = 0;
   // weights and caches
   void* embed = nullptr;
+  // bf16 rmsnorm of every embedding row ([vocab + 1][d], the last row NaN),
+  // rebuilt before a forward when the embedding may have changed
+  void* embed_norm = nullptr;
+  bool embed_norm_stale = true;
   void* w_lm = nullptr;
   void* inv_freq = nullptr;
   void* lens_table = nullptr;  // [(max_len + 1)][max_batch] u32
@@ -94,6 +98,7 @@ int ensure_rows(catena_decoder& m, uint64_t rows) {
 
 void release(catena_decoder* m) {
   pool_free(m->embed);
+  pool_free(m->embed_norm);
   pool_free(m->w_lm);
   pool_free(m->inv_freq);
   pool_free(m->lens_table);
@@ -144,12 +149,21 @@ int forward(catena_decoder& m, const uint32_t* tokens, uint32_t batch, uint32_t 
   const float scale = (float)(1.0 / std::sqrt((double)c.head_dim));
   const float* inv = static_cast<const float*>(m.inv_freq);
   const bool step = tq == 1 && batch <= 16;
+  const uint16_t* embed = static_cast<const uint16_t*>(m.embed);
+  if (m.embed_norm_stale) {
+    TRY(embed_norm_table_bf16(embed, c.vocab, static_cast<uint16_t*>(m.embed_norm), d));
+    m.embed_norm_stale = false;
+  }
 
   for (uint32_t l = 0; l < c.n_layers; ++l) {
-    // x_l = h_{l-1} + ffn_{l-1} (layer 0: the embedding), xn = bf16(rmsnorm(x_l))
-    if (l == 0)
-      TRY(embed_rmsnorm_bf16(tokens, static_cast<const uint16_t*>(m.embed), c.vocab, X, XN, rows, d));
-    else
+    // x_l = h_{l-1} + ffn_{l-1} (layer 0: the embedding), xn = bf16(rmsnorm(x_l)).
+    // A decode step's layer 0 reads xn as rows of the normalized embedding
+    // table (the same kernel's bits, computed once per embedding) and x as
+    // the embedding rows themselves: no norm runs for it.
+    const bool gathered = step && l == 0;
+    if (l == 0 && !gathered)
+      TRY(embed_rmsnorm_bf16(tokens, embed, c.vocab, X, XN, rows, d));
+    else if (l > 0)
       TRY(catena_mi355x_residual_rmsnorm_bf16(H, FO, nullptr, X, XN, rows, d));
     uint16_t* kc = static_cast<uint16_t*>(m.kc[l]);
     uint16_t* vc = static_cast<uint16_t*>(m.vc[l]);
@@ -163,7 +177,13 @@ int forward(catena_decoder& m, const uint32_t* tokens, uint32_t batch, uint32_t 
       e.inv_freq = inv;
       e.heads = c.n_heads;
       e.max_len = c.max_len;
-      TRY(gemm_bf16_decode(XN, wqkv, QKV, rows, 3 * d, d, DecodeEpilogue::Rope, e));
+      const uint16_t* xn = XN;
+      if (gathered) {
+        xn = static_cast<const uint16_t*>(m.embed_norm);
+        e.x_rows = tokens;
+        e.x_rows_limit = c.vocab;
+      }
+      TRY(gemm_bf16_decode(xn, wqkv, QKV, rows, 3 * d, d, DecodeEpilogue::Rope, e));
     } else {
       TRY(catena_mi355x_gemm_bf16(XN, wqkv, QKV, rows, 3 * d, d, 1));
       TRY(catena_mi355x_rope_qkv_bf16(QKV, inv, lens, Q, kc, vc, batch, tq, c.n_heads, c.head_dim,
@@ -172,7 +192,10 @@ int forward(catena_decoder& m, const uint32_t* tokens, uint32_t batch, uint32_t 
     TRY(catena_mi355x_attn_causal_bf16(Q, kc, vc, lens, ATT, batch, tq, c.n_heads, c.max_len,
                                        c.head_dim, scale, 0));
     TRY(catena_mi355x_gemm_bf16(ATT, static_cast<const uint16_t*>(m.w_o[l]), AP, rows, d, d, 1));
-    TRY(catena_mi355x_residual_rmsnorm_bf16(X, AP, nullptr, H, HN, rows, d));
+    if (gathered)
+      TRY(embed_residual_rmsnorm_bf16(tokens, embed, c.vocab, AP, H, HN, rows, d));
+    else
+      TRY(catena_mi355x_residual_rmsnorm_bf16(X, AP, nullptr, H, HN, rows, d));
     const uint16_t* wgu = static_cast<const uint16_t*>(m.w_gu[l]);
     if (step) {
       DecodeEpiArgs e;
@@ -253,6 +276,7 @@ int catena_mi355x_decoder_create(const catena_decoder_config_t* cfg, catena_deco
     return s;
   };
   if ((st = alloc((uint64_t)c.vocab * d * 2, &m->embed))) return fail_out(st);
+  if ((st = alloc(((uint64_t)c.vocab + 1) * d * 2, &m->embed_norm))) return fail_out(st);
   if ((st = alloc(d * c.vocab * 2, &m->w_lm))) return fail_out(st);
   try {
     for (auto* v : {&m->w_qkv, &m->w_o, &m->w_gu, &m->w_down, &m->kc, &m->vc}) v->reserve(c.n_layers);
@@ -328,7 +352,13 @@ int catena_mi355x_decoder_tensor(catena_decoder_t* dec, uint32_t which, uint32_t
     return fail(CATENA_ERR_INVALID_ARGUMENT, "layer %u out of range", layer);
   const uint64_t d = m.d, f = m.f;
   switch (which) {
-    case CATENA_DEC_EMBED: *out = {m.embed, (uint64_t)c.vocab * d * 2}; break;
+    case CATENA_DEC_EMBED:
+      // the caller may write the embedding through this: rebuild its
+      // normalized table before the next forward
+      *out = {m.embed, (uint64_t)c.vocab * d * 2};
+      m.embed_norm_stale = true;
+      break;
+    case CATENA_DEC_EMBED_NORM: *out = {m.embed_norm, ((uint64_t)c.vocab + 1) * d * 2}; break;
     case CATENA_DEC_W_QKV: *out = {m.w_qkv[layer], d * 3 * d * 2}; break;
     case CATENA_DEC_W_O: *out = {m.w_o[layer], d * d * 2}; break;
     case CATENA_DEC_W_GU: *out = {m.w_gu[layer], d * 2 * f * 2}; break;
@@ -364,6 +394,9 @@ int catena_mi355x_decoder_init_weights(catena_decoder_t* dec, uint64_t seed, flo
     TRY(catena_mi355x_fill_normal_bf16(static_cast<uint16_t*>(m.w_gu[l]), d * 2 * f, seed, s + 2, std));
     TRY(catena_mi355x_fill_normal_bf16(static_cast<uint16_t*>(m.w_down[l]), f * d, seed, s + 3, std));
   }
+  TRY(embed_norm_table_bf16(static_cast<const uint16_t*>(m.embed), (uint32_t)V,
+                            static_cast<uint16_t*>(m.embed_norm), d));
+  m.embed_norm_stale = false;
   return CATENA_OK;
 }
 

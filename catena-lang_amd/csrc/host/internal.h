@@ -144,6 +144,9 @@ struct DecodeEpiArgs {
   uint32_t* idx = nullptr;
   uint32_t* arg_ticket = nullptr;
   uint32_t* arg_partials = nullptr;
+  // X row m = X[min(x_rows[m], x_rows_limit)] when x_rows is not null
+  const uint32_t* x_rows = nullptr;
+  uint32_t x_rows_limit = 0;
 };
 enum class DecodeEpilogue { StoreF32, StoreBf16, Rope, Silu, Argmax };
 // Decode-shape GEMM (n <= 16) with an epilogue; c is Y (f32, or bf16 for
@@ -173,6 +176,14 @@ bool gemm_bf16_silu_fits(uint64_t n, uint64_t m, uint64_t k, const void* a, cons
 // written to x_out, bf16 output.
 int embed_rmsnorm_bf16(const uint32_t* tokens, const uint16_t* table, uint32_t vocab,
                        float* x_out, uint16_t* y, uint64_t rows, uint64_t n);
+// The same with a residual: h = widen(table[tok]) + resid to h_out, bf16
+// rmsnorm(h) to y.
+int embed_residual_rmsnorm_bf16(const uint32_t* tokens, const uint16_t* table, uint32_t vocab,
+                                const float* resid, float* h_out, uint16_t* y, uint64_t rows,
+                                uint64_t n);
+// bf16 rmsnorm(widen(table[t])) for every t < vocab into y[t], and a row of
+// NaN at y[vocab] (the row of a token out of range).
+int embed_norm_table_bf16(const uint16_t* table, uint32_t vocab, uint16_t* y, uint64_t n);
 
 // Fail-stop used by the program ABI: message on stderr, then trap, like
 // catena_assert / catena_host_gpu_check (catena-lang/src/codegen/prelude.rs:38-55).

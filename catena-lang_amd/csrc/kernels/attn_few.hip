@@ -392,7 +392,7 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* __
   lds_barrier();  // (2) exp~ written
   if (wave == 0) {
     // the one sequential fold den = (((0 + e_0) + e_1) + ...) in ascending t
-    const float den = len >= 1024 ? serial_sum_wave_long(sp, len) : serial_sum_wave(sp, len);
+    const float den = serial_sum_wave_long(sp, len);
     if (lane == 0) *den_slot = den;
   }
   lds_barrier();  // (3) den written

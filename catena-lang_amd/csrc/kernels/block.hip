@@ -78,8 +78,8 @@ extern "C" __global__ __launch_bounds__(256) void catena_embed_rows_bf16(
 
 // One workgroup per output row.  h = x[src] (+ resid[src] when resid is
 // given: one f32 add per element); then nn.rmsnorm of h:
-//   sum_sq = fold_{i asc} from +0 of h_i * h_i   (one wave, serial_sum_wave;
-//            serial_sum_wave_long for n >= 1024: same bits)
+//   sum_sq = fold_{i asc} from +0 of h_i * h_i   (one wave,
+//            serial_sum_wave_long)
 //   rms    = math.sqrt(sum_sq / (f32)n + 0x3727C5AC)
 //   y_i    = h_i / rms
 // src = row_index ? row_index[row] : row.  Outputs (each optional): h_out
@@ -114,7 +114,9 @@ CATENA_DEV void rms_finish_row(const float* hs, uint32_t n, uint64_t row, float 
 }  // namespace
 
 // With tokens given, the input row is the embedding gather
-// widen(table[tokens[src]]) (a token >= vocab gives NaN) instead of x[src].
+// widen(table[tokens[src]]) (a token >= vocab gives NaN) instead of x[src];
+// with a table but neither x nor tokens, it is widen(table[src]) (src >=
+// vocab gives NaN), which builds the normalized table of every token.
 extern "C" __global__ __launch_bounds__(256) void catena_rmsnorm_rows(
     const float* __restrict__ x, const float* __restrict__ resid,
     const uint32_t* __restrict__ row_index, float* __restrict__ h_out,
@@ -129,18 +131,19 @@ extern "C" __global__ __launch_bounds__(256) void catena_rmsnorm_rows(
   const uint64_t src = row_index ? row_index[row] : row;
   uint32_t tok = 0;
   bool tok_ok = true;
-  if (tokens) {
-    tok = tokens[src];
+  const bool gather = tokens || (!x && table);
+  if (gather) {
+    tok = tokens ? tokens[src] : (uint32_t)src;
     tok_ok = tok < vocab;
   }
   const float nan = __uint_as_float(kNaNBits);
   if (n % 4 == 0) {
     const f32x4_t* x4 = reinterpret_cast<const f32x4_t*>(x + src * n);
     const f32x4_t* r4 = resid ? reinterpret_cast<const f32x4_t*>(resid + src * n) : nullptr;
-    const uint2* e4 = tokens ? reinterpret_cast<const uint2*>(table + (uint64_t)tok * n) : nullptr;
+    const uint2* e4 = gather ? reinterpret_cast<const uint2*>(table + (uint64_t)tok * n) : nullptr;
     for (uint32_t i = threadIdx.x; i < n / 4; i += 256) {
       f32x4_t h;
-      if (tokens) {
+      if (gather) {
         if (tok_ok) {
           const uint2 w = e4[i];
           h = f32x4_t{bf16lo(w.x), bf16hi(w.x), bf16lo(w.y), bf16hi(w.y)};
@@ -165,7 +168,7 @@ extern "C" __global__ __launch_bounds__(256) void catena_rmsnorm_rows(
   } else {
     for (uint32_t i = threadIdx.x; i < n; i += 256) {
       float h;
-      if (tokens)
+      if (gather)
         h = tok_ok ? bf16_to_f32(table[(uint64_t)tok * n + i]) : nan;
       else
         h = x[src * n + i];
@@ -177,7 +180,7 @@ extern "C" __global__ __launch_bounds__(256) void catena_rmsnorm_rows(
   }
   __syncthreads();
   if (threadIdx.x < 64) {
-    const float sum_sq = n >= 1024 ? serial_sum_wave_long(sq, n) : serial_sum_wave(sq, n);
+    const float sum_sq = serial_sum_wave_long(sq, n);
     if (threadIdx.x == 0) {
       const float len_f = (float)(uint64_t)n;
       const float mean_sq = sum_sq / len_f;

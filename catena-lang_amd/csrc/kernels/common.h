@@ -275,51 +275,52 @@ CATENA_DEV float serial_sum_wave(const float* s, uint32_t n) {
   return acc;
 }
 
-// The same fold for long rows (n >= 1024, e.g. nn.rmsnorm over a model
-// width): each 2048-value chunk is held by 16 lanes, lane L (< 16) holding
-// values 128L .. 128L+127, and the running sum moves one lane up with DPP
-// row_shr:1 (inside lanes 0..15) instead of through a scalar register: 16
-// hand-overs per chunk instead of 64.  Slots past n hold +0: the running sum
-// starts at +0 and never becomes -0 (x + (-x) rounds to +0), so adding +0
-// leaves it unchanged and the bits equal serial_sum_wave's.
+// The same fold held by fewer lanes with shorter hand-offs (any n; s in
+// LDS): each 2048-value chunk is held by 16 lanes, lane L (< 16) holding
+// values 128L .. 128L+127 in registers, and the running sum moves one lane
+// up with DPP row_shr:1 (inside lanes 0..15) instead of through a scalar
+// register; a chunk shorter than 2048 stops after its last lane holding
+// values.  Every 16-byte chunk is loaded from an address inside [0, n) and
+// replaced by +0 past the data (no per-element guarded loads), and the
+// n % 4 values past the last whole chunk are added last, in order, by the
+// whole wave.  Slots past the data hold +0: the running sum starts at +0
+// and never becomes -0 (x + (-x) rounds to +0), so adding +0 leaves it
+// unchanged and the bits equal serial_sum_wave's.  s not 16-byte aligned:
+// serial_sum_wave.
 CATENA_DEV float serial_sum_wave_long(const float* s, uint32_t n) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  if ((reinterpret_cast<uintptr_t>(s) & 15u) != 0) return serial_sum_wave(s, n);
   const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t n4 = n & ~3u;  // values in whole 16-byte chunks
   float acc = __uint_as_float(0u);
-  for (uint32_t base = 0; base < n; base += 2048) {
+  for (uint32_t base = 0; base < n4; base += 2048) {
     const uint32_t lo = base + 128 * (lane & 15u);
     float v[128];
-    if (lane >= 16) {
-      // lanes 16..63 never add (the chain stays in lanes 0..15)
 #pragma unroll
-      for (int k = 0; k < 128; ++k) v[k] = __uint_as_float(0u);
-    } else if (lo + 128 <= n && (reinterpret_cast<uintptr_t>(s + lo) & 15u) == 0) {
-      typedef float f4 __attribute__((ext_vector_type(4)));
+    for (int i = 0; i < 32; ++i) {
+      const uint32_t e = lo + 4 * i;
+      const bool in = lane < 16u && e < n4;  // the whole chunk lies in [0, n4)
+      const f4 q = *reinterpret_cast<const f4*>(s + (in ? e : 0u));
 #pragma unroll
-      for (int i = 0; i < 32; ++i) {
-        const f4 e = *reinterpret_cast<const f4*>(s + lo + 4 * i);
-        v[4 * i + 0] = e[0];
-        v[4 * i + 1] = e[1];
-        v[4 * i + 2] = e[2];
-        v[4 * i + 3] = e[3];
-      }
-    } else {
-#pragma unroll
-      for (int k = 0; k < 128; ++k) v[k] = lo + k < n ? s[lo + k] : __uint_as_float(0u);
+      for (int j = 0; j < 4; ++j) v[4 * i + j] = in ? q[j] : __uint_as_float(0u);
     }
-    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_s_waitcnt(0);  // every load landed: no wait inside the chain
+    const uint32_t left = n4 - base;
+    const uint32_t nl = left >= 2048u ? 16u : (left + 127u) / 128u;
     float a = acc;
 #pragma unroll 1
-    for (uint32_t L = 0; L < 16; ++L) {
+    for (uint32_t L = 0; L < nl; ++L) {
       if (lane == L) {
 #pragma unroll
         for (int k = 0; k < 128; ++k) a = a + v[k];
       }
-      if (L < 15)
+      if (L + 1 < nl)
         a = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(a), __float_as_int(a), 0x111, 0xF, 0xF,
                                                        false));
     }
-    acc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 15));
+    acc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), (int)(nl - 1)));
   }
+  for (uint32_t t = n4; t < n; ++t) acc = acc + s[t];
   return acc;
 }
 

@@ -155,6 +155,10 @@ struct DecodeEpi {
   uint32_t* idx;            // [M]
   uint32_t* arg_ticket;     // one counter, zero between launches
   uint32_t* arg_partials;   // [M][gridDim.x][4]: last NaN, max value, max index, pad
+  // row m of X is X[min(x_rows[m], x_rows_limit)] when x_rows is given (a
+  // gather from a table whose row x_rows_limit is the out-of-range row)
+  const uint32_t* x_rows;
+  uint32_t x_rows_limit;
 };
 
 template <int EPI>
@@ -216,8 +220,13 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
     // per read instead of 4)
     const uint32_t xr = lane >> 2, xq = (uint32_t)(lane & 3) ^ ((xr >> 1) & 3u);
     const bool xl = xr < M;
+    uint32_t xrow = xr;
+    if (ep.x_rows && xl) {
+      xrow = ep.x_rows[xr];
+      if (xrow > ep.x_rows_limit) xrow = ep.x_rows_limit;
+    }
     const char* wsrc = reinterpret_cast<const char*>(W) + (kw0 * N + n0) * 2;
-    const char* xsrc = reinterpret_cast<const char*>(X) + ((uint64_t)xr * K + kw0 + 8 * xq) * 2;
+    const char* xsrc = reinterpret_cast<const char*>(X) + ((uint64_t)xrow * K + kw0 + 8 * xq) * 2;
     auto issue = [&](uint32_t t, int slot) {  // slab t of this wave = k kw0 + 128 t
       unsigned char* st = ring + slot * STAGE_BYTES;
       const char* w = wsrc + (uint64_t)t * 128 * N * 2;
@@ -275,8 +284,13 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
       }
     }
   } else {
-    const int xrow = lane & 15;
-    const bool xlive = xrow < (int)M;
+    const int xr16 = lane & 15;
+    const bool xlive = xr16 < (int)M;
+    uint64_t xrow = (uint64_t)xr16;
+    if (ep.x_rows && xlive) {
+      xrow = ep.x_rows[xr16];
+      if (xrow > ep.x_rows_limit) xrow = ep.x_rows_limit;
+    }
     if (kbeg < kend) {
       u32x4_t cur[8], nxt[8];
       load_w(W, K, N, kbeg, col, g, cur);
@@ -285,7 +299,7 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
         if (more) load_w(W, K, N, k0 + 32, col, g, nxt);
         const uint64_t xk = k0 + 8 * g;
         u32x4_t xa = u32x4_t{0u, 0u, 0u, 0u};
-        if (xlive && xk < K) xa = *reinterpret_cast<const u32x4_t*>(X + (uint64_t)xrow * K + xk);
+        if (xlive && xk < K) xa = *reinterpret_cast<const u32x4_t*>(X + xrow * K + xk);
         u32x4_t bt[8];
         transpose8x8(cur, bt);
         const bf16x8_t af = as_bf16x8(xa);

@@ -379,6 +379,13 @@ typedef enum catena_decoder_tensor {
   CATENA_DEC_FINAL_XN,  /* [batch][d] bf16 */
   CATENA_DEC_LOGITS,    /* [batch][vocab] f32 */
   CATENA_DEC_LENS,      /* [batch] u32: cache positions per sequence */
+  /* [vocab + 1][d] bf16: bf16(rmsnorm(widen(embed[t]))) for every token t,
+   * row vocab all NaN (the row of a token out of range); rebuilt before the
+   * next forward whenever the embedding may have changed (a
+   * decoder_tensor(CATENA_DEC_EMBED) call, init_weights).  A decode step
+   * gathers layer 0's normalized input from it, so in a decode step layer
+   * 0 writes neither CATENA_DEC_X nor CATENA_DEC_XN. */
+  CATENA_DEC_EMBED_NORM,
   CATENA_DEC_TENSOR_COUNT
 } catena_decoder_tensor_t;
 

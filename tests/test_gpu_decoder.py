@@ -66,10 +66,19 @@ def _check_forward(dec, cfg, w, tokens, tq, cache_len):
     lay = cfg.layers - 1
     lens = np.full(B, cache_len, np.int64)
     rd = lambda which, dt, shape: dec.read(which, dt, layer=lay).reshape(shape)  # noqa: E731
-    X = rd(ca.DEC_X, np.float32, (R, d))
-    if lay == 0:
-        _bitwise(X, as_f32(w["embed"][np.asarray(tokens, np.int64).ravel()]))
-    XN = rd(ca.DEC_XN, np.uint16, (R, d))
+    toks = np.asarray(tokens, np.int64).ravel()
+    if lay == 0 and tq == 1:
+        # a decode step gathers layer 0's normalized rows from the table of
+        # normalized embedding rows (row V: the out-of-range row) and reads x
+        # as the embedding rows: it writes neither X nor XN
+        X = as_f32(w["embed"][toks])
+        tab = dec.read(ca.DEC_EMBED_NORM, np.uint16).reshape(cfg.V + 1, d)
+        XN = tab[np.minimum(toks, cfg.V)]
+    else:
+        X = rd(ca.DEC_X, np.float32, (R, d))
+        if lay == 0:
+            _bitwise(X, as_f32(w["embed"][toks]))
+        XN = rd(ca.DEC_XN, np.uint16, (R, d))
     _bitwise(XN, od.residual_rmsnorm_bf16(X)[1])
     QKV = rd(ca.DEC_QKV, np.float32, (R, 3 * d))
     gemm_within_bound(XN, w["w_qkv"][lay], QKV)
@@ -145,6 +154,42 @@ def test_decoder_stagewise_prefill_and_steps():
     buf = ca.Buffer(cfg.B * 4 * (steps_left + 1))
     with pytest.raises(ca.CatenaError):
         dec.generate(steps_left + 1, buf)
+    dec.close()
+
+
+def test_decoder_embed_norm_table_and_rebuild():
+    """The table of normalized embedding rows that a decode step gathers
+    layer 0's input from: every row bitwise the oracle's rmsnorm of the
+    widened embedding row, row V all NaN; after the embedding is rewritten
+    through decoder_tensor, the next forward rebuilds it, and the decode
+    step then checks stage by stage against the new weights."""
+    cfg = Tiny
+    dec = ca.Decoder(cfg.d, cfg.H, cfg.F, cfg.layers, cfg.V, cfg.B, cfg.L)
+    dec.init_weights(seed=9, std=0.02)
+    say("normalized embedding table after init_weights")
+    tab = dec.read(ca.DEC_EMBED_NORM, np.uint16).reshape(cfg.V + 1, cfg.d)
+    emb = dec.read(ca.DEC_EMBED, np.uint16).reshape(cfg.V, cfg.d)
+    _bitwise(tab[:cfg.V], od.residual_rmsnorm_bf16(as_f32(emb))[1])
+    assert np.isnan(as_f32(tab[cfg.V])).all()
+    # a new embedding (rows of very different scales) written through the
+    # tensor handle
+    rng = np.random.default_rng(19)
+    new = oracle.f32_to_bf16_bits_np(
+        (rng.normal(0, 1, (cfg.V, cfg.d)) * np.exp(rng.normal(0, 3, (cfg.V, 1)))).astype(np.float32))
+    ca.mem_write(dec.tensor(ca.DEC_EMBED), new)
+    w = _weights(dec, cfg)
+    assert np.array_equal(w["embed"], new)
+    tokens = rng.integers(0, cfg.V, (cfg.B, cfg.T)).astype(np.uint32)
+    nxt = ca.Buffer(cfg.B * 4)
+    say("prefill and one step after rewriting the embedding")
+    dec.prefill(ca.Buffer.from_array(tokens), cfg.B, cfg.T, nxt)
+    tab = dec.read(ca.DEC_EMBED_NORM, np.uint16).reshape(cfg.V + 1, cfg.d)
+    _bitwise(tab[:cfg.V], od.residual_rmsnorm_bf16(as_f32(new))[1])
+    prev = nxt.read(np.uint32)
+    out = ca.Buffer(cfg.B * 4)
+    dec.generate(1, out)
+    want = _check_forward(dec, cfg, w, prev, 1, cfg.T + 1)
+    assert np.array_equal(out.read(np.uint32), want)
     dec.close()
 
 
