@@ -85,7 +85,7 @@ int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, 
   Device& d = device();
   const uint32_t M = (uint32_t)n;
   // streaming ring (4 waves x 4 stages x 9 KiB) when K % 32 == 0, else the
-  // register path with the reduction buffers only (3 x 8 KiB partials + the
+  // register path with the reduction buffers only (4 x 8 KiB wave sums + the
   // 16 x 132 f32 tile)
   const bool regs_path = k % 32 != 0;
   const uint32_t kw = decode_kw(m, k, regs_path);
@@ -148,7 +148,7 @@ int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, 
   uint64_t N = m, K = k;
   uint32_t* tickets = d.gemm_tickets();
   uint32_t stream_lds = regs_path ? 0u : 1u;
-  const size_t lds = stream_lds ? 4 * 4 * 9216 : 3 * 8 * 64 * 16 + 16 * 132 * 4;
+  const size_t lds = stream_lds ? 4 * 4 * 9216 : 4 * 8 * 64 * 16 + 16 * 132 * 4;
   void* args[] = {&X, &W, &Y, &P, &tickets, (void*)&M, &N, &K, (void*)&kw, &stream_lds, &e};
   if (lds > d.max_lds) return fail(CATENA_ERR_UNSUPPORTED, "decode GEMM needs %zu B of LDS", lds);
   return launch(id, dim3((unsigned)gx, (unsigned)S), dim3(256), lds, args);

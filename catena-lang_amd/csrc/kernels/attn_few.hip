@@ -159,7 +159,10 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* __
     // batch bt -> slot bt % VRING: 8 direct-to-LDS loads of 1 KiB (8 rows x
     // 128 bytes; lane l: row l / 8, chunk l % 8).  In the last batch rows
     // past len read row 0 instead (in bounds, never folded), so every batch
-    // is exactly 8 loads and the waits below are exact.
+    // is exactly 8 loads and the waits below are exact.  V is read with the
+    // non-temporal hint (cache policy nt): in the C5 decode step that keeps
+    // more of the weights in the Infinity Cache and measured 19.1 -> 18.6 us
+    // for this kernel.
     const uint32_t vr = (uint32_t)lane >> 3, vc = (uint32_t)lane & 7u;
     const uint16_t* vlane = vb + (uint64_t)vr * D + colbase + 8 * vc;
     auto issue = [&](uint32_t bt) {
@@ -168,14 +171,14 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* __
         const uint16_t* src = vlane + (uint64_t)bt * VB_ROWS * D;
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-          __builtin_amdgcn_global_load_lds(src + 8 * i * D, (lds_void*)(slot + 1024 * i), 16, 0, 0);
+          __builtin_amdgcn_global_load_lds(src + 8 * i * D, (lds_void*)(slot + 1024 * i), 16, 0, 2);
       } else {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           uint32_t t = bt * VB_ROWS + 8 * i + vr;
           if (t >= len) t = 0;
           __builtin_amdgcn_global_load_lds(vb + (uint64_t)t * D + colbase + 8 * vc,
-                                           (lds_void*)(slot + 1024 * i), 16, 0, 0);
+                                           (lds_void*)(slot + 1024 * i), 16, 0, 2);
         }
       }
     };

@@ -166,11 +166,11 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
                             void* __restrict__ Y, float* __restrict__ P,
                             uint32_t* __restrict__ tickets, uint32_t M, uint64_t N, uint64_t K,
                             uint32_t KW, uint32_t stream_lds, const DecodeEpi& ep) {
-  // Dynamic LDS: the streaming ring, reused after the k loop for the
-  // partials of waves 1..3 (red[3][8][64]) and the output tile.
+  // Dynamic LDS: the streaming ring, reused after the k loop for the four
+  // waves' sums (red[4][8][64]) and the output tile.
   extern __shared__ __attribute__((aligned(1024))) unsigned char dsm[];
   f32x4_t(*red)[8][64] = reinterpret_cast<f32x4_t(*)[8][64]>(dsm);
-  float* tile = reinterpret_cast<float*>(dsm + 3 * 8 * 64 * 16);
+  float* tile = reinterpret_cast<float*>(dsm + 4 * 8 * 64 * 16);
   __shared__ uint32_t last_flag;
   const bool streamed = stream_lds != 0;  // host: only when K % 32 == 0
 
@@ -227,12 +227,18 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
     }
     const char* wsrc = reinterpret_cast<const char*>(W) + (kw0 * N + n0) * 2;
     const char* xsrc = reinterpret_cast<const char*>(X) + ((uint64_t)xrow * K + kw0 + 8 * xq) * 2;
+    // The LM head (argmax epilogue) streams its weight, the largest tensor
+    // of a decode step and read once per step, with the non-temporal hint:
+    // measured in the C5 step, the Infinity Cache then keeps the block
+    // weights and the KV cache between steps (W_qkv 13.7 -> 12.4 us, W_down
+    // 12.0 -> 10.5 us, the LM head itself 31.2 -> 31.6 us).
+    constexpr int kWAux = EPI == EPI_ARGMAX ? 2 : 0;  // cache policy: nt
     auto issue = [&](uint32_t t, int slot) {  // slab t of this wave = k kw0 + 128 t
       unsigned char* st = ring + slot * STAGE_BYTES;
       const char* w = wsrc + (uint64_t)t * 128 * N * 2;
 #pragma unroll
       for (int i = 0; i < 8; ++i)
-        if (wlive[i]) __builtin_amdgcn_global_load_lds(w + woff[i], (lds_void*)(st + 1024 * i), 16, 0, 0);
+        if (wlive[i]) __builtin_amdgcn_global_load_lds(w + woff[i], (lds_void*)(st + 1024 * i), 16, 0, kWAux);
       if (xl) __builtin_amdgcn_global_load_lds(xsrc + (uint64_t)t * 256, (lds_void*)(st + W_SLAB), 16, 0, 0);
     };
     const uint32_t pre = steps < (uint32_t)RING ? steps : (uint32_t)RING;
@@ -316,39 +322,36 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
   // the streaming path's LDS is reused below
   __syncthreads();
 
-  if (wave > 0) {
+  // every wave's sums into LDS; then all threads add the four waves' values
+  // of each f32x4 in wave order, ((w0 + w1) + w2) + w3, into the tile (lane
+  // (G, s) of register j holds rows 4G .. 4G+3 of tile column 16j + s when
+  // streamed, else 8s + j)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) red[wave - 1][j][lane] = acc[j];
+  for (int j = 0; j < 8; ++j) red[wave][j][lane] = acc[j];
+  __syncthreads();
+  for (uint32_t e = tid; e < 8u * 64u; e += 256) {
+    const uint32_t j = e >> 6, ln = e & 63u;
+    f32x4_t v = red[0][j][ln];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) {
+      const f32x4_t o = red[w][j][ln];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = v[q] + o[q];
+    }
+    const uint32_t gg = ln >> 4, sc = ln & 15u;
+    const uint32_t tc = streamed ? 16 * j + sc : 8 * sc + j;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t row = 4 * gg + q;
+      if (row < M) tile[row * TILE_LD + tc] = v[q];
+    }
   }
   __syncthreads();
   const uint32_t S = gridDim.y;
-  if (wave == 0) {
-#pragma unroll
-    for (int w = 0; w < 3; ++w)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        f32x4_t o = red[w][j][lane];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) acc[j][q] = acc[j][q] + o[q];
-      }
-    // lane holds rows 4g+q of tile column tc(j): 16j + c when streamed,
-    // else 8c + j
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t row = 4 * g + q;
-      if (row >= M) continue;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t tc = streamed ? 16 * j + c : 8 * c + j;
-        tile[row * TILE_LD + tc] = acc[j][q];
-      }
-    }
-  }
   if (S > 1) {
     // This workgroup's partial, P[blockIdx.y][m][n0 ..], read by another
     // workgroup: 16-byte stores that bypass the XCD-private caches (sc1), as
     // agent-scope atomics do, from all threads.
-    __syncthreads();
     const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)P, (short)0, (int)(S * (uint64_t)M * N * 4), kRsrcWord3);
     for (uint32_t e = tid; e < M * 32u; e += 256) {
