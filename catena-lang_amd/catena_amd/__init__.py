@@ -123,6 +123,7 @@ SIGNATURES = {
     "catena_pool_trim": (_int, []),
     "catena_mi355x_gemm_f32_exact": (_int, [_vp, _vp, _vp, _u64, _u64, _u64]),
     "catena_mi355x_gemm_bf16": (_int, [_vp, _vp, _vp, _u64, _u64, _u64, _int]),
+    "catena_mi355x_gemm_bf16_argmax": (_int, [_vp, _vp, _vp, _vp, _u64, _u64, _u64]),
     "catena_mi355x_gemm_bf16_decode_plan": (_int, [_u64, _u64, _u64, ctypes.POINTER(_u32),
                                                    ctypes.POINTER(_u64)]),
     "catena_mi355x_gemm_bf16_decode_noalloc": (_int, [_vp, _vp, _vp, _u64, _u64, _u64, _int]),
@@ -308,6 +309,12 @@ def gemm_f32_exact(a, b, c, n: int, m: int, k: int) -> None:
 
 def gemm_bf16(a, b, c, n: int, m: int, k: int, out_f32: bool = False) -> None:
     check(lib().catena_mi355x_gemm_bf16(_p(a), _p(b), _p(c), n, m, k, 1 if out_f32 else 0))
+
+
+def gemm_bf16_argmax(a, b, c, idx, n: int, m: int, k: int) -> None:
+    """LM head: c = a * b (f32, decode shape) and idx[r] = tensor.argmax-f32
+    of row r of c, in one launch."""
+    check(lib().catena_mi355x_gemm_bf16_argmax(_p(a), _p(b), _p(c), _p(idx), n, m, k))
 
 
 def gemm_bf16_decode_noalloc(a, b, c, n: int, m: int, k: int, out_f32: bool = False) -> None:

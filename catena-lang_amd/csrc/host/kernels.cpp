@@ -271,6 +271,17 @@ int catena_mi355x_gemm_bf16_silu(const uint16_t* a, const uint16_t* b, uint16_t*
                 dim3(512), lds, args);
 }
 
+int catena_mi355x_gemm_bf16_argmax(const uint16_t* a, const uint16_t* b, float* c, uint32_t* idx,
+                                   uint64_t n, uint64_t m, uint64_t k) {
+  int st = ensure_init();
+  if (st) return st;
+  if (n == 0 || m == 0) return CATENA_OK;
+  if (!a || !b || !c || !idx) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
+  DecodeEpiArgs e;
+  e.idx = idx;
+  return gemm_bf16_decode(a, b, c, n, m, k, DecodeEpilogue::Argmax, e);
+}
+
 int catena_mi355x_attn_decode_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                    const uint32_t* lens, float* o, uint32_t batch, uint32_t heads,
                                    uint32_t max_len, uint32_t head_dim, float scale) {

@@ -83,48 +83,6 @@ typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) unsigned char lds_u8;
 typedef __attribute__((address_space(3))) f32x4_t lds_f32x4;
 
-// The f32.max-env fold (acc = (acc >= x) ? acc : x from -inf, ascending)
-// returns, without NaNs, the first score equal to the maximum (+0 and -0
-// compare equal, so the earlier of them wins).  max_key orders (score,
-// position) so that the largest key is exactly that score: the score's bits
-// made monotone (with -0 taken as +0) above the complemented position, and
-// the sign bit at the bottom so that the score's exact bits come back
-// (key_score).  0 is below every key (no score).  A NaN resets the fold:
-// the result is then the last NaN if it is the final score, otherwise the
-// first maximum of the scores after the last NaN.
-CATENA_DEV uint32_t mono_bits(uint32_t bits) {
-  const uint32_t canon = bits == 0x80000000u ? 0u : bits;
-  return (canon & 0x80000000u) ? ~canon : (canon | 0x80000000u);
-}
-CATENA_DEV uint64_t make_key(uint32_t mono, uint32_t t, uint32_t bits) {
-  return ((uint64_t)mono << 32) | ((0x7FFFFFFFu - t) << 1) | (bits >> 31);
-}
-CATENA_DEV uint64_t max_key(float v, uint32_t t) {
-  const uint32_t bits = __float_as_uint(v);
-  return make_key(mono_bits(bits), t, bits);
-}
-
-// Maximum over the wave of an unsigned value (0 is the identity): inclusive
-// max scans within rows of 16 lanes (row_shr 1, 2, 4, 8), rows joined
-// through row_bcast 15 and 31, lane 63's result returned uniformly.
-CATENA_DEV uint32_t wave_umax(uint32_t x) {
-#define FEW_DPP_MAX(ctrl, rows) \
-  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, (ctrl), (rows), 0xF, false))
-  FEW_DPP_MAX(0x111, 0xF);
-  FEW_DPP_MAX(0x112, 0xF);
-  FEW_DPP_MAX(0x114, 0xF);
-  FEW_DPP_MAX(0x118, 0xF);
-  FEW_DPP_MAX(0x142, 0xA);
-  FEW_DPP_MAX(0x143, 0xC);
-#undef FEW_DPP_MAX
-  return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
-}
-CATENA_DEV float key_score(uint64_t key) {
-  const uint32_t mono = (uint32_t)(key >> 32);
-  const uint32_t canon = (mono & 0x80000000u) ? (mono & 0x7FFFFFFFu) : ~mono;
-  return __uint_as_float(canon == 0u ? ((uint32_t)key & 1u) << 31 : canon);
-}
-
 template <bool OUT_BF16>
 CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                               const uint16_t* __restrict__ v, const uint32_t* __restrict__ lens,

@@ -391,3 +391,43 @@ CATENA_DEV FirstMax first_max_combine(FirstMax a, FirstMax b) {
   if (b.v > a.v) return b;
   return (a.i < b.i) ? a : b;  // equal (incl. +0/-0): earlier index wins
 }
+
+// The same first maximum as one integer maximum: max_key orders (value,
+// index) so that the largest key over non-NaN values is exactly the value
+// first_max_combine keeps -- the value's bits made monotone (with -0 taken as
+// +0, so equal values compare equal) above the complemented index (the
+// earlier index wins), and the sign bit at the bottom so that the value's
+// exact bits come back (key_score).  0 is below every key (no value).
+// Index < 2^31.
+CATENA_DEV uint32_t mono_bits(uint32_t bits) {
+  const uint32_t canon = bits == 0x80000000u ? 0u : bits;
+  return (canon & 0x80000000u) ? ~canon : (canon | 0x80000000u);
+}
+CATENA_DEV uint64_t make_key(uint32_t mono, uint32_t t, uint32_t bits) {
+  return ((uint64_t)mono << 32) | ((0x7FFFFFFFu - t) << 1) | (bits >> 31);
+}
+CATENA_DEV uint64_t max_key(float v, uint32_t t) {
+  const uint32_t bits = __float_as_uint(v);
+  return make_key(mono_bits(bits), t, bits);
+}
+
+// Maximum over the wave of an unsigned value (0 is the identity): inclusive
+// max scans within rows of 16 lanes (row_shr 1, 2, 4, 8), rows joined
+// through row_bcast 15 and 31, lane 63's result returned uniformly.
+CATENA_DEV uint32_t wave_umax(uint32_t x) {
+#define CATENA_DPP_MAX(ctrl, rows) \
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, (ctrl), (rows), 0xF, false))
+  CATENA_DPP_MAX(0x111, 0xF);
+  CATENA_DPP_MAX(0x112, 0xF);
+  CATENA_DPP_MAX(0x114, 0xF);
+  CATENA_DPP_MAX(0x118, 0xF);
+  CATENA_DPP_MAX(0x142, 0xA);
+  CATENA_DPP_MAX(0x143, 0xC);
+#undef CATENA_DPP_MAX
+  return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+}
+CATENA_DEV float key_score(uint64_t key) {
+  const uint32_t mono = (uint32_t)(key >> 32);
+  const uint32_t canon = (mono & 0x80000000u) ? (mono & 0x7FFFFFFFu) : ~mono;
+  return __uint_as_float(canon == 0u ? ((uint32_t)key & 1u) << 31 : canon);
+}

@@ -77,26 +77,6 @@ CATENA_DEV void load_w(const uint16_t* __restrict__ W, uint64_t K, uint64_t N, u
   }
 }
 
-CATENA_DEV int wave_max_i32(int v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const int o = __shfl_xor(v, off, 64);
-    v = o > v ? o : v;
-  }
-  return v;
-}
-
-CATENA_DEV FirstMax wave_first_max(FirstMax a) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    FirstMax b;
-    b.v = __shfl_xor(a.v, off, 64);
-    b.i = (uint32_t)__shfl_xor((int)a.i, off, 64);
-    a = first_max_combine(a, b);
-  }
-  return a;
-}
-
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
@@ -128,16 +108,6 @@ constexpr int kCpolSc1 = 16;
 #define DEC_WAIT_VMCNT(n) \
   __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | 0x0070 | 0x0F00)
 
-// Composition of argmax chunk summaries in index order: a chunk holding a
-// NaN replaces the state, one without merges its first max into it.
-struct ArgState {
-  int j;
-  FirstMax fm;
-};
-CATENA_DEV ArgState arg_compose(ArgState a, ArgState b) {
-  if (b.j >= 0) return b;
-  return ArgState{a.j, first_max_combine(a.fm, b.fm)};
-}
 }  // namespace
 
 // Extra operands of the fused epilogues (unused fields may be null).
@@ -470,65 +440,93 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
     const uint32_t gx = gridDim.x;
     const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
         (void*)ep.arg_partials, (short)0, (int)((uint64_t)M * gx * 16), kRsrcWord3);
-    // this block's summary per row: columns n0 + lane, n0 + 64 + lane
+    // this block's summary per row (one wave per row; lane l holds columns
+    // n0 + l and n0 + 64 + l): the last NaN from two ballots, then the first
+    // maximum after it as the largest monotone value (DPP max) and the
+    // lowest column holding it (ballots) -- the first_max_combine result
     for (uint32_t r = wave; r < M; r += 4) {
       const float* t = tile + r * TILE_LD;
-      int lastnan = -1;
-#pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        const uint64_t cc = n0 + lane + 64 * h2;
-        if (cc < N && t[lane + 64 * h2] != t[lane + 64 * h2]) lastnan = (int)cc;
+      const float v0 = t[lane], v1 = t[lane + 64];
+      const bool in0 = n0 + lane < N, in1 = n0 + 64 + lane < N;
+      const uint64_t nan0 = __builtin_amdgcn_ballot_w64(in0 && v0 != v0);
+      const uint64_t nan1 = __builtin_amdgcn_ballot_w64(in1 && v1 != v1);
+      int J = -1;
+      if (nan1 != 0u)
+        J = (int)(n0 + 64 + (63u - (uint32_t)__builtin_clzll(nan1)));
+      else if (nan0 != 0u)
+        J = (int)(n0 + (63u - (uint32_t)__builtin_clzll(nan0)));
+      const uint32_t b0 = __float_as_uint(v0), b1 = __float_as_uint(v1);
+      const uint32_t m0 = (in0 && v0 == v0 && (int)(n0 + lane) > J) ? mono_bits(b0) : 0u;
+      const uint32_t m1 = (in1 && v1 == v1 && (int)(n0 + 64 + lane) > J) ? mono_bits(b1) : 0u;
+      const uint32_t m = wave_umax(m0 > m1 ? m0 : m1);
+      uint32_t fv = 0xFF800000u, fi = 0xFFFFFFFFu;  // empty: -inf, no index
+      if (m != 0u) {
+        const uint64_t w0 = __builtin_amdgcn_ballot_w64(m0 == m);
+        if (w0 != 0u) {
+          const int wl = __builtin_ctzll(w0);
+          fv = (uint32_t)__builtin_amdgcn_readlane((int)b0, wl);
+          fi = (uint32_t)(n0 + wl);
+        } else {
+          const int wl = __builtin_ctzll(__builtin_amdgcn_ballot_w64(m1 == m));
+          fv = (uint32_t)__builtin_amdgcn_readlane((int)b1, wl);
+          fi = (uint32_t)(n0 + 64 + wl);
+        }
       }
-      const int J = wave_max_i32(lastnan);
-      FirstMax fm{__uint_as_float(0xFF800000u), 0xFFFFFFFFu};
-#pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        const uint64_t cc = n0 + lane + 64 * h2;
-        if (cc < N && (int)cc > J) fm = first_max_combine(fm, FirstMax{t[lane + 64 * h2], (uint32_t)cc});
-      }
-      fm = wave_first_max(fm);
       if (lane == 0) {
         // one 16-byte summary, stored past the XCD caches (sc1)
-        const u32x4_t v = u32x4_t{(uint32_t)J, __float_as_uint(fm.v), fm.i, 0u};
+        const u32x4_t v = u32x4_t{(uint32_t)J, fv, fi, 0u};
         __builtin_amdgcn_raw_buffer_store_b128(v, ars, (int)(((uint64_t)r * gx + blockIdx.x) * 16), 0,
                                                kCpolSc1);
       }
     }
     if (!last_arrival(ep.arg_ticket, gx, &last_flag)) return;
-    // compose the gx chunk summaries of each row in column order: 16
-    // threads per row take contiguous runs (every summary of a run loaded
-    // in one batch of 16-byte coherent loads), then one composes the 16 runs
-    __shared__ int run_j[16][16];
-    __shared__ float run_v[16][16];
-    __shared__ uint32_t run_i[16][16];
-    const uint32_t r = tid >> 4, sub = tid & 15u;
-    const uint32_t per = (gx + 15) / 16;
-    if (r < M) {
-      ArgState st{-1, FirstMax{__uint_as_float(0xFF800000u), 0xFFFFFFFFu}};
-      const uint32_t c0 = sub * per < gx ? sub * per : gx;
-      const uint32_t c1 = c0 + per < gx ? c0 + per : gx;
-      for (uint32_t cb = c0; cb < c1; cb += 16) {
-        u32x4_t pe[16];
+    // The gx summaries of a row composed in column order (one wave per row,
+    // summaries of blocks lane, lane + 64, ... loaded coherently): the last
+    // NaN J* is the largest J; the answer is the first maximum over the
+    // blocks from J*'s block on, whose summaries hold their first maximum
+    // after their own last NaN (after J* in J*'s block, over the whole block
+    // after it) -- the first maximum as the largest (monotone value,
+    // complemented column) pair -- or J* itself if it is the last column.
+    for (uint32_t r = wave; r < M; r += 4) {
+      uint32_t jm = 0, bm = 0, bl = 0;  // J + 1; best monotone value, its complemented column
+      auto load_sum = [&](uint32_t b) {
+        return b < gx ? __builtin_amdgcn_raw_buffer_load_b128(ars, (int)(((uint64_t)r * gx + b) * 16), 0, kCpolSc1)
+                      : u32x4_t{0xFFFFFFFFu, 0u, 0xFFFFFFFFu, 0u};
+      };
+      auto take = [&](uint32_t b, const u32x4_t& pv, uint32_t bstart) {
+        if (b < gx && b >= bstart && pv[2] != 0xFFFFFFFFu) {
+          const uint32_t mo = mono_bits(pv[1]), lo = (0x7FFFFFFFu - pv[2]) << 1;
+          if (mo > bm || (mo == bm && lo > bl)) {
+            bm = mo;
+            bl = lo;
+          }
+        }
+      };
+      // the first 256 blocks stay in registers between the two passes
+      u32x4_t pe[4];
 #pragma unroll
-        for (int u = 0; u < 16; ++u)
-          if (cb + u < c1)
-            pe[u] = __builtin_amdgcn_raw_buffer_load_b128(ars, (int)(((uint64_t)r * gx + cb + u) * 16), 0,
-                                                         kCpolSc1);
+      for (int u = 0; u < 4; ++u) pe[u] = load_sum((uint32_t)lane + 64u * u);
 #pragma unroll
-        for (int u = 0; u < 16; ++u)
-          if (cb + u < c1)
-            st = arg_compose(st, ArgState{(int)pe[u][0], FirstMax{__uint_as_float(pe[u][1]), pe[u][2]}});
-      }
-      run_j[r][sub] = st.j;
-      run_v[r][sub] = st.fm.v;
-      run_i[r][sub] = st.fm.i;
-    }
-    __syncthreads();
-    if (r < M && sub == 0) {
-      ArgState st{-1, FirstMax{__uint_as_float(0xFF800000u), 0xFFFFFFFFu}};
-      for (int s2 = 0; s2 < 16; ++s2)
-        st = arg_compose(st, ArgState{run_j[r][s2], FirstMax{run_v[r][s2], run_i[r][s2]}});
-      ep.idx[r] = (st.j == (int)N - 1) ? (uint32_t)st.j : st.fm.i;
+      for (int u = 0; u < 4; ++u) jm = pe[u][0] + 1u > jm ? pe[u][0] + 1u : jm;
+      for (uint32_t b0 = 256; b0 < gx; b0 += 256)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const u32x4_t pv = load_sum(b0 + (uint32_t)lane + 64u * u);
+          jm = pv[0] + 1u > jm ? pv[0] + 1u : jm;
+        }
+      const uint32_t J1 = wave_umax(jm);  // J* + 1, 0 when no NaN
+      const uint32_t bstart = J1 ? (J1 - 1) / 128u : 0u;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) take((uint32_t)lane + 64u * u, pe[u], bstart);
+      for (uint32_t b0 = 256; b0 < gx; b0 += 256)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const uint32_t b = b0 + (uint32_t)lane + 64u * u;
+          take(b, load_sum(b), bstart);
+        }
+      const uint32_t M_hi = wave_umax(bm);
+      const uint32_t L_lo = wave_umax(bm == M_hi ? bl : 0u);
+      if (lane == 0) ep.idx[r] = (J1 != 0u && J1 == N) ? (uint32_t)(N - 1) : 0x7FFFFFFFu - (L_lo >> 1);
     }
   }
 }

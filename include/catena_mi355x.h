@@ -141,6 +141,16 @@ int catena_mi355x_gemm_bf16_decode_plan(uint64_t n, uint64_t m, uint64_t k, uint
 int catena_mi355x_gemm_bf16_decode_noalloc(const uint16_t *a, const uint16_t *b, void *c,
                                            uint64_t n, uint64_t m, uint64_t k, int out_f32);
 
+/* LM head of a decode step in one launch: c = a * b as the decode shape of
+ * catena_mi355x_gemm_bf16 computes it (f32 c[n][m]), and idx[r] =
+ * tensor.argmax-f32 of row r of c (catena-lang/stdlib/tensor.hex:204-227:
+ * the first maximum after the last NaN, or the last NaN when it is the
+ * final element).  1 <= n <= 16, m % 8 == 0, k % 8 == 0, k > 0, m < 2^31,
+ * n * ceil(m / 128) <= 57,344 (the per-block summaries' buffer); 16-byte
+ * aligned a, b, c.  No reference counterpart (the decoder's greedy step). */
+int catena_mi355x_gemm_bf16_argmax(const uint16_t *a, const uint16_t *b, float *c, uint32_t *idx,
+                                   uint64_t n, uint64_t m, uint64_t k);
+
 /* Decode attention, one query per (batch, head): q[B][H][D], k/v[B][H][L][D]
  * bf16, lens[B] (device u32, each <= L), o[B][H][D] f32.  Bitwise the
  * sequential composition of cell-dot, nn.softmax and cell-dot

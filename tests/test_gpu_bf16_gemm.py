@@ -21,7 +21,7 @@ import pytest
 
 import catena_amd as ca
 import oracle
-from gpu_util import U, as_f32, bf16_ulp_diff, bf16_ulp_of, dev_normal_bf16, hash_bits, say
+from gpu_util import U, as_f32, bf16_ulp_diff, bf16_ulp_of, dev_normal_bf16, gemm_within_bound, hash_bits, say
 
 pytestmark = pytest.mark.gpu
 
@@ -319,3 +319,67 @@ def test_gemm_swiglu_special_values():
     assert np.array_equal(g16, w16), int(np.sum(g16 != w16))
     g = gu.read(np.float32, (n, m))
     assert np.isnan(g[3]).all() and not np.isfinite(g[5]).all() and np.isnan(g[9, 64:128]).all()
+
+
+def _lm_head_case(x16, w16, n, m, k):
+    """The fused LM head (catena_mi355x_gemm_bf16_argmax): its logits within
+    the GEMM bound where finite, and every index equal to the oracle's
+    tensor.argmax-f32 of the GPU's own logits row."""
+    xb, wb = ca.Buffer.from_array(x16), ca.Buffer.from_array(w16)
+    c = ca.Buffer(n * m * 4)
+    idx = ca.Buffer(n * 4)
+    ca.gemm_bf16_argmax(xb, wb, c, idx, n, m, k)
+    logits = c.read(np.float32, (n, m))
+    got = idx.read(np.uint32)
+    want = [oracle.argmax_f32(logits[r]) for r in range(n)]
+    assert list(got) == want, (list(got), want)
+    return logits, got
+
+
+def test_lm_head_argmax_nan_tie_and_zero_patterns():
+    """Logit patterns for the per-block summaries and their composition
+    across 128-column blocks (ragged last block): an exact tie between two
+    blocks (duplicated weight columns: the earlier wins), NaN columns at a
+    block boundary with the maximum after them, NaN in the last column (the
+    answer), every logit +0 or -0, and rows with different maxima."""
+    n, k = 8, 256
+    m = 128 * 20 + 64
+    rng = np.random.default_rng(23)
+    x = rng.normal(0, 1, (n, k)).astype(np.float32)
+    w = rng.normal(0, 0.05, (k, m)).astype(np.float32)
+    w[:, 1000] = w[:, 400] = rng.normal(0, 1, k).astype(np.float32)  # the same dominant column twice
+    x16 = oracle.f32_to_bf16_bits_np(x)
+
+    say("LM head argmax: tie across blocks")
+    w16 = oracle.f32_to_bf16_bits_np(w)
+    logits, got = _lm_head_case(x16, w16, n, m, k)
+    gemm_within_bound(x16, w16, logits)
+    assert 1000 not in got  # its twin, column 400, comes first
+
+    say("LM head argmax: NaN at a block boundary, the maximum after it")
+    wn = w.copy()
+    wn[3, 127] = wn[5, 128] = np.nan
+    wn[:, 2000] = 4 * w[:, 1000]
+    _lm_head_case(x16, oracle.f32_to_bf16_bits_np(wn), n, m, k)
+
+    say("LM head argmax: NaN in the last column")
+    wl = w.copy()
+    wl[7, m - 1] = np.nan
+    wl[7, 130] = np.nan
+    _, got = _lm_head_case(x16, oracle.f32_to_bf16_bits_np(wl), n, m, k)
+    assert list(got) == [m - 1] * n
+
+    say("LM head argmax: all logits zero")
+    wz = np.zeros((k, m), np.float32)
+    _, got = _lm_head_case(x16, oracle.f32_to_bf16_bits_np(wz), n, m, k)
+
+    say("LM head argmax: 8 x 32000 x 2048 against the plain GEMM")
+    a, b, a16, b16 = _inputs(8, 32000, 2048, 29)
+    c = ca.Buffer(8 * 32000 * 4)
+    idx = ca.Buffer(8 * 4)
+    ca.gemm_bf16_argmax(a, b, c, idx, 8, 32000, 2048)
+    plain = ca.Buffer(8 * 32000 * 4)
+    ca.gemm_bf16(a, b, plain, 8, 32000, 2048, out_f32=True)
+    lg = c.read(np.float32, (8, 32000))
+    assert np.array_equal(lg.view(np.uint32), plain.read(np.float32, (8, 32000)).view(np.uint32))
+    assert list(idx.read(np.uint32)) == [oracle.argmax_f32(lg[r]) for r in range(8)]
