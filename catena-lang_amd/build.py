@@ -91,6 +91,13 @@ def build(jobs: int = 8) -> list[str]:
     if not os.path.exists(HIPCC):
         raise RuntimeError(f"hipcc not found at {HIPCC}")
     os.makedirs(OUT, exist_ok=True)
+    # The library goes first and comes back only when everything built: the
+    # host passes structs by value that the kernels read with their own
+    # layout, so an old library beside new code objects (or the reverse)
+    # must never be loadable.
+    lib = os.path.join(OUT, LIB_NAME)
+    if os.path.exists(lib):
+        os.remove(lib)
     srcs = sorted(glob.glob(os.path.join(KDIR, "*.hip")))
     # code objects whose source is gone would otherwise linger in lib/
     live = {os.path.splitext(os.path.basename(s))[0] for s in srcs}
@@ -100,7 +107,14 @@ def build(jobs: int = 8) -> list[str]:
     with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         futs = [ex.submit(build_kernel, s) for s in srcs]
         futs.append(ex.submit(build_host))
-        return [f.result() for f in futs]
+        try:
+            return [f.result() for f in futs]
+        except Exception:
+            for f in futs:
+                f.exception()  # wait for the rest before removing anything
+            if os.path.exists(lib):
+                os.remove(lib)
+            raise
 
 
 def main(argv=None) -> int:

@@ -66,6 +66,16 @@ int embed_norm_table_bf16(const uint16_t* table, uint32_t vocab, uint16_t* y, ui
   return rmsnorm_launch(nullptr, nullptr, nullptr, nullptr, nullptr, y, (uint64_t)vocab + 1, n, nullptr,
                         table, vocab);
 }
+
+int rope_table_f32(const float* inv_freq, float* tab, uint32_t positions, uint32_t half) {
+  int st = ensure_init();
+  if (st) return st;
+  if (!inv_freq || !tab) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
+  if (positions == 0 || half == 0) return CATENA_OK;
+  if (positions > 65535) return fail(CATENA_ERR_UNSUPPORTED, "rope table of %u positions", positions);
+  void* args[] = {&inv_freq, &tab, &positions, &half};
+  return launch(KernelId::RopeTable, dim3((unsigned)ceil_div(half, 256), positions), dim3(256), 0, args);
+}
 }  // namespace catena
 
 extern "C" {

@@ -31,6 +31,7 @@ struct catena_decoder {
   bool embed_norm_stale = true;
   void* w_lm = nullptr;
   void* inv_freq = nullptr;
+  void* rope_tab = nullptr;  // [max_len][head_dim / 2][2] f32: (cos, sin) per position and pair
   void* lens_table = nullptr;  // [(max_len + 1)][max_batch] u32
   std::vector<void*> w_qkv, w_o, w_gu, w_down, kc, vc;
   // activations (capacity rows_cap rows) and per-sequence buffers
@@ -101,6 +102,7 @@ void release(catena_decoder* m) {
   pool_free(m->embed_norm);
   pool_free(m->w_lm);
   pool_free(m->inv_freq);
+  pool_free(m->rope_tab);
   pool_free(m->lens_table);
   for (auto* v : {&m->w_qkv, &m->w_o, &m->w_gu, &m->w_down, &m->kc, &m->vc})
     for (void* p : *v) pool_free(p);
@@ -175,6 +177,7 @@ int forward(catena_decoder& m, const uint32_t* tokens, uint32_t batch, uint32_t 
       e.v_cache = vc;
       e.lens = lens;
       e.inv_freq = inv;
+      e.rope_tab = static_cast<const float*>(m.rope_tab);
       e.heads = c.n_heads;
       e.max_len = c.max_len;
       const uint16_t* xn = XN;
@@ -326,6 +329,12 @@ int catena_mi355x_decoder_create(const catena_decoder_config_t* cfg, catena_deco
     for (uint32_t b = 0; b < c.max_batch; ++b) lt[t * c.max_batch + b] = (uint32_t)t;
   if ((st = alloc(lt.size() * 4, &m->lens_table))) return fail_out(st);
   if ((st = catena_mem_write(catena_mem_t{m->inv_freq, inv.size() * 4}, 0, inv.data(), inv.size() * 4)))
+    return fail_out(st);
+  // the decode step's RoPE reads its rotations from a table of every
+  // position (computed by the same functions, so the same bits)
+  if ((st = alloc((uint64_t)c.max_len * c.head_dim * 4, &m->rope_tab))) return fail_out(st);
+  if ((st = rope_table_f32(static_cast<const float*>(m->inv_freq), static_cast<float*>(m->rope_tab),
+                           c.max_len, c.head_dim / 2)))
     return fail_out(st);
   if ((st = catena_mem_write(catena_mem_t{m->lens_table, lt.size() * 4}, 0, lt.data(), lt.size() * 4)))
     return fail_out(st);

@@ -77,6 +77,7 @@ const KernelSpec kKernels[] = {
     {KernelId::EmbedRowsBf16, "block", "catena_embed_rows_bf16"},
     {KernelId::RmsnormRows, "block", "catena_rmsnorm_rows"},
     {KernelId::RopeQkvStore, "block", "catena_rope_qkv_store"},
+    {KernelId::RopeTable, "block", "catena_rope_table"},
     {KernelId::SiluMulBf16, "block", "catena_silu_mul_bf16"},
     {KernelId::ArgmaxRowsF32, "block", "catena_argmax_rows_f32"},
     {KernelId::BroadcastF32, "tensor", "catena_broadcast_f32"},

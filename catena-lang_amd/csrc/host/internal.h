@@ -39,6 +39,7 @@ enum class KernelId : int {
   EmbedRowsBf16,
   RmsnormRows,
   RopeQkvStore,
+  RopeTable,
   SiluMulBf16,
   ArgmaxRowsF32,
   BroadcastF32,
@@ -147,6 +148,9 @@ struct DecodeEpiArgs {
   // X row m = X[min(x_rows[m], x_rows_limit)] when x_rows is not null
   const uint32_t* x_rows = nullptr;
   uint32_t x_rows_limit = 0;
+  // Rope: (cos, sin) of every (position, pair) when not null
+  // ([max_len][64][2] f32, rope_table_f32), else computed
+  const float* rope_tab = nullptr;
 };
 enum class DecodeEpilogue { StoreF32, StoreBf16, Rope, Silu, Argmax };
 // Decode-shape GEMM (n <= 16) with an epilogue; c is Y (f32, or bf16 for
@@ -184,6 +188,9 @@ int embed_residual_rmsnorm_bf16(const uint32_t* tokens, const uint16_t* table, u
 // bf16 rmsnorm(widen(table[t])) for every t < vocab into y[t], and a row of
 // NaN at y[vocab] (the row of a token out of range).
 int embed_norm_table_bf16(const uint16_t* table, uint32_t vocab, uint16_t* y, uint64_t n);
+// tab[pos][i] = (cos, sin) of (f32)pos * inv_freq[i] for pos < positions,
+// i < half, as the RoPE kernels compute them.
+int rope_table_f32(const float* inv_freq, float* tab, uint32_t positions, uint32_t half);
 
 // Fail-stop used by the program ABI: message on stderr, then trap, like
 // catena_assert / catena_host_gpu_check (catena-lang/src/codegen/prelude.rs:38-55).

@@ -246,6 +246,22 @@ extern "C" __global__ __launch_bounds__(256) void catena_rope_qkv_store(
   vc[cache + i + half] = (uint16_t)f32_to_bf16_bits(src[2 * HD + i + half]);
 }
 
+// The rotation pairs of every position: tab[pos][i] = (cos_full(theta),
+// sin_full(theta)) with theta = (f32)pos * inv_freq[i], the values
+// catena_rope_qkv_store computes for that position (a table of them gives
+// the same bits).  One thread per (pos, i); grid = (ceil(half / 256),
+// positions).
+extern "C" __global__ __launch_bounds__(256) void catena_rope_table(
+    const float* __restrict__ inv_freq, float* __restrict__ tab, uint32_t positions, uint32_t half) {
+  const uint32_t pos = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= half) return;
+  const uint64_t id = (uint64_t)pos * half + i;
+  const float pf = (float)pos;
+  const float theta = pf * inv_freq[i];
+  tab[2 * id] = cos_full(theta);
+  tab[2 * id + 1] = sin_full(theta);
+}
+
 // SwiGLU gate: gu[R][2F] f32 -> out[R][F] = bf16(nn.silu(gate) * up).
 // group = 0: gate columns [0, F), up columns [F, 2F); group = G: columns
 // interleaved in groups of G (gate 0..G-1, up 0..G-1, gate G..2G-1, ...).

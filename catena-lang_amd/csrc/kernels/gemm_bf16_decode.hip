@@ -129,6 +129,9 @@ struct DecodeEpi {
   // gather from a table whose row x_rows_limit is the out-of-range row)
   const uint32_t* x_rows;
   uint32_t x_rows_limit;
+  // EPI_ROPE: (cos, sin) of every (position, pair), [max_len][64][2], when
+  // given (the values cos_full / sin_full give, so the same bits)
+  const float* rope_tab;
 };
 
 template <int EPI>
@@ -407,10 +410,17 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
         }
         continue;
       }
-      const float pf = (float)pos;
-      const float theta = pf * ep.inv_freq[i];
-      const float cs = cos_full(theta);
-      const float sn = sin_full(theta);
+      float cs, sn;
+      if (ep.rope_tab) {
+        const float2 cp = reinterpret_cast<const float2*>(ep.rope_tab)[(uint64_t)pos * 64 + i];
+        cs = cp.x;
+        sn = cp.y;
+      } else {
+        const float pf = (float)pos;
+        const float theta = pf * ep.inv_freq[i];
+        cs = cos_full(theta);
+        sn = sin_full(theta);
+      }
       const float x1 = t[i], x2 = t[i + 64];
       const float t1 = x1 * cs, t2 = x2 * sn, t3 = x2 * cs, t4 = x1 * sn;
       const float y1 = t1 - t2, y2 = t3 + t4;
