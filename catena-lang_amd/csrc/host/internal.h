@@ -157,10 +157,13 @@ enum class DecodeEpilogue { StoreF32, StoreBf16, Rope, Silu, Argmax };
 // StoreBf16).  Rope: m = 3 * heads * 128, one token per row; Silu: gate / up
 // interleaved in 64-column groups, act[n][m/2]; Argmax: idx[n].  The split-K
 // partials go to `scratch` (scratch_bytes long) when it is not NULL, else to
-// the library's pool-backed workspace.
+// the library's pool-backed workspace.  whole_k: every workgroup streams the
+// whole K of its column block (no k groups, partials or ticket), for weights
+// that stay in the Infinity Cache between calls, where the hand-off costs
+// more than spreading K over more CUs gains (K % 32 == 0 only).
 int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, uint64_t m,
                      uint64_t k, DecodeEpilogue epi, const DecodeEpiArgs& ep,
-                     void* scratch = nullptr, uint64_t scratch_bytes = 0);
+                     void* scratch = nullptr, uint64_t scratch_bytes = 0, bool whole_k = false);
 // Bytes of split-K partials the decode GEMM needs for an (n x k) * (k x m)
 // product (0 when K is not split), and its number of k groups; a function of
 // the shape alone.

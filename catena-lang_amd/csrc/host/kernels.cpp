@@ -75,7 +75,7 @@ uint64_t decode_partials_bytes(uint64_t n, uint64_t m, uint64_t k, uint32_t* k_g
 
 int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, uint64_t m,
                      uint64_t k, DecodeEpilogue epi, const DecodeEpiArgs& ep, void* scratch,
-                     uint64_t scratch_bytes) {
+                     uint64_t scratch_bytes, bool whole_k) {
   int st = ensure_init();
   if (st) return st;
   if (n == 0 || m == 0) return CATENA_OK;
@@ -88,7 +88,8 @@ int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, 
   // register path with the reduction buffers only (4 x 8 KiB wave sums + the
   // 16 x 132 f32 tile)
   const bool regs_path = k % 32 != 0;
-  const uint32_t kw = decode_kw(m, k, regs_path);
+  const uint32_t kw =
+      whole_k && !regs_path ? (uint32_t)(ceil_div(ceil_div(k, 4), 32) * 32) : decode_kw(m, k, regs_path);
   const uint64_t chunks = ceil_div(k, kw);
   const uint64_t S = ceil_div(chunks, 4);
   const uint64_t gx = ceil_div(m, 128);

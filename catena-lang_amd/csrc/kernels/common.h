@@ -275,16 +275,20 @@ CATENA_DEV float serial_sum_wave(const float* s, uint32_t n) {
   return acc;
 }
 
-// The same fold held by fewer lanes with shorter hand-offs (any n; s in
-// LDS): each 2048-value chunk is held by 16 lanes, lane L (< 16) holding
-// values 128L .. 128L+127 in registers, and the running sum moves one lane
-// up with DPP row_shr:1 (inside lanes 0..15) instead of through a scalar
-// register; a chunk shorter than 2048 stops after its last lane holding
-// values.  Every 16-byte chunk is loaded from an address inside [0, n) and
-// replaced by +0 past the data (no per-element guarded loads), and the
-// n % 4 values past the last whole chunk are added last, in order, by the
-// whole wave.  Slots past the data hold +0: the running sum starts at +0
-// and never becomes -0 (x + (-x) rounds to +0), so adding +0 leaves it
+// The same fold with the running sum handed from lane to lane inside the
+// vector unit (any n; s in LDS): each 2048-value chunk is held by the wave,
+// lane L holding values 32L .. 32L+31 in registers.  Step L: every lane adds
+// its own 32 values, in order, to the sum its left neighbour held after step
+// L - 1 (lane 0 at step 0: the running sum), read through the first add's
+// DPP source operand (wave_shr:1); only lane L's result is the fold's, the
+// other lanes' are discarded.  No lane is masked off, so the chain carries
+// no exec-mask updates, branches or scalar round trips: one dependent
+// v_add_f32 per value (~4.5 cycles).  A chunk shorter than 2048 stops after
+// its last lane holding values.  Every 16-byte chunk is loaded from an
+// address inside [0, n) and replaced by +0 past the data, and the n % 4
+// values past the last whole chunk are added last, in order, by the whole
+// wave.  Slots past the data hold +0: the running sum starts at +0 and
+// never becomes -0 (x + (-x) rounds to +0), so adding +0 leaves it
 // unchanged and the bits equal serial_sum_wave's.  s not 16-byte aligned:
 // serial_sum_wave.
 CATENA_DEV float serial_sum_wave_long(const float* s, uint32_t n) {
@@ -294,29 +298,42 @@ CATENA_DEV float serial_sum_wave_long(const float* s, uint32_t n) {
   const uint32_t n4 = n & ~3u;  // values in whole 16-byte chunks
   float acc = __uint_as_float(0u);
   for (uint32_t base = 0; base < n4; base += 2048) {
-    const uint32_t lo = base + 128 * (lane & 15u);
-    float v[128];
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      const uint32_t e = lo + 4 * i;
-      const bool in = lane < 16u && e < n4;  // the whole chunk lies in [0, n4)
-      const f4 q = *reinterpret_cast<const f4*>(s + (in ? e : 0u));
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[4 * i + j] = in ? q[j] : __uint_as_float(0u);
-    }
-    __builtin_amdgcn_s_waitcnt(0);  // every load landed: no wait inside the chain
     const uint32_t left = n4 - base;
-    const uint32_t nl = left >= 2048u ? 16u : (left + 127u) / 128u;
-    float a = acc;
-#pragma unroll 1
-    for (uint32_t L = 0; L < nl; ++L) {
-      if (lane == L) {
+    const uint32_t lo = base + 32 * lane;
+    float v[32];
+    if (left >= 2048u) {
 #pragma unroll
-        for (int k = 0; k < 128; ++k) a = a + v[k];
+      for (int i = 0; i < 8; ++i) {
+        const f4 q = *reinterpret_cast<const f4*>(s + lo + 4 * i);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[4 * i + j] = q[j];
       }
-      if (L + 1 < nl)
-        a = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(a), __float_as_int(a), 0x111, 0xF, 0xF,
-                                                       false));
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t e = lo + 4 * i;
+        const bool in = e < n4;  // the whole chunk lies in [0, n4)
+        const f4 q = *reinterpret_cast<const f4*>(s + (in ? e : 0u));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[4 * i + j] = in ? q[j] : __uint_as_float(0u);
+      }
+    }
+    // every load is issued and has landed before the chain starts, so no
+    // wait sits inside it
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t nl = left >= 2048u ? 64u : (left + 31u) / 32u;
+    float a = acc;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) a = a + v[k];
+#pragma unroll 1
+    for (uint32_t L = 1; L < nl; ++L) {
+      // a DPP read of a VGPR needs two wait states after the VALU write of
+      // it; across the loop's back edge only the branch separates them
+      asm volatile("s_nop 1");
+      a = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x138, 0xF, 0xF, true)) + v[0];
+#pragma unroll
+      for (int k = 1; k < 32; ++k) a = a + v[k];
     }
     acc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), (int)(nl - 1)));
   }

@@ -385,6 +385,14 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
       o.x = pack_bf16x2(t[0], t[1]);
       o.y = pack_bf16x2(t[2], t[3]);
       *reinterpret_cast<uint2*>(static_cast<uint16_t*>(Y) + (uint64_t)row * N + cc) = o;
+    } else if (EPI == EPI_ARGMAX) {
+      // the logits go past the XCD cache (sc1), so the completion ticket's
+      // release below has no dirty lines of them to write back
+      const __amdgpu_buffer_rsrc_t yrs =
+          __builtin_amdgcn_make_buffer_rsrc(Y, (short)0, (int)((uint64_t)M * N * 4), kRsrcWord3);
+      const u32x4_t v = u32x4_t{__float_as_uint(t[0]), __float_as_uint(t[1]), __float_as_uint(t[2]),
+                                __float_as_uint(t[3])};
+      __builtin_amdgcn_raw_buffer_store_b128(v, yrs, (int)(((uint64_t)row * N + cc) * 4), 0, kCpolSc1);
     } else {
       *reinterpret_cast<f32x4_t*>(static_cast<float*>(Y) + (uint64_t)row * N + cc) =
           f32x4_t{t[0], t[1], t[2], t[3]};
@@ -450,43 +458,45 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
     const uint32_t gx = gridDim.x;
     const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
         (void*)ep.arg_partials, (short)0, (int)((uint64_t)M * gx * 16), kRsrcWord3);
-    // this block's summary per row (one wave per row; lane l holds columns
-    // n0 + l and n0 + 64 + l): the last NaN from two ballots, then the first
-    // maximum after it as the largest monotone value (DPP max) and the
-    // lowest column holding it (ballots) -- the first_max_combine result
-    for (uint32_t r = wave; r < M; r += 4) {
+    // this block's summary of row r (lane l holds columns n0 + l and
+    // n0 + 64 + l): the last NaN from two ballots, then the first maximum
+    // after it as the largest monotone value (DPP max; every value that is
+    // not NaN has a nonzero one) and the lowest column holding it (ballots)
+    // -- the first_max_combine result.  Branch-free, so a wave's two rows
+    // (r, r + 4) run as one straight sequence whose ballots, DPP steps and
+    // readlanes overlap.
+    auto summary = [&](uint32_t r) -> u32x4_t {
       const float* t = tile + r * TILE_LD;
       const float v0 = t[lane], v1 = t[lane + 64];
       const bool in0 = n0 + lane < N, in1 = n0 + 64 + lane < N;
       const uint64_t nan0 = __builtin_amdgcn_ballot_w64(in0 && v0 != v0);
       const uint64_t nan1 = __builtin_amdgcn_ballot_w64(in1 && v1 != v1);
-      int J = -1;
-      if (nan1 != 0u)
-        J = (int)(n0 + 64 + (63u - (uint32_t)__builtin_clzll(nan1)));
-      else if (nan0 != 0u)
-        J = (int)(n0 + (63u - (uint32_t)__builtin_clzll(nan0)));
+      const int J = nan1 != 0u   ? (int)(n0 + 64 + (63u - (uint32_t)__builtin_clzll(nan1)))
+                    : nan0 != 0u ? (int)(n0 + (63u - (uint32_t)__builtin_clzll(nan0)))
+                                 : -1;
       const uint32_t b0 = __float_as_uint(v0), b1 = __float_as_uint(v1);
       const uint32_t m0 = (in0 && v0 == v0 && (int)(n0 + lane) > J) ? mono_bits(b0) : 0u;
       const uint32_t m1 = (in1 && v1 == v1 && (int)(n0 + 64 + lane) > J) ? mono_bits(b1) : 0u;
       const uint32_t m = wave_umax(m0 > m1 ? m0 : m1);
-      uint32_t fv = 0xFF800000u, fi = 0xFFFFFFFFu;  // empty: -inf, no index
-      if (m != 0u) {
-        const uint64_t w0 = __builtin_amdgcn_ballot_w64(m0 == m);
-        if (w0 != 0u) {
-          const int wl = __builtin_ctzll(w0);
-          fv = (uint32_t)__builtin_amdgcn_readlane((int)b0, wl);
-          fi = (uint32_t)(n0 + wl);
-        } else {
-          const int wl = __builtin_ctzll(__builtin_amdgcn_ballot_w64(m1 == m));
-          fv = (uint32_t)__builtin_amdgcn_readlane((int)b1, wl);
-          fi = (uint32_t)(n0 + 64 + wl);
-        }
-      }
+      const uint64_t w0 = __builtin_amdgcn_ballot_w64(m != 0u && m0 == m);
+      const uint64_t w1 = __builtin_amdgcn_ballot_w64(m != 0u && m1 == m);
+      const int wl = w0 != 0u ? __builtin_ctzll(w0) : w1 != 0u ? __builtin_ctzll(w1) : 0;
+      const uint32_t fb = (uint32_t)__builtin_amdgcn_readlane((int)(w0 != 0u ? b0 : b1), wl);
+      // empty (no value after the last NaN): -inf, no index
+      const uint32_t fv = m != 0u ? fb : 0xFF800000u;
+      const uint32_t fi = m == 0u ? 0xFFFFFFFFu : (uint32_t)(n0 + (w0 != 0u ? 0u : 64u) + (uint32_t)wl);
+      return u32x4_t{(uint32_t)J, fv, fi, 0u};
+    };
+    for (uint32_t r = wave; r < M; r += 8) {
+      const bool two = r + 4 < M;
+      const u32x4_t sa = summary(r), sb = summary(two ? r + 4 : r);
       if (lane == 0) {
-        // one 16-byte summary, stored past the XCD caches (sc1)
-        const u32x4_t v = u32x4_t{(uint32_t)J, fv, fi, 0u};
-        __builtin_amdgcn_raw_buffer_store_b128(v, ars, (int)(((uint64_t)r * gx + blockIdx.x) * 16), 0,
+        // 16-byte summaries, stored past the XCD caches (sc1)
+        __builtin_amdgcn_raw_buffer_store_b128(sa, ars, (int)(((uint64_t)r * gx + blockIdx.x) * 16), 0,
                                                kCpolSc1);
+        if (two)
+          __builtin_amdgcn_raw_buffer_store_b128(sb, ars, (int)(((uint64_t)(r + 4) * gx + blockIdx.x) * 16),
+                                                 0, kCpolSc1);
       }
     }
     if (!last_arrival(ep.arg_ticket, gx, &last_flag)) return;
@@ -497,12 +507,13 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
     // after their own last NaN (after J* in J*'s block, over the whole block
     // after it) -- the first maximum as the largest (monotone value,
     // complemented column) pair -- or J* itself if it is the last column.
-    for (uint32_t r = wave; r < M; r += 4) {
+    auto load_sum = [&](uint32_t r, uint32_t b) {
+      return b < gx ? __builtin_amdgcn_raw_buffer_load_b128(ars, (int)(((uint64_t)r * gx + b) * 16), 0, kCpolSc1)
+                    : u32x4_t{0xFFFFFFFFu, 0u, 0xFFFFFFFFu, 0u};
+    };
+    // pe: the row's first 256 summaries, kept in registers between passes
+    auto compose = [&](uint32_t r, const u32x4_t (&pe)[4]) {
       uint32_t jm = 0, bm = 0, bl = 0;  // J + 1; best monotone value, its complemented column
-      auto load_sum = [&](uint32_t b) {
-        return b < gx ? __builtin_amdgcn_raw_buffer_load_b128(ars, (int)(((uint64_t)r * gx + b) * 16), 0, kCpolSc1)
-                      : u32x4_t{0xFFFFFFFFu, 0u, 0xFFFFFFFFu, 0u};
-      };
       auto take = [&](uint32_t b, const u32x4_t& pv, uint32_t bstart) {
         if (b < gx && b >= bstart && pv[2] != 0xFFFFFFFFu) {
           const uint32_t mo = mono_bits(pv[1]), lo = (0x7FFFFFFFu - pv[2]) << 1;
@@ -512,16 +523,12 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
           }
         }
       };
-      // the first 256 blocks stay in registers between the two passes
-      u32x4_t pe[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) pe[u] = load_sum((uint32_t)lane + 64u * u);
 #pragma unroll
       for (int u = 0; u < 4; ++u) jm = pe[u][0] + 1u > jm ? pe[u][0] + 1u : jm;
       for (uint32_t b0 = 256; b0 < gx; b0 += 256)
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-          const u32x4_t pv = load_sum(b0 + (uint32_t)lane + 64u * u);
+          const u32x4_t pv = load_sum(r, b0 + (uint32_t)lane + 64u * u);
           jm = pv[0] + 1u > jm ? pv[0] + 1u : jm;
         }
       const uint32_t J1 = wave_umax(jm);  // J* + 1, 0 when no NaN
@@ -532,11 +539,22 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const uint32_t b = b0 + (uint32_t)lane + 64u * u;
-          take(b, load_sum(b), bstart);
+          take(b, load_sum(r, b), bstart);
         }
       const uint32_t M_hi = wave_umax(bm);
       const uint32_t L_lo = wave_umax(bm == M_hi ? bl : 0u);
       if (lane == 0) ep.idx[r] = (J1 != 0u && J1 == N) ? (uint32_t)(N - 1) : 0x7FFFFFFFu - (L_lo >> 1);
+    };
+    for (uint32_t r = wave; r < M; r += 8) {
+      // both rows' summary loads are in flight together
+      const bool two = r + 4 < M;
+      u32x4_t pa[4], pb[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) pa[u] = load_sum(r, (uint32_t)lane + 64u * u);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) pb[u] = load_sum(two ? r + 4 : r, (uint32_t)lane + 64u * u);
+      compose(r, pa);
+      if (two) compose(r + 4, pb);
     }
   }
 }
