@@ -17,7 +17,8 @@ uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 int rmsnorm_launch(const float* x, const float* resid, const uint32_t* row_index, float* h_out,
                    float* y_f32, uint16_t* y_bf16, uint64_t rows, uint64_t n,
                    const uint32_t* tokens = nullptr, const uint16_t* table = nullptr,
-                   uint32_t vocab = 0) {
+                   uint32_t vocab = 0, uint32_t resid_parts = 1, uint64_t resid_stride = 0,
+                   float* resid_out = nullptr) {
   int st = ensure_init();
   if (st) return st;
   if (rows == 0 || n == 0) return CATENA_OK;
@@ -29,7 +30,7 @@ int rmsnorm_launch(const float* x, const float* resid, const uint32_t* row_index
   if (rows > 0x7FFFFFFFull || n > 0xFFFFFFFFull)
     return fail(CATENA_ERR_UNSUPPORTED, "rmsnorm shape too large");
   if (n % 4 == 0) {
-    const void* ptrs[] = {x, resid, h_out, y_f32};
+    const void* ptrs[] = {x, resid, h_out, y_f32, resid_out};
     for (const void* p : ptrs)
       if (p && !aligned16(p))
         return fail(CATENA_ERR_INVALID_ARGUMENT, "rmsnorm rows must be 16-byte aligned");
@@ -41,8 +42,11 @@ int rmsnorm_launch(const float* x, const float* resid, const uint32_t* row_index
   if (rmsnorm_lds_bytes(n) > device().max_lds)
     return fail(CATENA_ERR_UNSUPPORTED, "rmsnorm row of %llu needs %zu B of LDS",
                 (unsigned long long)n, rmsnorm_lds_bytes(n));
+  if (resid_parts == 0 || (resid_parts > 1 && (!resid || (n % 4 == 0 && resid_stride % 4 != 0))))
+    return fail(CATENA_ERR_INVALID_ARGUMENT, "rmsnorm residual partials");
   uint32_t n32 = (uint32_t)n;
-  void* args[] = {&x, &resid, &row_index, &h_out, &y_f32, &y_bf16, &n32, &tokens, &table, &vocab};
+  void* args[] = {&x,      &resid, &row_index, &h_out,       &y_f32,       &y_bf16,   &n32,
+                  &tokens, &table, &vocab,     &resid_parts, &resid_stride, &resid_out};
   return launch(KernelId::RmsnormRows, dim3((unsigned)rows), dim3(256), lds, args);
 }
 }  // namespace
@@ -56,9 +60,18 @@ int embed_rmsnorm_bf16(const uint32_t* tokens, const uint16_t* table, uint32_t v
 
 int embed_residual_rmsnorm_bf16(const uint32_t* tokens, const uint16_t* table, uint32_t vocab,
                                 const float* resid, float* h_out, uint16_t* y, uint64_t rows,
-                                uint64_t n) {
+                                uint64_t n, uint32_t resid_parts, float* resid_out) {
   if (!tokens || !resid || !y) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
-  return rmsnorm_launch(nullptr, resid, nullptr, h_out, nullptr, y, rows, n, tokens, table, vocab);
+  return rmsnorm_launch(nullptr, resid, nullptr, h_out, nullptr, y, rows, n, tokens, table, vocab,
+                        resid_parts, rows * n, resid_out);
+}
+
+int residual_parts_rmsnorm_bf16(const float* x, const float* resid, uint32_t resid_parts,
+                                float* resid_out, const uint32_t* row_index, float* h_out,
+                                uint16_t* y, uint64_t rows, uint64_t resid_rows, uint64_t n) {
+  if (!x || !resid || !y) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
+  return rmsnorm_launch(x, resid, row_index, h_out, nullptr, y, rows, n, nullptr, nullptr, 0,
+                        resid_parts, resid_rows * n, resid_out);
 }
 
 int embed_norm_table_bf16(const uint16_t* table, uint32_t vocab, uint16_t* y, uint64_t n) {

@@ -10,6 +10,7 @@
 // step s + 1 on the device.  Sequence lengths are uniform across the batch,
 // so the per-sequence lengths a step needs are rows of a table uploaded once
 // (lens_table[t][b] = t).
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -32,6 +33,10 @@ struct catena_decoder {
   void* w_lm = nullptr;
   void* inv_freq = nullptr;
   void* rope_tab = nullptr;  // [max_len][head_dim / 2][2] f32: (cos, sin) per position and pair
+  // a decode step's W_o / W_down k-group partials ([S][rows][d] f32), added
+  // by the RMSNorm that consumes the projection
+  void* parts = nullptr;
+  uint64_t parts_bytes = 0;
   void* lens_table = nullptr;  // [(max_len + 1)][max_batch] u32
   std::vector<void*> w_qkv, w_o, w_gu, w_down, kc, vc;
   // activations (capacity rows_cap rows) and per-sequence buffers
@@ -103,6 +108,7 @@ void release(catena_decoder* m) {
   pool_free(m->w_lm);
   pool_free(m->inv_freq);
   pool_free(m->rope_tab);
+  pool_free(m->parts);
   pool_free(m->lens_table);
   for (auto* v : {&m->w_qkv, &m->w_o, &m->w_gu, &m->w_down, &m->kc, &m->vc})
     for (void* p : *v) pool_free(p);
@@ -157,6 +163,7 @@ int forward(catena_decoder& m, const uint32_t* tokens, uint32_t batch, uint32_t 
     m.embed_norm_stale = false;
   }
 
+  uint32_t parts_down = 0;  // k groups of the last W_down partials (decode step)
   for (uint32_t l = 0; l < c.n_layers; ++l) {
     // x_l = h_{l-1} + ffn_{l-1} (layer 0: the embedding), xn = bf16(rmsnorm(x_l)).
     // A decode step's layer 0 reads xn as rows of the normalized embedding
@@ -165,6 +172,10 @@ int forward(catena_decoder& m, const uint32_t* tokens, uint32_t batch, uint32_t 
     const bool gathered = step && l == 0;
     if (l == 0 && !gathered)
       TRY(embed_rmsnorm_bf16(tokens, embed, c.vocab, X, XN, rows, d));
+    else if (l > 0 && step)
+      // the previous layer's W_down arrives as k-group partials
+      TRY(residual_parts_rmsnorm_bf16(H, static_cast<const float*>(m.parts), parts_down, FO, nullptr,
+                                      X, XN, rows, rows, d));
     else if (l > 0)
       TRY(catena_mi355x_residual_rmsnorm_bf16(H, FO, nullptr, X, XN, rows, d));
     uint16_t* kc = static_cast<uint16_t*>(m.kc[l]);
@@ -194,11 +205,21 @@ int forward(catena_decoder& m, const uint32_t* tokens, uint32_t batch, uint32_t 
     }
     TRY(catena_mi355x_attn_causal_bf16(Q, kc, vc, lens, ATT, batch, tq, c.n_heads, c.max_len,
                                        c.head_dim, scale, 0));
-    TRY(catena_mi355x_gemm_bf16(ATT, static_cast<const uint16_t*>(m.w_o[l]), AP, rows, d, d, 1));
-    if (gathered)
-      TRY(embed_residual_rmsnorm_bf16(tokens, embed, c.vocab, AP, H, HN, rows, d));
-    else
+    if (step) {
+      // W_o without its split-K hand-off: the norm below adds the k-group
+      // partials (and writes their sum to AP)
+      uint32_t parts_o = 0;
+      float* P = static_cast<float*>(m.parts);
+      TRY(gemm_bf16_decode_parts(ATT, static_cast<const uint16_t*>(m.w_o[l]), P, m.parts_bytes, rows, d,
+                                 d, &parts_o));
+      if (gathered)
+        TRY(embed_residual_rmsnorm_bf16(tokens, embed, c.vocab, P, H, HN, rows, d, parts_o, AP));
+      else
+        TRY(residual_parts_rmsnorm_bf16(X, P, parts_o, AP, nullptr, H, HN, rows, rows, d));
+    } else {
+      TRY(catena_mi355x_gemm_bf16(ATT, static_cast<const uint16_t*>(m.w_o[l]), AP, rows, d, d, 1));
       TRY(catena_mi355x_residual_rmsnorm_bf16(X, AP, nullptr, H, HN, rows, d));
+    }
     const uint16_t* wgu = static_cast<const uint16_t*>(m.w_gu[l]);
     if (step) {
       DecodeEpiArgs e;
@@ -217,12 +238,22 @@ int forward(catena_decoder& m, const uint32_t* tokens, uint32_t batch, uint32_t 
       TRY(catena_mi355x_gemm_bf16(HN, wgu, GU, rows, 2 * f, d, 1));
       TRY(catena_mi355x_silu_mul_bf16(GU, ACT, rows, (uint32_t)f, 64));
     }
-    TRY(catena_mi355x_gemm_bf16(ACT, static_cast<const uint16_t*>(m.w_down[l]), FO, rows, d, f, 1));
+    if (step)
+      // k-group partials, added by the next norm (the next layer's input
+      // norm or the final norm)
+      TRY(gemm_bf16_decode_parts(ACT, static_cast<const uint16_t*>(m.w_down[l]), static_cast<float*>(m.parts),
+                                 m.parts_bytes, rows, d, f, &parts_down));
+    else
+      TRY(catena_mi355x_gemm_bf16(ACT, static_cast<const uint16_t*>(m.w_down[l]), FO, rows, d, f, 1));
   }
   float* FH = static_cast<float*>(A(CATENA_DEC_FINAL_H));
   uint16_t* FXN = static_cast<uint16_t*>(A(CATENA_DEC_FINAL_XN));
   float* LG = static_cast<float*>(A(CATENA_DEC_LOGITS));
-  TRY(catena_mi355x_residual_rmsnorm_bf16(H, FO, final_rows, FH, FXN, batch, d));
+  if (step)
+    TRY(residual_parts_rmsnorm_bf16(H, static_cast<const float*>(m.parts), parts_down, FO, final_rows, FH,
+                                    FXN, batch, rows, d));
+  else
+    TRY(catena_mi355x_residual_rmsnorm_bf16(H, FO, final_rows, FH, FXN, batch, d));
   const uint16_t* wlm = static_cast<const uint16_t*>(m.w_lm);
   if (batch <= 16) {
     DecodeEpiArgs e;
@@ -343,6 +374,16 @@ int catena_mi355x_decoder_create(const catena_decoder_config_t* cfg, catena_deco
     return fail_out(st);
   if ((st = catena_mem_write(catena_mem_t{m->lens_table, lt.size() * 4}, 0, lt.data(), lt.size() * 4)))
     return fail_out(st);
+  // partials of the decode step's two row-reduced projections: S k groups of
+  // max_batch x d floats for W_o (k = d) and W_down (k = d_ff)
+  {
+    uint32_t s_o = 0, s_down = 0;
+    decode_partials_bytes(c.max_batch, c.d_model, c.d_model, &s_o);
+    decode_partials_bytes(c.max_batch, c.d_model, c.ffn_dim, &s_down);
+    const uint64_t groups = std::max<uint64_t>(1, std::max(s_o, s_down));
+    m->parts_bytes = groups * c.max_batch * c.d_model * 4;
+    if ((st = alloc(m->parts_bytes, &m->parts))) return fail_out(st);
+  }
   *out = m;
   return CATENA_OK;
 }

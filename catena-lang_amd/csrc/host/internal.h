@@ -29,6 +29,7 @@ enum class KernelId : int {
   GemmBf16DecodeRope,
   GemmBf16DecodeSilu,
   GemmBf16DecodeArgmax,
+  GemmBf16DecodeParts,
   AttnDecodeD128,
   AttnFewD128F32,  // eight waves per pair for few pairs (attn_few.hip)
   AttnFewD128Bf16,
@@ -152,7 +153,7 @@ struct DecodeEpiArgs {
   // ([max_len][64][2] f32, rope_table_f32), else computed
   const float* rope_tab = nullptr;
 };
-enum class DecodeEpilogue { StoreF32, StoreBf16, Rope, Silu, Argmax };
+enum class DecodeEpilogue { StoreF32, StoreBf16, Rope, Silu, Argmax, Partials };
 // Decode-shape GEMM (n <= 16) with an epilogue; c is Y (f32, or bf16 for
 // StoreBf16).  Rope: m = 3 * heads * 128, one token per row; Silu: gate / up
 // interleaved in 64-column groups, act[n][m/2]; Argmax: idx[n].  The split-K
@@ -168,6 +169,12 @@ int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, 
 // product (0 when K is not split), and its number of k groups; a function of
 // the shape alone.
 uint64_t decode_partials_bytes(uint64_t n, uint64_t m, uint64_t k, uint32_t* k_groups);
+// The decode GEMM without its split-K hand-off: writes the product's S k-group
+// partials parts[s][n][m] (f32; S = *k_groups, parts[0] = the product when
+// S = 1) for a consumer that adds them in ascending s.  parts_bytes must hold
+// max(S, 1) * n * m floats.
+int gemm_bf16_decode_parts(const uint16_t* a, const uint16_t* b, float* parts, uint64_t parts_bytes,
+                           uint64_t n, uint64_t m, uint64_t k, uint32_t* k_groups);
 // Scratch of the allocation-free decode GEMM (noalloc.hip): its device
 // address, looked up once per device at init (noalloc_setup, with that
 // device current), and its size.
@@ -187,7 +194,14 @@ int embed_rmsnorm_bf16(const uint32_t* tokens, const uint16_t* table, uint32_t v
 // rmsnorm(h) to y.
 int embed_residual_rmsnorm_bf16(const uint32_t* tokens, const uint16_t* table, uint32_t vocab,
                                 const float* resid, float* h_out, uint16_t* y, uint64_t rows,
-                                uint64_t n);
+                                uint64_t n, uint32_t resid_parts = 1, float* resid_out = nullptr);
+// h = x[src] + resid[src] and y = bf16(rmsnorm(h)) where resid arrives as
+// resid_parts k-group partials of resid_rows x n floats each (added in
+// ascending order, the sum also written to resid_out when given); src =
+// row_index ? row_index[row] : row.
+int residual_parts_rmsnorm_bf16(const float* x, const float* resid, uint32_t resid_parts,
+                                float* resid_out, const uint32_t* row_index, float* h_out,
+                                uint16_t* y, uint64_t rows, uint64_t resid_rows, uint64_t n);
 // bf16 rmsnorm(widen(table[t])) for every t < vocab into y[t], and a row of
 // NaN at y[vocab] (the row of a token out of range).
 int embed_norm_table_bf16(const uint16_t* table, uint32_t vocab, uint16_t* y, uint64_t n);

@@ -110,6 +110,9 @@ int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, 
       if (m % 128 != 0 || !e.act) return fail(CATENA_ERR_INVALID_ARGUMENT, "silu epilogue operands");
       id = KernelId::GemmBf16DecodeSilu;
       break;
+    case DecodeEpilogue::Partials:
+      id = KernelId::GemmBf16DecodeParts;
+      break;
     case DecodeEpilogue::Argmax:
       if (!e.idx || m >= 0x7FFFFFFFull) return fail(CATENA_ERR_INVALID_ARGUMENT, "argmax epilogue operands");
       if (n * gx * 16 > Device::kRowPartialBytes)
@@ -153,6 +156,20 @@ int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, 
   void* args[] = {&X, &W, &Y, &P, &tickets, (void*)&M, &N, &K, (void*)&kw, &stream_lds, &e};
   if (lds > d.max_lds) return fail(CATENA_ERR_UNSUPPORTED, "decode GEMM needs %zu B of LDS", lds);
   return launch(id, dim3((unsigned)gx, (unsigned)S), dim3(256), lds, args);
+}
+
+int gemm_bf16_decode_parts(const uint16_t* a, const uint16_t* b, float* parts, uint64_t parts_bytes,
+                           uint64_t n, uint64_t m, uint64_t k, uint32_t* k_groups) {
+  if (!parts || !k_groups) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
+  uint32_t S = 0;
+  decode_partials_bytes(n, m, k, &S);
+  *k_groups = S > 0 ? S : 1;
+  if ((uint64_t)*k_groups * n * m * sizeof(float) > parts_bytes)
+    return fail(CATENA_ERR_UNSUPPORTED, "decode GEMM partials need %llu B",
+                (unsigned long long)((uint64_t)*k_groups * n * m * sizeof(float)));
+  // S > 1: the partials go to P = parts; S = 1: the product goes to Y = parts
+  return gemm_bf16_decode(a, b, parts, n, m, k, DecodeEpilogue::Partials, DecodeEpiArgs(), parts,
+                          parts_bytes);
 }
 
 int attn_few_launch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint32_t* lens,

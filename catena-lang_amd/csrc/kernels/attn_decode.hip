@@ -25,7 +25,7 @@
 // Softmax: the max is the exact parallel form of the sequential fold (see
 // FirstMax in common.h); exp~ is elementwise; the denominator is the one
 // truly sequential fold and runs as one lane-to-lane chain in wave 0
-// (serial_sum_wave); p_t is one correctly rounded division per element.
+// (serial_sum_wave_long); p_t is one correctly rounded division per element.
 // V pass: waves 0 and 1 own 64 output columns each (lane = column) and walk
 // t ascending through 64-row batches staged in LDS, with the next two
 // batches' loads in flight while one is folded; the first batch is requested
@@ -229,7 +229,7 @@ CATENA_DEV void attn_body(const uint16_t* __restrict__ q, const uint16_t* __rest
   __syncthreads();
   if (wave == 0) {
     // The one sequential fold: den = (((0 + e_0) + e_1) + ...) in ascending t.
-    const float den = serial_sum_wave(sp, len);
+    const float den = serial_sum_wave_long(sp, len);
     if (lane == 0) red_v[0] = den;
   }
   __syncthreads();

@@ -83,6 +83,22 @@ typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) unsigned char lds_u8;
 typedef __attribute__((address_space(3))) f32x4_t lds_f32x4;
 
+// Lane j of each 16-lane row broadcast to its row (DPP row_newbcast); j is a
+// constant once the callers' loops are unrolled.
+CATENA_DEV float row_bcast(float x, int j) {
+#define CATENA_ROW_BCAST(J) \
+  case J:                   \
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x150 + J, 0xF, 0xF, false))
+  switch (j) {
+    CATENA_ROW_BCAST(0); CATENA_ROW_BCAST(1); CATENA_ROW_BCAST(2); CATENA_ROW_BCAST(3);
+    CATENA_ROW_BCAST(4); CATENA_ROW_BCAST(5); CATENA_ROW_BCAST(6); CATENA_ROW_BCAST(7);
+    CATENA_ROW_BCAST(8); CATENA_ROW_BCAST(9); CATENA_ROW_BCAST(10); CATENA_ROW_BCAST(11);
+    CATENA_ROW_BCAST(12); CATENA_ROW_BCAST(13); CATENA_ROW_BCAST(14); default: break;
+  }
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x15F, 0xF, 0xF, false));
+#undef CATENA_ROW_BCAST
+}
+
 template <bool OUT_BF16>
 CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                               const uint16_t* __restrict__ v, const uint32_t* __restrict__ lens,
@@ -168,22 +184,24 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* __
     // half a batch (32 rows) into registers: four rows of this lane's
     // column per transposing read (lane 4j + a of a 16-lane group addresses
     // row 4u + j, columns 16g + 4a .. +3, and lane i receives column 16g + i
-    // of rows 4u .. 4u+3), p four at a time.  The bases are opaque 32-bit
-    // LDS addresses so that the eight reads of each kind share one base
-    // register and differ only in their immediate offsets.
+    // of rows 4u .. 4u+3), and p as two vectors holding p of rows 0-15 and
+    // 16-31 of the half in every 16-lane row (lane l: row l % 16), from
+    // which each multiply takes its row's p by a DPP row broadcast -- one LDS
+    // read per 16 positions instead of a 16-byte broadcast read per 4.  The
+    // bases are opaque 32-bit LDS addresses so that the reads of each kind
+    // share one base register and differ only in their immediate offsets.
     const uint32_t tr_off = (4u * (((uint32_t)lane & 15u) >> 2)) * 32u +
                             2u * (16u * ((uint32_t)lane >> 4) + 4u * ((uint32_t)lane & 3u));
-    auto read_half = [&](uint32_t bt, int half, f32x4_t p4[8], i16x4_t v4[8]) {
+    auto read_half = [&](uint32_t bt, int half, float p16[2], i16x4_t v4[8]) {
       uint32_t vbase = ring_off + (bt % VRING) * VB_BYTES + half * 32 * 128 + tr_off;
-      uint32_t pbase = kOffState + (bt * VB_ROWS + half * 32) * 4;
+      uint32_t pbase = kOffState + (bt * VB_ROWS + half * 32 + ((uint32_t)lane & 15u)) * 4;
       asm volatile("" : "+v"(vbase), "+v"(pbase));
       const lds_u8* vp = (const lds_u8*)smem + vbase;
       const lds_u8* pp = (const lds_u8*)smem + pbase;
+      p16[0] = *(const __attribute__((address_space(3))) float*)(pp);
+      p16[1] = *(const __attribute__((address_space(3))) float*)(pp + 64);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        p4[u] = *(const lds_f32x4*)(pp + 16 * u);
-        v4[u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vp + 512 * u));
-      }
+      for (int u = 0; u < 8; ++u) v4[u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vp + 512 * u));
     };
     float acc = __uint_as_float(0u);
     // once a batch's reads are done its slot takes batch bt + VRING; the
@@ -194,20 +212,24 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* __
       asm volatile("" ::: "memory");
       if (bt + VRING < nblk) issue(bt + VRING);
     };
-    // products first (independent of acc), then the t-ascending chain
-    auto fold_regs = [&](const f32x4_t p4[8], const i16x4_t v4[8]) {
+    // products first (independent of acc), then the t-ascending chain; row
+    // 4u + e's p comes from lane (4u + e) % 16 of its 16-lane row
+    auto fold_regs = [&](const float p16[2], const i16x4_t v4[8]) {
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         float prod[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) prod[e] = p4[u][e] * bf16_to_f32((uint16_t)v4[u][e]);
+        for (int e = 0; e < 4; ++e) {
+          const float pv = row_bcast(p16[u >> 2], (4 * u + e) & 15);
+          prod[e] = pv * bf16_to_f32((uint16_t)v4[u][e]);
+        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc = acc + prod[e];
       }
     };
     // full batches: each half is read while the one before it folds
     const uint32_t nfull = len / VB_ROWS;
-    f32x4_t pa[8], pb[8];
+    float pa[2], pb[2];
     i16x4_t va[8], vb8[8];
     if (nfull > 0) {
       wait_batch(0);

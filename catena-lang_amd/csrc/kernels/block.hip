@@ -117,11 +117,16 @@ CATENA_DEV void rms_finish_row(const float* hs, uint32_t n, uint64_t row, float 
 // widen(table[tokens[src]]) (a token >= vocab gives NaN) instead of x[src];
 // with a table but neither x nor tokens, it is widen(table[src]) (src >=
 // vocab gives NaN), which builds the normalized table of every token.
+// resid may come as the k-group partials of the decode GEMM that produced it
+// (resid_parts > 1, part s at resid + s * resid_stride): resid[src] is then
+// ((P0 + P1) + ...) + P(parts-1), the adds that GEMM's own reduction makes.
+// resid[src] (the sum) is written to resid_out[src] when resid_out is given.
 extern "C" __global__ __launch_bounds__(256) void catena_rmsnorm_rows(
     const float* __restrict__ x, const float* __restrict__ resid,
     const uint32_t* __restrict__ row_index, float* __restrict__ h_out,
     float* __restrict__ y_f32, uint16_t* __restrict__ y_bf16, uint32_t n,
-    const uint32_t* __restrict__ tokens, const uint16_t* __restrict__ table, uint32_t vocab) {
+    const uint32_t* __restrict__ tokens, const uint16_t* __restrict__ table, uint32_t vocab,
+    uint32_t resid_parts, uint64_t resid_stride, float* __restrict__ resid_out) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const uint32_t n_pad = (n + 3u) & ~3u;
   float* hs = reinterpret_cast<float*>(smem);  // [n_pad]
@@ -154,7 +159,25 @@ extern "C" __global__ __launch_bounds__(256) void catena_rmsnorm_rows(
         h = x4[i];
       }
       if (r4) {
-        const f32x4_t rr = r4[i];
+        f32x4_t rr = r4[i];
+        if (resid_parts > 1) {
+          // every part's load in flight before the adds (up to 8 at once)
+          const f32x4_t* p4 = reinterpret_cast<const f32x4_t*>(resid + resid_stride + src * n);
+          const uint64_t st4 = resid_stride / 4;
+          for (uint32_t s0 = 1; s0 < resid_parts; s0 += 8) {
+            f32x4_t pp[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+              if (s0 + u < resid_parts) pp[u] = p4[(s0 - 1 + u) * st4 + i];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+              if (s0 + u < resid_parts) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) rr[j] = rr[j] + pp[u][j];
+              }
+          }
+        }
+        if (resid_out) reinterpret_cast<f32x4_t*>(resid_out + src * n)[i] = rr;
 #pragma unroll
         for (int j = 0; j < 4; ++j) h[j] = h[j] + rr[j];
       }
@@ -172,7 +195,12 @@ extern "C" __global__ __launch_bounds__(256) void catena_rmsnorm_rows(
         h = tok_ok ? bf16_to_f32(table[(uint64_t)tok * n + i]) : nan;
       else
         h = x[src * n + i];
-      if (resid) h = h + resid[src * n + i];
+      if (resid) {
+        float rr = resid[src * n + i];
+        for (uint32_t s0 = 1; s0 < resid_parts; ++s0) rr = rr + resid[s0 * resid_stride + src * n + i];
+        if (resid_out) resid_out[src * n + i] = rr;
+        h = h + rr;
+      }
       hs[i] = h;
       sq[i] = h * h;
       if (h_out) h_out[(uint64_t)row * n + i] = h;

@@ -29,6 +29,11 @@
 //               the K/V cache append, exactly as catena_rope_qkv_store
 //   EPI_SILU    SwiGLU with gate / up columns interleaved in groups of 64:
 //               act[m][64*bx + c] = bf16(silu(gate) * up), as catena_silu_mul_bf16
+//   EPI_PARTIALS  no hand-off: with S > 1 every workgroup stores its partial
+//               P[s] and ends, and the kernel that consumes Y adds P[0] ..
+//               P[S-1] in ascending s itself (the same adds, so the same
+//               bits); the launch boundary orders the partials before that
+//               kernel reads them.  With S = 1 it is EPI_STORE.
 //   EPI_ARGMAX  LM head: per row, (last NaN, first max) of the block's 128
 //               logits as one 16-byte summary, then a second ticket over the
 //               column blocks; the last block composes them in column order:
@@ -48,7 +53,7 @@ namespace {
 constexpr int COLS_PER_WAVE = 128;
 constexpr int TILE_LD = 132;  // f32 row stride of the LDS output tile
 
-enum Epi : int { EPI_STORE = 0, EPI_STORE_BF16 = 1, EPI_ROPE = 2, EPI_SILU = 3, EPI_ARGMAX = 4 };
+enum Epi : int { EPI_STORE = 0, EPI_STORE_BF16 = 1, EPI_ROPE = 2, EPI_SILU = 3, EPI_ARGMAX = 4, EPI_PARTIALS = 5 };
 
 CATENA_DEV bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
 
@@ -337,6 +342,7 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
             v, prs, (int)((((uint64_t)blockIdx.y * M + row) * N + n0 + c4) * 4), 0, kCpolSc1);
       }
     }
+    if (EPI == EPI_PARTIALS) return;
     if (!last_arrival(&tickets[blockIdx.x], S, &last_flag)) return;
     // Last k group of this column block: P[0] + P[1] + ... + P[S-1],
     // ascending s, for the block's M rows x 128 columns; every partial's
@@ -574,3 +580,4 @@ CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_bf16out, EPI_STORE_BF16)
 CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_rope, EPI_ROPE)
 CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_silu, EPI_SILU)
 CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_argmax, EPI_ARGMAX)
+CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_parts, EPI_PARTIALS)
