@@ -37,6 +37,9 @@ struct catena_decoder {
   // by the RMSNorm that consumes the projection
   void* parts = nullptr;
   uint64_t parts_bytes = 0;
+  // the generate loop's deferred LM-head argmax: per-column-block summaries
+  // ([max_batch][ceil(vocab / 128)][4] u32) composed by the next step
+  void* arg_sums = nullptr;
   void* lens_table = nullptr;  // [(max_len + 1)][max_batch] u32
   std::vector<void*> w_qkv, w_o, w_gu, w_down, kc, vc;
   // activations (capacity rows_cap rows) and per-sequence buffers
@@ -109,6 +112,7 @@ void release(catena_decoder* m) {
   pool_free(m->inv_freq);
   pool_free(m->rope_tab);
   pool_free(m->parts);
+  pool_free(m->arg_sums);
   pool_free(m->lens_table);
   for (auto* v : {&m->w_qkv, &m->w_o, &m->w_gu, &m->w_down, &m->kc, &m->vc})
     for (void* p : *v) pool_free(p);
@@ -138,7 +142,8 @@ void release(catena_decoder* m) {
 // cache append after W_qkv, the SwiGLU gate after W_gu, greedy argmax after
 // W_lm; the embedding gather is fused into the first RMSNorm in both cases.
 int forward(catena_decoder& m, const uint32_t* tokens, uint32_t batch, uint32_t tq,
-            const uint32_t* lens, const uint32_t* final_rows, uint32_t* next) {
+            const uint32_t* lens, const uint32_t* final_rows, uint32_t* next,
+            const uint32_t* in_sums = nullptr, bool defer_argmax = false) {
   const catena_decoder_config_t& c = m.cfg;
   const uint64_t rows = (uint64_t)batch * tq, d = m.d, f = m.f;
   TRY(ensure_rows(m, rows));
@@ -194,8 +199,17 @@ int forward(catena_decoder& m, const uint32_t* tokens, uint32_t batch, uint32_t 
       const uint16_t* xn = XN;
       if (gathered) {
         xn = static_cast<const uint16_t*>(m.embed_norm);
-        e.x_rows = tokens;
         e.x_rows_limit = c.vocab;
+        if (in_sums) {
+          // the tokens are the previous step's deferred argmax: composed
+          // here from its summaries and written to `tokens` for the norm
+          e.x_sums = in_sums;
+          e.x_sums_blocks = (uint32_t)((c.vocab + 127) / 128);
+          e.x_sums_cols = c.vocab;
+          e.x_rows_out = const_cast<uint32_t*>(tokens);
+        } else {
+          e.x_rows = tokens;
+        }
       }
       TRY(gemm_bf16_decode(xn, wqkv, QKV, rows, 3 * d, d, DecodeEpilogue::Rope, e));
     } else {
@@ -257,7 +271,14 @@ int forward(catena_decoder& m, const uint32_t* tokens, uint32_t batch, uint32_t 
   const uint16_t* wlm = static_cast<const uint16_t*>(m.w_lm);
   if (batch <= 16) {
     DecodeEpiArgs e;
-    e.idx = next;
+    if (defer_argmax) {
+      // logits and column-block summaries only; the next step's W_qkv (or
+      // argmax_compose after the last step) composes the argmax
+      e.arg_defer = 1;
+      e.arg_partials = static_cast<uint32_t*>(m.arg_sums);
+    } else {
+      e.idx = next;
+    }
     TRY(gemm_bf16_decode(FXN, wlm, LG, batch, c.vocab, d, DecodeEpilogue::Argmax, e));
   } else {
     TRY(catena_mi355x_gemm_bf16(FXN, wlm, LG, batch, c.vocab, d, 1));
@@ -384,6 +405,7 @@ int catena_mi355x_decoder_create(const catena_decoder_config_t* cfg, catena_deco
     m->parts_bytes = groups * c.max_batch * c.d_model * 4;
     if ((st = alloc(m->parts_bytes, &m->parts))) return fail_out(st);
   }
+  if ((st = alloc((uint64_t)c.max_batch * ((c.vocab + 127) / 128) * 16, &m->arg_sums))) return fail_out(st);
   *out = m;
   return CATENA_OK;
 }
@@ -497,14 +519,23 @@ int catena_mi355x_decoder_generate(catena_decoder_t* dec, uint32_t steps, uint32
                 steps, m.cur_len, c.max_len);
   if (steps == 0) return CATENA_OK;
   const uint32_t B = m.batch;
+  // Each step's argmax is composed by the next step's first GEMM, from the
+  // LM head's column-block summaries (the LM head then ends without its
+  // completion ticket); the last step's by argmax_compose.  Decode steps
+  // whose first GEMM streams (d % 32 == 0) and whose LM head is the decode
+  // GEMM (batch <= 16) only.
+  const bool defer = B <= 16 && m.d % 32 == 0;
+  const uint32_t* sums = static_cast<const uint32_t*>(m.arg_sums);
   for (uint32_t s = 0; s < steps; ++s) {
     const uint32_t* in = s == 0 ? static_cast<const uint32_t*>(m.cur_tok) : out + (uint64_t)(s - 1) * B;
     const uint32_t* lens =
         static_cast<const uint32_t*>(m.lens_table) + (uint64_t)(m.cur_len + 1) * c.max_batch;
     m.last_rows = B;
-    TRY(forward(m, in, B, 1, lens, nullptr, out + (uint64_t)s * B));
+    TRY(forward(m, in, B, 1, lens, nullptr, out + (uint64_t)s * B, defer && s > 0 ? sums : nullptr, defer));
     m.cur_len += 1;
   }
+  if (defer)
+    TRY(argmax_compose(sums, B, (uint32_t)((c.vocab + 127) / 128), c.vocab, out + (uint64_t)(steps - 1) * B));
   Device& dv = device();
   const uint32_t* lens = static_cast<const uint32_t*>(m.lens_table) + (uint64_t)m.cur_len * c.max_batch;
   TRY(hip_check(hipMemcpyAsync(m.act[CATENA_DEC_LENS], lens, B * 4, hipMemcpyDeviceToDevice, dv.stream),

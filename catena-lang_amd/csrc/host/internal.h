@@ -30,6 +30,7 @@ enum class KernelId : int {
   GemmBf16DecodeSilu,
   GemmBf16DecodeArgmax,
   GemmBf16DecodeParts,
+  ArgmaxCompose,
   AttnDecodeD128,
   AttnFewD128F32,  // eight waves per pair for few pairs (attn_few.hip)
   AttnFewD128Bf16,
@@ -152,6 +153,17 @@ struct DecodeEpiArgs {
   // Rope: (cos, sin) of every (position, pair) when not null
   // ([max_len][64][2] f32, rope_table_f32), else computed
   const float* rope_tab = nullptr;
+  // X rows by the tokens of a deferred argmax: row m = X[min(argmax of row m
+  // of x_sums, x_rows_limit)], x_sums being a deferred LM head's summaries
+  // ([n][x_sums_blocks][4] u32 over x_sums_cols logits); the tokens are also
+  // written to x_rows_out
+  const uint32_t* x_sums = nullptr;
+  uint32_t x_sums_blocks = 0;
+  uint64_t x_sums_cols = 0;
+  uint32_t* x_rows_out = nullptr;
+  // Argmax: nonzero -> write the logits and the summaries (to arg_partials
+  // when given) only, for a later x_sums gather or argmax_compose
+  uint32_t arg_defer = 0;
 };
 enum class DecodeEpilogue { StoreF32, StoreBf16, Rope, Silu, Argmax, Partials };
 // Decode-shape GEMM (n <= 16) with an epilogue; c is Y (f32, or bf16 for
@@ -173,6 +185,9 @@ uint64_t decode_partials_bytes(uint64_t n, uint64_t m, uint64_t k, uint32_t* k_g
 // partials parts[s][n][m] (f32; S = *k_groups, parts[0] = the product when
 // S = 1) for a consumer that adds them in ascending s.  parts_bytes must hold
 // max(S, 1) * n * m floats.
+// idx[m] = the argmax of row m of a deferred LM head's summaries
+// ([n][blocks][4] u32 over cols logits), as its own composition would give.
+int argmax_compose(const uint32_t* sums, uint32_t n, uint32_t blocks, uint64_t cols, uint32_t* idx);
 int gemm_bf16_decode_parts(const uint16_t* a, const uint16_t* b, float* parts, uint64_t parts_bytes,
                            uint64_t n, uint64_t m, uint64_t k, uint32_t* k_groups);
 // Scratch of the allocation-free decode GEMM (noalloc.hip): its device

@@ -88,6 +88,10 @@ int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, 
   // register path with the reduction buffers only (4 x 8 KiB wave sums + the
   // 16 x 132 f32 tile)
   const bool regs_path = k % 32 != 0;
+  if (ep.x_sums && (regs_path || !ep.x_rows_out || !aligned16(ep.x_sums) || ep.x_sums_blocks == 0 ||
+                    ep.x_sums_cols == 0 || ep.x_sums_cols >= 0x7FFFFFFFull ||
+                    (uint64_t)n * ep.x_sums_blocks * 16 >= (1ull << 31)))
+    return fail(CATENA_ERR_INVALID_ARGUMENT, "decode GEMM token composition operands");
   const uint32_t kw =
       whole_k && !regs_path ? (uint32_t)(ceil_div(ceil_div(k, 4), 32) * 32) : decode_kw(m, k, regs_path);
   const uint64_t chunks = ceil_div(k, kw);
@@ -114,12 +118,15 @@ int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, 
       id = KernelId::GemmBf16DecodeParts;
       break;
     case DecodeEpilogue::Argmax:
-      if (!e.idx || m >= 0x7FFFFFFFull) return fail(CATENA_ERR_INVALID_ARGUMENT, "argmax epilogue operands");
+      if ((!e.idx && !e.arg_defer) || m >= 0x7FFFFFFFull)
+        return fail(CATENA_ERR_INVALID_ARGUMENT, "argmax epilogue operands");
       if (n * gx * 16 > Device::kRowPartialBytes)
         return fail(CATENA_ERR_UNSUPPORTED, "argmax epilogue over %llu column blocks",
                     (unsigned long long)gx);
       e.arg_ticket = d.misc_tickets();
-      e.arg_partials = static_cast<uint32_t*>(d.row_partials());
+      if (!e.arg_partials) e.arg_partials = static_cast<uint32_t*>(d.row_partials());
+      else if (!aligned16(e.arg_partials))
+        return fail(CATENA_ERR_INVALID_ARGUMENT, "argmax summaries must be 16-byte aligned");
       id = KernelId::GemmBf16DecodeArgmax;
       break;
   }
@@ -156,6 +163,17 @@ int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, 
   void* args[] = {&X, &W, &Y, &P, &tickets, (void*)&M, &N, &K, (void*)&kw, &stream_lds, &e};
   if (lds > d.max_lds) return fail(CATENA_ERR_UNSUPPORTED, "decode GEMM needs %zu B of LDS", lds);
   return launch(id, dim3((unsigned)gx, (unsigned)S), dim3(256), lds, args);
+}
+
+int argmax_compose(const uint32_t* sums, uint32_t n, uint32_t blocks, uint64_t cols, uint32_t* idx) {
+  int st = ensure_init();
+  if (st) return st;
+  if (n == 0) return CATENA_OK;
+  if (!sums || !idx || n > 16 || blocks == 0 || cols == 0 || cols >= 0x7FFFFFFFull ||
+      (uint64_t)n * blocks * 16 >= (1ull << 31))
+    return fail(CATENA_ERR_INVALID_ARGUMENT, "argmax composition operands");
+  void* args[] = {&sums, &n, &blocks, &cols, &idx};
+  return launch(KernelId::ArgmaxCompose, dim3(1), dim3(256), 0, args);
 }
 
 int gemm_bf16_decode_parts(const uint16_t* a, const uint16_t* b, float* parts, uint64_t parts_bytes,

@@ -137,7 +137,102 @@ struct DecodeEpi {
   // EPI_ROPE: (cos, sin) of every (position, pair), [max_len][64][2], when
   // given (the values cos_full / sin_full give, so the same bits)
   const float* rope_tab;
+  // X rows by tokens composed here from a deferred LM-head argmax: when
+  // x_sums is given, row m's token is the argmax of row m of those column-
+  // block summaries ([M][x_sums_blocks][4], over x_sums_cols logits), and
+  // workgroup (0, 0) writes the M tokens to x_rows_out
+  const uint32_t* x_sums;
+  uint32_t x_sums_blocks;
+  uint64_t x_sums_cols;
+  uint32_t* x_rows_out;
+  // EPI_ARGMAX: nonzero -> only the logits and the summaries are written;
+  // the argmax is composed by the next kernel that needs it
+  uint32_t arg_defer;
 };
+
+// Argmax composition from per-column-block summaries (u32x4: last NaN or
+// -1, first-max bits, first-max column or 0xFFFFFFFF, pad) of one row, in
+// column order, by one wave: the last NaN J* is the largest J; the answer is
+// the first maximum over the blocks from J*'s block on, whose summaries hold
+// their first maximum after their own last NaN (after J* in J*'s block, over
+// the whole block after it) -- the first maximum as the largest (monotone
+// value, complemented column) pair -- or J* itself if it is the last column.
+// Summaries are loaded coherently (sc1); pe holds the row's first 256 (lane
+// l: blocks l, l + 64, l + 128, l + 192), loaded by argmax_first_sums.
+// (loaded from an in-range block and replaced past gx, so that no branch
+// sits around the load and waits for it can leave later loads in flight)
+CATENA_DEV u32x4_t argmax_sum_load(__amdgpu_buffer_rsrc_t ars, uint32_t r, uint32_t gx, uint32_t b) {
+  const u32x4_t v =
+      __builtin_amdgcn_raw_buffer_load_b128(ars, (int)(((uint64_t)r * gx + (b < gx ? b : gx - 1)) * 16), 0, kCpolSc1);
+  return b < gx ? v : u32x4_t{0xFFFFFFFFu, 0u, 0xFFFFFFFFu, 0u};
+}
+// (raw loads: the blocks past gx are replaced in argmax_compose, so nothing
+// waits on these loads until it runs)
+CATENA_DEV void argmax_first_sums(__amdgpu_buffer_rsrc_t ars, uint32_t r, uint32_t gx, uint32_t lane,
+                                  u32x4_t (&pe)[4]) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const uint32_t b = lane + 64u * u;
+    pe[u] = __builtin_amdgcn_raw_buffer_load_b128(ars, (int)(((uint64_t)r * gx + (b < gx ? b : gx - 1)) * 16), 0,
+                                                  kCpolSc1);
+  }
+}
+CATENA_DEV uint32_t argmax_compose(__amdgpu_buffer_rsrc_t ars, uint32_t r, uint32_t gx, uint64_t N,
+                                   uint32_t lane, const u32x4_t (&pe_raw)[4]) {
+  u32x4_t pe[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+    pe[u] = lane + 64u * u < gx ? pe_raw[u] : u32x4_t{0xFFFFFFFFu, 0u, 0xFFFFFFFFu, 0u};
+  uint32_t jm = 0, bm = 0, bl = 0;  // J + 1; best monotone value, its complemented column
+  auto take = [&](uint32_t b, const u32x4_t& pv, uint32_t bstart) {
+    if (b < gx && b >= bstart && pv[2] != 0xFFFFFFFFu) {
+      const uint32_t mo = mono_bits(pv[1]), lo = (0x7FFFFFFFu - pv[2]) << 1;
+      if (mo > bm || (mo == bm && lo > bl)) {
+        bm = mo;
+        bl = lo;
+      }
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < 4; ++u) jm = pe[u][0] + 1u > jm ? pe[u][0] + 1u : jm;
+  for (uint32_t b0 = 256; b0 < gx; b0 += 256)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const u32x4_t pv = argmax_sum_load(ars, r, gx, b0 + lane + 64u * u);
+      jm = pv[0] + 1u > jm ? pv[0] + 1u : jm;
+    }
+  const uint32_t J1 = wave_umax(jm);  // J* + 1, 0 when no NaN
+  const uint32_t bstart = J1 ? (J1 - 1) / 128u : 0u;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) take(lane + 64u * u, pe[u], bstart);
+  for (uint32_t b0 = 256; b0 < gx; b0 += 256)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t b = b0 + lane + 64u * u;
+      take(b, argmax_sum_load(ars, r, gx, b), bstart);
+    }
+  const uint32_t M_hi = wave_umax(bm);
+  const uint32_t L_lo = wave_umax(bm == M_hi ? bl : 0u);
+  return (J1 != 0u && J1 == N) ? (uint32_t)(N - 1) : 0x7FFFFFFFu - (L_lo >> 1);
+}
+// Rows r = wave, wave + 4, ... < M of a 4-wave workgroup, two rows per pass
+// with both rows' summary loads in flight together; out(r, idx) from lane 0.
+template <typename Out>
+CATENA_DEV void argmax_compose_rows(__amdgpu_buffer_rsrc_t ars, uint32_t M, uint32_t gx, uint64_t N,
+                                    uint32_t wave, uint32_t lane, Out out) {
+  for (uint32_t r = wave; r < M; r += 8) {
+    const bool two = r + 4 < M;
+    u32x4_t pa[4], pb[4];
+    argmax_first_sums(ars, r, gx, lane, pa);
+    argmax_first_sums(ars, two ? r + 4 : r, gx, lane, pb);
+    const uint32_t ia = argmax_compose(ars, r, gx, N, lane, pa);
+    if (lane == 0) out(r, ia);
+    if (two) {
+      const uint32_t ib = argmax_compose(ars, r + 4, gx, N, lane, pb);
+      if (lane == 0) out(r + 4, ib);
+    }
+  }
+}
 
 template <int EPI>
 CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __restrict__ W,
@@ -182,14 +277,16 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
     const uint32_t steps = nslab > (uint32_t)wave ? (nslab - (uint32_t)wave + 3u) / 4u : 0u;
     const uint64_t kw0 = kg0 + 32ull * wave;
     // per-lane global byte offsets of the 8 W instructions (4 rows each)
+    // (a lane whose columns lie past N reads the block's first columns
+    // instead: every load is issued, so the per-stage waits count exactly,
+    // and those columns' sums are never stored)
     uint32_t woff[8];
-    bool wlive[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const uint32_t r = 4 * i + (lane >> 4);
       const uint32_t q = (uint32_t)(lane & 15) ^ hW(r);
-      woff[i] = (uint32_t)(((uint64_t)r * N + 8 * q) * 2);
-      wlive[i] = n0 + 8 * q < N;
+      const bool live = n0 + 8 * q < N;
+      woff[i] = (uint32_t)(((uint64_t)r * N + (live ? 8 * q : 0u)) * 2);
     }
     // X slab: lane l fetches row l / 4 into slot l % 4, which holds the
     // row's global chunk (l % 4) ^ ((row >> 1) & 3): the fragment read
@@ -198,28 +295,52 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
     // per read instead of 4)
     const uint32_t xr = lane >> 2, xq = (uint32_t)(lane & 3) ^ ((xr >> 1) & 3u);
     const bool xl = xr < M;
-    uint32_t xrow = xr;
-    if (ep.x_rows && xl) {
-      xrow = ep.x_rows[xr];
-      if (xrow > ep.x_rows_limit) xrow = ep.x_rows_limit;
-    }
     const char* wsrc = reinterpret_cast<const char*>(W) + (kw0 * N + n0) * 2;
-    const char* xsrc = reinterpret_cast<const char*>(X) + ((uint64_t)xrow * K + kw0 + 8 * xq) * 2;
     // The LM head (argmax epilogue) streams its weight, the largest tensor
     // of a decode step and read once per step, with the non-temporal hint:
     // measured in the C5 step, the Infinity Cache then keeps the block
     // weights and the KV cache between steps (W_qkv 13.7 -> 12.4 us, W_down
     // 12.0 -> 10.5 us, the LM head itself 31.2 -> 31.6 us).
     constexpr int kWAux = EPI == EPI_ARGMAX ? 2 : 0;  // cache policy: nt
-    auto issue = [&](uint32_t t, int slot) {  // slab t of this wave = k kw0 + 128 t
+    auto issue_w = [&](uint32_t t, int slot) {  // slab t of this wave = k kw0 + 128 t
       unsigned char* st = ring + slot * STAGE_BYTES;
       const char* w = wsrc + (uint64_t)t * 128 * N * 2;
 #pragma unroll
       for (int i = 0; i < 8; ++i)
-        if (wlive[i]) __builtin_amdgcn_global_load_lds(w + woff[i], (lds_void*)(st + 1024 * i), 16, 0, kWAux);
-      if (xl) __builtin_amdgcn_global_load_lds(xsrc + (uint64_t)t * 256, (lds_void*)(st + W_SLAB), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(w + woff[i], (lds_void*)(st + 1024 * i), 16, 0, kWAux);
     };
     const uint32_t pre = steps < (uint32_t)RING ? steps : (uint32_t)RING;
+    uint32_t xrow = xr;
+    if (ep.x_sums) {
+      // the tokens of the previous step's LM head, composed from its column
+      // block summaries (the same composition its own last workgroup makes)
+      __shared__ uint32_t tok_s[16];
+      const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)ep.x_sums, (short)0, (int)((uint64_t)M * ep.x_sums_blocks * 16), kRsrcWord3);
+      argmax_compose_rows(srs, M, ep.x_sums_blocks, ep.x_sums_cols, (uint32_t)wave, (uint32_t)lane,
+                          [&](uint32_t r, uint32_t idx) { tok_s[r] = idx; });
+      __syncthreads();
+      if (blockIdx.x == 0 && blockIdx.y == 0 && tid < (int)M) ep.x_rows_out[tid] = tok_s[tid];
+      if (xl) {
+        xrow = tok_s[xr];
+        if (xrow > ep.x_rows_limit) xrow = ep.x_rows_limit;
+      }
+    } else if (ep.x_rows && xl) {
+      xrow = ep.x_rows[xr];
+      if (xrow > ep.x_rows_limit) xrow = ep.x_rows_limit;
+    }
+    // rows past M read row 0: loaded, never stored (an MFMA output row
+    // depends on its own A row only), so every X request is issued too
+    if (!xl) xrow = 0;
+    const char* xsrc = reinterpret_cast<const char*>(X) + ((uint64_t)xrow * K + kw0 + 8 * xq) * 2;
+    auto issue_x = [&](uint32_t t, int slot) {
+      __builtin_amdgcn_global_load_lds(xsrc + (uint64_t)t * 256, (lds_void*)(ring + slot * STAGE_BYTES + W_SLAB), 16,
+                                       0, 0);
+    };
+    auto issue = [&](uint32_t t, int slot) {
+      issue_w(t, slot);
+      issue_x(t, slot);
+    };
     for (uint32_t t = 0; t < pre; ++t) issue(t, (int)t);
     // fragment read addresses inside a stage
     const int G = lane >> 4, sl = lane & 15;
@@ -236,8 +357,7 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
       const int slot = (int)(t % RING);
       const uint32_t later = steps - 1 - t < (uint32_t)(RING - 1) ? steps - 1 - t : (uint32_t)(RING - 1);
       // every instruction of stage t has landed; the later stages may not
-      // have (9 instructions per stage, fewer when lanes are masked, which
-      // only makes the wait stricter)
+      // have (9 instructions per stage)
       if (later >= 3) {
         DEC_WAIT_VMCNT(27);
       } else if (later == 2) {
@@ -505,63 +625,11 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
                                                  0, kCpolSc1);
       }
     }
+    if (ep.arg_defer) return;
+    // the last column block composes every row's argmax from the summaries
     if (!last_arrival(ep.arg_ticket, gx, &last_flag)) return;
-    // The gx summaries of a row composed in column order (one wave per row,
-    // summaries of blocks lane, lane + 64, ... loaded coherently): the last
-    // NaN J* is the largest J; the answer is the first maximum over the
-    // blocks from J*'s block on, whose summaries hold their first maximum
-    // after their own last NaN (after J* in J*'s block, over the whole block
-    // after it) -- the first maximum as the largest (monotone value,
-    // complemented column) pair -- or J* itself if it is the last column.
-    auto load_sum = [&](uint32_t r, uint32_t b) {
-      return b < gx ? __builtin_amdgcn_raw_buffer_load_b128(ars, (int)(((uint64_t)r * gx + b) * 16), 0, kCpolSc1)
-                    : u32x4_t{0xFFFFFFFFu, 0u, 0xFFFFFFFFu, 0u};
-    };
-    // pe: the row's first 256 summaries, kept in registers between passes
-    auto compose = [&](uint32_t r, const u32x4_t (&pe)[4]) {
-      uint32_t jm = 0, bm = 0, bl = 0;  // J + 1; best monotone value, its complemented column
-      auto take = [&](uint32_t b, const u32x4_t& pv, uint32_t bstart) {
-        if (b < gx && b >= bstart && pv[2] != 0xFFFFFFFFu) {
-          const uint32_t mo = mono_bits(pv[1]), lo = (0x7FFFFFFFu - pv[2]) << 1;
-          if (mo > bm || (mo == bm && lo > bl)) {
-            bm = mo;
-            bl = lo;
-          }
-        }
-      };
-#pragma unroll
-      for (int u = 0; u < 4; ++u) jm = pe[u][0] + 1u > jm ? pe[u][0] + 1u : jm;
-      for (uint32_t b0 = 256; b0 < gx; b0 += 256)
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const u32x4_t pv = load_sum(r, b0 + (uint32_t)lane + 64u * u);
-          jm = pv[0] + 1u > jm ? pv[0] + 1u : jm;
-        }
-      const uint32_t J1 = wave_umax(jm);  // J* + 1, 0 when no NaN
-      const uint32_t bstart = J1 ? (J1 - 1) / 128u : 0u;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) take((uint32_t)lane + 64u * u, pe[u], bstart);
-      for (uint32_t b0 = 256; b0 < gx; b0 += 256)
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const uint32_t b = b0 + (uint32_t)lane + 64u * u;
-          take(b, load_sum(r, b), bstart);
-        }
-      const uint32_t M_hi = wave_umax(bm);
-      const uint32_t L_lo = wave_umax(bm == M_hi ? bl : 0u);
-      if (lane == 0) ep.idx[r] = (J1 != 0u && J1 == N) ? (uint32_t)(N - 1) : 0x7FFFFFFFu - (L_lo >> 1);
-    };
-    for (uint32_t r = wave; r < M; r += 8) {
-      // both rows' summary loads are in flight together
-      const bool two = r + 4 < M;
-      u32x4_t pa[4], pb[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) pa[u] = load_sum(r, (uint32_t)lane + 64u * u);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) pb[u] = load_sum(two ? r + 4 : r, (uint32_t)lane + 64u * u);
-      compose(r, pa);
-      if (two) compose(r + 4, pb);
-    }
+    argmax_compose_rows(ars, M, gx, N, (uint32_t)wave, (uint32_t)lane,
+                        [&](uint32_t r, uint32_t idx) { ep.idx[r] = idx; });
   }
 }
 
@@ -581,3 +649,15 @@ CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_rope, EPI_ROPE)
 CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_silu, EPI_SILU)
 CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_argmax, EPI_ARGMAX)
 CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_parts, EPI_PARTIALS)
+
+// The argmax of a deferred LM head (arg_defer): idx[m] composed from the M
+// rows of gx column-block summaries over N logits.  One 256-thread
+// workgroup.
+extern "C" __global__ __launch_bounds__(256) void catena_argmax_compose(const uint32_t* __restrict__ sums,
+                                                                        uint32_t M, uint32_t gx, uint64_t N,
+                                                                        uint32_t* __restrict__ idx) {
+  const __amdgpu_buffer_rsrc_t srs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)sums, (short)0, (int)((uint64_t)M * gx * 16), kRsrcWord3);
+  argmax_compose_rows(srs, M, gx, N, threadIdx.x >> 6, threadIdx.x & 63u,
+                      [&](uint32_t r, uint32_t v) { idx[r] = v; });
+}
