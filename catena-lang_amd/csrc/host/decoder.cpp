@@ -33,8 +33,9 @@ struct catena_decoder {
   void* w_lm = nullptr;
   void* inv_freq = nullptr;
   void* rope_tab = nullptr;  // [max_len][head_dim / 2][2] f32: (cos, sin) per position and pair
-  // a decode step's W_o / W_down k-group partials ([S][rows][d] f32), added
-  // by the RMSNorm that consumes the projection
+  // a decode step's W_qkv / W_o / W_down k-group partials ([S][rows][width]
+  // f32), added by the kernel that consumes the projection (the attention,
+  // the RMSNorms)
   void* parts = nullptr;
   uint64_t parts_bytes = 0;
   // the generate loop's deferred LM-head argmax: per-column-block summaries
@@ -169,6 +170,9 @@ int forward(catena_decoder& m, const uint32_t* tokens, uint32_t batch, uint32_t 
   }
 
   uint32_t parts_down = 0;  // k groups of the last W_down partials (decode step)
+  // a decode step whose attention is the eight-wave kernel takes q / k / v
+  // as W_qkv's partials
+  const bool few_attn = step && attn_few_fits(batch, 1, c.n_heads, c.max_len);
   for (uint32_t l = 0; l < c.n_layers; ++l) {
     // x_l = h_{l-1} + ffn_{l-1} (layer 0: the embedding), xn = bf16(rmsnorm(x_l)).
     // A decode step's layer 0 reads xn as rows of the normalized embedding
@@ -211,14 +215,36 @@ int forward(catena_decoder& m, const uint32_t* tokens, uint32_t batch, uint32_t 
           e.x_rows = tokens;
         }
       }
-      TRY(gemm_bf16_decode(xn, wqkv, QKV, rows, 3 * d, d, DecodeEpilogue::Rope, e));
+      if (few_attn) {
+        // W_qkv as k-group partials: the attention adds them, rotates q and
+        // k and appends the caches itself (no hand-off in the projection)
+        uint32_t parts_qkv = 0;
+        float* P = static_cast<float*>(m.parts);
+        TRY(gemm_bf16_decode_parts(xn, wqkv, P, m.parts_bytes, rows, 3 * d, d, &parts_qkv, e));
+        FewQkvArgs fq;
+        fq.parts = P;
+        fq.part_stride = rows * 3 * d;
+        fq.n_parts = parts_qkv;
+        fq.rope_tab = static_cast<const float*>(m.rope_tab);
+        fq.q_out = Q;
+        fq.qkv_out = QKV;
+        fq.k_cache = kc;
+        fq.v_cache = vc;
+        const int st_ = attn_few_launch(nullptr, kc, vc, lens, ATT, batch, 1, c.n_heads, c.max_len, scale,
+                                        false, fq);
+        if (st_ < 0) return fail(CATENA_ERR_UNSUPPORTED, "eight-wave attention did not apply");
+        TRY(st_);
+      } else {
+        TRY(gemm_bf16_decode(xn, wqkv, QKV, rows, 3 * d, d, DecodeEpilogue::Rope, e));
+      }
     } else {
       TRY(catena_mi355x_gemm_bf16(XN, wqkv, QKV, rows, 3 * d, d, 1));
       TRY(catena_mi355x_rope_qkv_bf16(QKV, inv, lens, Q, kc, vc, batch, tq, c.n_heads, c.head_dim,
                                       c.max_len));
     }
-    TRY(catena_mi355x_attn_causal_bf16(Q, kc, vc, lens, ATT, batch, tq, c.n_heads, c.max_len,
-                                       c.head_dim, scale, 0));
+    if (!(step && few_attn))
+      TRY(catena_mi355x_attn_causal_bf16(Q, kc, vc, lens, ATT, batch, tq, c.n_heads, c.max_len,
+                                         c.head_dim, scale, 0));
     if (step) {
       // W_o without its split-K hand-off: the norm below adds the k-group
       // partials (and writes their sum to AP)
@@ -398,11 +424,13 @@ int catena_mi355x_decoder_create(const catena_decoder_config_t* cfg, catena_deco
   // partials of the decode step's two row-reduced projections: S k groups of
   // max_batch x d floats for W_o (k = d) and W_down (k = d_ff)
   {
-    uint32_t s_o = 0, s_down = 0;
+    uint32_t s_o = 0, s_down = 0, s_qkv = 0;
     decode_partials_bytes(c.max_batch, c.d_model, c.d_model, &s_o);
     decode_partials_bytes(c.max_batch, c.d_model, c.ffn_dim, &s_down);
+    decode_partials_bytes(c.max_batch, 3ull * c.d_model, c.d_model, &s_qkv);
     const uint64_t groups = std::max<uint64_t>(1, std::max(s_o, s_down));
-    m->parts_bytes = groups * c.max_batch * c.d_model * 4;
+    m->parts_bytes = std::max<uint64_t>(groups * c.d_model, std::max<uint64_t>(1, s_qkv) * 3ull * c.d_model) *
+                     c.max_batch * 4;
     if ((st = alloc(m->parts_bytes, &m->parts))) return fail_out(st);
   }
   if ((st = alloc((uint64_t)c.max_batch * ((c.vocab + 127) / 128) * 16, &m->arg_sums))) return fail_out(st);

@@ -107,11 +107,28 @@ constexpr size_t kAttnFewFixed = 4096 + 6 * 4096 + 2 * 6 * 8192;
 inline size_t attn_few_lds_bytes(uint32_t max_len) {
   return kAttnFewFixed + (size_t)((max_len + 63) / 64) * (64 * 4);
 }
+// A decode step's q / k / v as its fused projection's k-group partials
+// (FewQkv in attn_few.hip, field for field): parts[n_parts][rows][3 H 128]
+// f32, added in ascending order, q / k rotated with rope_tab
+// ([max_len][64] (cos, sin)), q written to q_out (bf16), the sums to qkv_out
+// (when given) and the new k / v rows to k_cache / v_cache at lens[b] - 1.
+struct FewQkvArgs {
+  const float* parts = nullptr;
+  uint64_t part_stride = 0;
+  uint32_t n_parts = 0;
+  const float* rope_tab = nullptr;
+  uint16_t* q_out = nullptr;
+  float* qkv_out = nullptr;
+  uint16_t* k_cache = nullptr;
+  uint16_t* v_cache = nullptr;
+};
+// Whether the eight-wave attention serves this shape.
+bool attn_few_fits(uint32_t batch, uint32_t tq, uint32_t heads, uint32_t max_len);
 // Launch the eight-wave attention when it applies; returns -1 (nothing
 // launched) when it does not.
 int attn_few_launch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint32_t* lens,
                     void* o, uint32_t batch, uint32_t tq, uint32_t heads, uint32_t max_len,
-                    float scale, bool out_f32);
+                    float scale, bool out_f32, const FewQkvArgs& qkv = FewQkvArgs());
 
 // LDS of catena_rmsnorm_rows (block.hip): its static __shared__ f32 (rounded
 // up to the 16-byte alignment of the dynamic area that follows it) plus the
@@ -189,7 +206,8 @@ uint64_t decode_partials_bytes(uint64_t n, uint64_t m, uint64_t k, uint32_t* k_g
 // ([n][blocks][4] u32 over cols logits), as its own composition would give.
 int argmax_compose(const uint32_t* sums, uint32_t n, uint32_t blocks, uint64_t cols, uint32_t* idx);
 int gemm_bf16_decode_parts(const uint16_t* a, const uint16_t* b, float* parts, uint64_t parts_bytes,
-                           uint64_t n, uint64_t m, uint64_t k, uint32_t* k_groups);
+                           uint64_t n, uint64_t m, uint64_t k, uint32_t* k_groups,
+                           const DecodeEpiArgs& gather = DecodeEpiArgs());
 // Scratch of the allocation-free decode GEMM (noalloc.hip): its device
 // address, looked up once per device at init (noalloc_setup, with that
 // device current), and its size.

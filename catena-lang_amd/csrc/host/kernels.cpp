@@ -177,7 +177,8 @@ int argmax_compose(const uint32_t* sums, uint32_t n, uint32_t blocks, uint64_t c
 }
 
 int gemm_bf16_decode_parts(const uint16_t* a, const uint16_t* b, float* parts, uint64_t parts_bytes,
-                           uint64_t n, uint64_t m, uint64_t k, uint32_t* k_groups) {
+                           uint64_t n, uint64_t m, uint64_t k, uint32_t* k_groups,
+                           const DecodeEpiArgs& gather) {
   if (!parts || !k_groups) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
   uint32_t S = 0;
   decode_partials_bytes(n, m, k, &S);
@@ -186,19 +187,33 @@ int gemm_bf16_decode_parts(const uint16_t* a, const uint16_t* b, float* parts, u
     return fail(CATENA_ERR_UNSUPPORTED, "decode GEMM partials need %llu B",
                 (unsigned long long)((uint64_t)*k_groups * n * m * sizeof(float)));
   // S > 1: the partials go to P = parts; S = 1: the product goes to Y = parts
-  return gemm_bf16_decode(a, b, parts, n, m, k, DecodeEpilogue::Partials, DecodeEpiArgs(), parts,
-                          parts_bytes);
+  // (gather: only its X-row fields are read)
+  DecodeEpiArgs e;
+  e.x_rows = gather.x_rows;
+  e.x_rows_limit = gather.x_rows_limit;
+  e.x_sums = gather.x_sums;
+  e.x_sums_blocks = gather.x_sums_blocks;
+  e.x_sums_cols = gather.x_sums_cols;
+  e.x_rows_out = gather.x_rows_out;
+  return gemm_bf16_decode(a, b, parts, n, m, k, DecodeEpilogue::Partials, e, parts, parts_bytes);
+}
+
+bool attn_few_fits(uint32_t batch, uint32_t tq, uint32_t heads, uint32_t max_len) {
+  const uint64_t nq = (uint64_t)batch * tq * heads;
+  return nq > 0 && nq <= kAttnFewMaxQueries && tq < 8 && max_len >= 64 &&
+         attn_few_lds_bytes(max_len) <= device().max_lds;
 }
 
 int attn_few_launch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint32_t* lens,
                     void* o, uint32_t batch, uint32_t tq, uint32_t heads, uint32_t max_len,
-                    float scale, bool out_f32) {
+                    float scale, bool out_f32, const FewQkvArgs& qkv) {
   const uint64_t nq = (uint64_t)batch * tq * heads;
-  Device& d = device();
-  if (nq == 0 || nq > kAttnFewMaxQueries || tq >= 8 || max_len < 64 ||
-      attn_few_lds_bytes(max_len) > d.max_lds)
-    return -1;
-  void* args[] = {&q, &k, &v, &lens, &o, &heads, &max_len, &tq, &scale};
+  if (!attn_few_fits(batch, tq, heads, max_len)) return -1;
+  if (qkv.parts && (tq != 1 || qkv.n_parts == 0 || !qkv.rope_tab || !qkv.q_out || !qkv.k_cache ||
+                    !qkv.v_cache || qkv.part_stride < (uint64_t)batch * 3 * heads * 128))
+    return fail(CATENA_ERR_INVALID_ARGUMENT, "attention q/k/v partials operands");
+  FewQkvArgs a = qkv;
+  void* args[] = {&q, &k, &v, &lens, &o, &heads, &max_len, &tq, &scale, &a};
   return launch(out_f32 ? KernelId::AttnFewD128F32 : KernelId::AttnFewD128Bf16, dim3((unsigned)nq),
                 dim3(512), attn_few_lds_bytes(max_len), args);
 }

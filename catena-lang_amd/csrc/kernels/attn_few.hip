@@ -50,9 +50,11 @@ constexpr int VB_ROWS = 64;              // rows per V batch
 constexpr int VB_BYTES = VB_ROWS * 128;  // 64 rows x 64 columns bf16
 constexpr int VRING = 6;                 // batches in flight per V wave (8 loads each)
 
-// LDS: q copies [6][128] f32 | den, last score, last NaN, max keys |
-// K stages [6][4 KiB] | V rings [2][VRING][8 KiB] | scores sp[64 * ceil(L/64)]
+// LDS: q copies [6][128] f32 | den, last score, last NaN, max keys | new key
+// row | K stages [6][4 KiB] | V rings [2][VRING][8 KiB] | scores
+// sp[64 * ceil(L/64)]
 constexpr uint32_t kOffDen = KWAVES * 512;
+constexpr uint32_t kOffKNew = kOffDen + 256;  // the new key row (partials mode), 256 B
 constexpr uint32_t kOffK = 4096;
 constexpr uint32_t kOffV = kOffK + KWAVES * KSTAGE_WAVE;
 constexpr uint32_t kOffState = kOffV + 2 * VRING * VB_BYTES;
@@ -99,10 +101,34 @@ CATENA_DEV float row_bcast(float x, int j) {
 #undef CATENA_ROW_BCAST
 }
 
+}  // namespace
+
+// A decode step's q / k / v as the k-group partials of its fused projection
+// (parts != null; Tq = 1, row = b): the kernel adds them in ascending k group
+// (the adds the projection's own reduction makes), rotates q and k with the
+// RoPE table rows of the row's position pos = lens[b] - 1 (the rotation the
+// projection's epilogue makes), rounds to bf16, writes q_out, the f32 sums
+// to qkv_out (when given) and the new k / v rows to the caches at pos (when
+// pos < L), and attends with them: the new key's row is put into the
+// registers of the block that holds it and the new value's row into its V
+// batch in LDS, so the rows read from the caches at pos are never used.
+struct FewQkv {
+  const float* parts;    // [n_parts][rows][3 * H * 128]
+  uint64_t part_stride;  // rows * 3 * H * 128
+  uint32_t n_parts;
+  const float* rope_tab;  // [L][64] (cos, sin) pairs
+  uint16_t* q_out;        // [rows][H * 128]
+  float* qkv_out;         // [rows][3 * H * 128] or null
+  uint16_t* k_cache;      // the caches k / v read, written at pos
+  uint16_t* v_cache;
+};
+
+namespace {
+
 template <bool OUT_BF16>
-CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-                              const uint16_t* __restrict__ v, const uint32_t* __restrict__ lens,
-                              void* __restrict__ o, uint32_t H, uint32_t L, uint32_t Tq, float scale) {
+CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* k, const uint16_t* v,
+                              const uint32_t* __restrict__ lens, void* __restrict__ o, uint32_t H, uint32_t L,
+                              uint32_t Tq, float scale, const FewQkv& qkv) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
   float* den_slot = reinterpret_cast<float*>(smem + kOffDen);
   float* last_slot = den_slot + 1;                                          // score at len - 1
@@ -122,6 +148,46 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* __
   const uint16_t* kb = k + bh * (uint64_t)L * D;
   const uint16_t* vb = v + bh * (uint64_t)L * D;
   const uint32_t nblk = (len + 63u) / 64u;
+  // partials mode: the new row's position and the sum of a column's parts
+  const uint32_t raw_len = lens[b];
+  const bool pos_ok = raw_len >= 1u && raw_len - 1u < L;
+  const uint32_t pos = pos_ok ? raw_len - 1u : 0u;
+  const uint64_t HD = (uint64_t)H * D;
+  // columns c and c2 of the fused row, parts added in ascending order; the
+  // first four parts' loads are all issued before the first add
+  auto part_sums = [&](uint64_t c, uint64_t c2, float& x, float& x2) {
+    const float* p = qkv.parts + (uint64_t)row * 3 * HD;
+    const uint32_t n = qkv.n_parts;
+    float v[4], v2[4];
+#pragma unroll
+    for (uint32_t u = 0; u < 4; ++u) {
+      const uint64_t o = (u < n ? u : 0u) * qkv.part_stride;
+      v[u] = p[o + c];
+      v2[u] = p[o + c2];
+    }
+    x = v[0];
+    x2 = v2[0];
+#pragma unroll
+    for (uint32_t u = 1; u < 4; ++u) {  // (selects, not branches: one straight sequence)
+      const float s1 = x + v[u], s2 = x2 + v2[u];
+      x = u < n ? s1 : x;
+      x2 = u < n ? s2 : x2;
+    }
+    for (uint32_t u = 4; u < n; ++u) {
+      x = x + p[u * qkv.part_stride + c];
+      x2 = x2 + p[u * qkv.part_stride + c2];
+    }
+  };
+  // pair (lane, lane + 64) of head h's part 0 (q) or 1 (k), rotated:
+  // y1 = x1 c - x2 s, y2 = x2 c + x1 s (each op rounded)
+  auto rope_pair = [&](uint32_t part, float& x1, float& x2, float& y1, float& y2) {
+    const uint64_t c0 = part * HD + (uint64_t)h * D + (uint32_t)lane;
+    const float2 cp = reinterpret_cast<const float2*>(qkv.rope_tab)[(uint64_t)pos * 64 + (uint32_t)lane];
+    part_sums(c0, c0 + 64, x1, x2);
+    const float t1 = x1 * cp.x, t2 = x2 * cp.y, t3 = x2 * cp.x, t4 = x1 * cp.y;
+    y1 = t1 - t2;
+    y2 = t3 + t4;
+  };
 
   if (wave >= KWAVES) {
     // ---------------------------------------------------------- V waves
@@ -139,6 +205,27 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* __
     // for this kernel.
     const uint32_t vr = (uint32_t)lane >> 3, vc = (uint32_t)lane & 7u;
     const uint16_t* vlane = vb + (uint64_t)vr * D + colbase + 8 * vc;
+    // partials mode: this wave's column of the new value row, to the cache
+    // now and into its V batch once that batch is in LDS
+    const bool new_val = qkv.parts && pos_ok;
+    uint16_t vnew = 0;
+    if (qkv.parts) {
+      float x, x_unused;
+      const uint64_t cv = 2 * HD + (uint64_t)h * D + colbase + (uint32_t)lane;
+      part_sums(cv, cv, x, x_unused);
+      vnew = (uint16_t)f32_to_bf16_bits(x);
+      if (pos_ok) qkv.v_cache[(bh * L + pos) * D + colbase + lane] = vnew;
+      if (qkv.qkv_out) qkv.qkv_out[(uint64_t)row * 3 * HD + 2 * HD + (uint64_t)h * D + colbase + lane] = x;
+    }
+    const uint32_t bt_new = pos / (uint32_t)VB_ROWS;
+    auto put_new_val = [&](uint32_t bt) {
+      if (new_val && bt == bt_new) {
+        uint16_t* slot16 = reinterpret_cast<uint16_t*>(smem + ring_off + (bt % VRING) * VB_BYTES);
+        slot16[(pos % VB_ROWS) * 64 + lane] = vnew;
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): written before any lane reads it
+        __builtin_amdgcn_wave_barrier();
+      }
+    };
     auto issue = [&](uint32_t bt) {
       unsigned char* slot = smem + ring_off + (bt % VRING) * VB_BYTES;
       if ((bt + 1) * VB_ROWS <= len) {
@@ -233,6 +320,7 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* __
     i16x4_t va[8], vb8[8];
     if (nfull > 0) {
       wait_batch(0);
+      put_new_val(0);
       read_half(0, 0, pa, va);
     }
     uint32_t bt = 0;
@@ -242,6 +330,7 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* __
       refill(bt);
       if (bt + 1 < nfull) {
         wait_batch(bt + 1);
+        put_new_val(bt + 1);
         read_half(bt + 1, 0, pa, va);
       }
       fold_regs(pb, vb8);
@@ -249,6 +338,7 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* __
     if (bt < nblk) {
       // the last, partial batch
       wait_batch(bt);
+      put_new_val(bt);
       const uint16_t* st16 = reinterpret_cast<const uint16_t*>(smem + ring_off + (bt % VRING) * VB_BYTES);
       const uint32_t t0 = bt * VB_ROWS;
       for (uint32_t rr = 0; rr < len - t0; ++rr) {
@@ -264,9 +354,49 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* __
   }
 
   // ------------------------------------------------------------ K waves
-  // this wave's q, requested ahead of its K rows so it lands first
-  const uint16_t q_lo = q[(uint64_t)qi * D + 2 * lane];
-  const uint16_t q_hi = q[(uint64_t)qi * D + 2 * lane + 1];
+  // this wave's q, requested ahead of its K rows so it lands first (lane l:
+  // elements 2l, 2l+1; partials mode: l and l + 64, rotated here)
+  uint16_t q_lo = 0, q_hi = 0;
+  uint16_t* kbuf = reinterpret_cast<uint16_t*>(smem + kOffKNew);  // the new key row, bf16
+  const uint32_t blk_new = pos / 64u;  // the block holding the new row
+  if (qkv.parts) {
+    float x1, x2, y1, y2, kx1, kx2, ky1, ky2;
+    rope_pair(0, x1, x2, y1, y2);
+    // every score wave requests the new key's pair too (its loads go out
+    // with q's); the wave whose blocks hold it uses it
+    rope_pair(1, kx1, kx2, ky1, ky2);
+    q_lo = (uint16_t)f32_to_bf16_bits(y1);
+    q_hi = (uint16_t)f32_to_bf16_bits(y2);
+    if (wave == 0) {
+      uint16_t* dq = qkv.q_out + (uint64_t)row * HD + (uint64_t)h * D;
+      dq[lane] = q_lo;
+      dq[lane + 64] = q_hi;
+      if (qkv.qkv_out) {
+        float* dx = qkv.qkv_out + (uint64_t)row * 3 * HD + (uint64_t)h * D;
+        dx[lane] = x1;
+        dx[lane + 64] = x2;
+      }
+    }
+    if (wave == (int)(blk_new % KWAVES)) {
+      // the new key: into this wave's LDS row buffer, and to the cache
+      const uint16_t k1 = (uint16_t)f32_to_bf16_bits(ky1), k2 = (uint16_t)f32_to_bf16_bits(ky2);
+      kbuf[lane] = k1;
+      kbuf[lane + 64] = k2;
+      if (pos_ok) {
+        uint16_t* dk = qkv.k_cache + (bh * L + pos) * D;
+        dk[lane] = k1;
+        dk[lane + 64] = k2;
+      }
+      if (qkv.qkv_out) {
+        float* dx = qkv.qkv_out + (uint64_t)row * 3 * HD + HD + (uint64_t)h * D;
+        dx[lane] = kx1;
+        dx[lane + 64] = kx2;
+      }
+    }
+  } else {
+    q_lo = q[(uint64_t)qi * D + 2 * lane];
+    q_hi = q[(uint64_t)qi * D + 2 * lane + 1];
+  }
   const int lrow = lane >> 2, lchunk = lane & 3;
   unsigned char* st = smem + kOffK + wave * KSTAGE_WAVE;
   float* qf = reinterpret_cast<float*>(smem + wave * 512);
@@ -346,13 +476,36 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* __
     key_word[1] = 0u;
   }
   lds_barrier();  // (0) K requested (V follows it), max words cleared
-  qf[2 * lane] = bf16_to_f32(q_lo);
-  qf[2 * lane + 1] = bf16_to_f32(q_hi);
+  if (qkv.parts) {
+    qf[lane] = bf16_to_f32(q_lo);
+    qf[lane + 64] = bf16_to_f32(q_hi);
+  } else {
+    qf[2 * lane] = bf16_to_f32(q_lo);
+    qf[2 * lane + 1] = bf16_to_f32(q_hi);
+  }
   wave_sync();
+  // partials mode: the rows of block blk_new in registers r, row pos % 64
+  // replaced by the new key (row lrow + 16 i of segment seg is r[4 seg + i])
+  auto put_new_key = [&](u32x4_t r[16]) {
+    const uint32_t rp = pos & 63u;
+    const bool mine = (uint32_t)lrow == (rp & 15u);
+#pragma unroll
+    for (int seg = 0; seg < 4; ++seg) {
+      const u32x4_t nv = *reinterpret_cast<const u32x4_t*>(kbuf + seg * 32 + lchunk * 8);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (mine && (uint32_t)i == (rp >> 4)) r[4 * seg + i] = nv;
+    }
+  };
+  const bool new_key = qkv.parts && pos_ok;  // then len = pos + 1 >= 1
   for (uint32_t bk = b0; bk < nblk; bk += 2 * KWAVES) {
+    if (new_key && bk == blk_new) put_new_key(ra);
     fold(bk, ra);
     gload(bk + 2 * KWAVES, ra);
-    if (bk + KWAVES < nblk) fold(bk + KWAVES, rb);
+    if (bk + KWAVES < nblk) {
+      if (new_key && bk + KWAVES == blk_new) put_new_key(rb);
+      fold(bk + KWAVES, rb);
+    }
     gload(bk + 3 * KWAVES, rb);
   }
   lds_barrier();  // (1) scores, last NaN and first key written
@@ -387,15 +540,13 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* __
 }  // namespace
 
 extern "C" __global__ __launch_bounds__(512) void catena_attn_few_bf16_d128_f32out(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-    const uint32_t* __restrict__ lens, float* __restrict__ o, uint32_t H, uint32_t L, uint32_t Tq,
-    float scale) {
-  attn_few_body<false>(q, k, v, lens, o, H, L, Tq, scale);
+    const uint16_t* __restrict__ q, const uint16_t* k, const uint16_t* v, const uint32_t* __restrict__ lens,
+    float* __restrict__ o, uint32_t H, uint32_t L, uint32_t Tq, float scale, FewQkv qkv) {
+  attn_few_body<false>(q, k, v, lens, o, H, L, Tq, scale, qkv);
 }
 
 extern "C" __global__ __launch_bounds__(512) void catena_attn_few_bf16_d128_bf16out(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-    const uint32_t* __restrict__ lens, uint16_t* __restrict__ o, uint32_t H, uint32_t L, uint32_t Tq,
-    float scale) {
-  attn_few_body<true>(q, k, v, lens, o, H, L, Tq, scale);
+    const uint16_t* __restrict__ q, const uint16_t* k, const uint16_t* v, const uint32_t* __restrict__ lens,
+    uint16_t* __restrict__ o, uint32_t H, uint32_t L, uint32_t Tq, float scale, FewQkv qkv) {
+  attn_few_body<true>(q, k, v, lens, o, H, L, Tq, scale, qkv);
 }
