@@ -69,6 +69,7 @@ const KernelSpec kKernels[] = {
     {KernelId::GemmBf16DecodeArgmax, "gemm_bf16_decode", "catena_gemm_bf16_decode_argmax"},
     {KernelId::GemmBf16DecodeParts, "gemm_bf16_decode", "catena_gemm_bf16_decode_parts"},
     {KernelId::ArgmaxCompose, "gemm_bf16_decode", "catena_argmax_compose"},
+    {KernelId::DecodeReduce, "gemm_bf16_decode", "catena_decode_reduce"},
     {KernelId::AttnDecodeD128, "attn_decode", "catena_attn_decode_bf16_d128"},
     {KernelId::AttnFewD128F32, "attn_few", "catena_attn_few_bf16_d128_f32out"},
     {KernelId::AttnFewD128Bf16, "attn_few", "catena_attn_few_bf16_d128_bf16out"},

@@ -31,6 +31,7 @@ enum class KernelId : int {
   GemmBf16DecodeArgmax,
   GemmBf16DecodeParts,
   ArgmaxCompose,
+  DecodeReduce,
   AttnDecodeD128,
   AttnFewD128F32,  // eight waves per pair for few pairs (attn_few.hip)
   AttnFewD128Bf16,

@@ -650,6 +650,45 @@ CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_silu, EPI_SILU)
 CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_argmax, EPI_ARGMAX)
 CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_parts, EPI_PARTIALS)
 
+// The split-K reduction of a plain decode GEMM, as a launch of its own after
+// the partials kernel (EPI_PARTIALS): Y = ((P[0] + P[1]) + ...) + P[S-1]
+// elementwise, ascending s -- the adds the last-arriving workgroup of the
+// ticketed form makes, so the same bits -- stored as f32 or as bf16 (RNE).
+// The launch boundary orders the partials before these loads, which takes
+// the place of the ticket's agent-scope release / acquire (an L2 write-back
+// per workgroup and an L2 invalidate per column block).  Four elements per
+// thread; n4 = M * N / 4.
+extern "C" __global__ __launch_bounds__(256) void catena_decode_reduce(const float* __restrict__ P,
+                                                                       uint64_t part_elems, uint32_t S,
+                                                                       void* __restrict__ Y, uint64_t n4,
+                                                                       uint32_t out_bf16) {
+  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  const f32x4_t* p4 = reinterpret_cast<const f32x4_t*>(P) + i;
+  const uint64_t st4 = part_elems / 4;
+  f32x4_t sum = p4[0];
+  for (uint32_t s0 = 1; s0 < S; s0 += 8) {
+    f32x4_t v[8];
+#pragma unroll
+    for (uint32_t u = 0; u < 8; ++u)
+      if (s0 + u < S) v[u] = p4[(s0 + u) * st4];
+#pragma unroll
+    for (uint32_t u = 0; u < 8; ++u)
+      if (s0 + u < S) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sum[q] = sum[q] + v[u][q];
+      }
+  }
+  if (out_bf16) {
+    uint2 o;
+    o.x = pack_bf16x2(sum[0], sum[1]);
+    o.y = pack_bf16x2(sum[2], sum[3]);
+    reinterpret_cast<uint2*>(Y)[i] = o;
+  } else {
+    reinterpret_cast<f32x4_t*>(Y)[i] = sum;
+  }
+}
+
 // The argmax of a deferred LM head (arg_defer): idx[m] composed from the M
 // rows of gx column-block summaries over N logits.  One 256-thread
 // workgroup.
