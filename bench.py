@@ -44,8 +44,11 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
 
 
 def measured_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE summary (copy-kernel calibrated), or None."""
+    """HBM bytes per launch of `kernel` (or per call of a workload whose
+    entry sums the kernels one call launches) from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (copy-kernel calibrated), or None.  Read
+    from the file, not measured in this run: counters need a profiler pass
+    of their own."""
     try:
         with open(TRAFFIC_FILE) as f:
             d = json.load(f)
@@ -231,7 +234,7 @@ def bench_decode_gemm(steps, warmup, ev):
                              "roofline": {"bound": "hbm", "achieved": round(gbs, 1),
                                           "peak": PEAK_HBM_GBS, "unit": "GB/s",
                                           "frac": round(gbs / PEAK_HBM_GBS, 4),
-                                          "traffic": measured_traffic("catena_gemm_bf16_decode_bf16out")},
+                                          "traffic": measured_traffic(f"decode_gemm_N{N}_K{K}")},
                              "inputs": (x.read(np.uint16, (M, K)), ws[0].read(np.uint16, (K, N)))}
         del ws
     return res

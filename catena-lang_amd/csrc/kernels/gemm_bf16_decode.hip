@@ -14,13 +14,16 @@
 //     taking slabs w, w+4, ...; register path: 4 consecutive chunks of KW),
 //     and the workgroup adds the 4 wave sums in wave order through LDS;
 //   * grid.y = number of k ranges (S).  With S > 1 each workgroup stores
-//     its f32 partial P[s][m][n] (16-byte stores that bypass the XCD caches)
-//     and takes a completion ticket for its column block; the last of the S
-//     workgroups loads the S partials the same way and adds them in
-//     ascending s.  The final M x 128 tile then goes through LDS to the
-//     epilogue.
-// The addition order depends only on the shape (the ticket decides which
-// workgroup adds, not how), so results are bitwise identical run to run.
+//     its f32 partial P[s][m][n] (16-byte stores that bypass the XCD caches).
+//     Plain outputs (Y f32 or bf16) then end the kernel (EPI_PARTIALS) and
+//     catena_decode_reduce, launched next, adds P[0] .. P[S-1] in ascending
+//     s.  The fused epilogues instead take a completion ticket for their
+//     column block; the last of the S workgroups loads the S partials the
+//     same way, adds them in ascending s and runs the epilogue on the final
+//     M x 128 tile, staged in LDS.
+// The addition order depends only on the shape (which workgroup or launch
+// adds never changes how), so results are bitwise identical run to run and
+// between the two forms.
 //
 // Epilogues (each also writes the f32 tile to Y unless EPI_STORE_BF16):
 //   EPI_STORE   Y f32;          EPI_STORE_BF16  Y bf16 (RNE)
