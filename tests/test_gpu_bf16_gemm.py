@@ -215,8 +215,14 @@ def test_gemm_4096_full_compare_and_run_to_run():
 
 
 @pytest.mark.parametrize("mrows,n,k", [(16, 11008, 4096), (16, 4096, 11008), (1, 4096, 4096),
-                                       (7, 1024, 960), (16, 128, 32), (5, 136, 8)])
+                                       (7, 1024, 960), (16, 128, 32), (5, 136, 8),
+                                       (16, 256, 16384), (3, 136, 20000)])
 def test_decode_kernel_full_compare(mrows, n, k):
+    """Whole-output comparison with the oracle under the stated bound, f32
+    and bf16 outputs consistent, bits run to run.  The last two shapes split
+    K into 64 and 79 k groups, so the reduction launch adds its partials in
+    several batches of loads (and the second one over a ragged column
+    block)."""
     say(f"bf16 decode gemm M={mrows} N={n} K={k}")
     a, b, a16, b16 = _inputs(mrows, n, k, seed=300 + mrows + n + k, wscale=0.02)
     c16 = ca.Buffer(mrows * n * 2)
