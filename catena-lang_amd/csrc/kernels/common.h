@@ -326,15 +326,25 @@ CATENA_DEV float serial_sum_wave_long(const float* s, uint32_t n) {
     float a = acc;
 #pragma unroll
     for (int k = 0; k < 32; ++k) a = a + v[k];
-#pragma unroll 1
-    for (uint32_t L = 1; L < nl; ++L) {
+    // lane L's 32 values after lane L-1's; eight lane blocks per loop
+    // iteration, so that a taken branch sits in the chain once per 256
+    // adds (2048 values: 11.4k -> 10.5k cycles)
+    auto block = [&]() {
       // a DPP read of a VGPR needs two wait states after the VALU write of
       // it; across the loop's back edge only the branch separates them
       asm volatile("s_nop 1");
       a = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x138, 0xF, 0xF, true)) + v[0];
 #pragma unroll
       for (int k = 1; k < 32; ++k) a = a + v[k];
+    };
+    uint32_t L = 1;
+#pragma unroll 1
+    for (; L + 8 <= nl; L += 8) {
+#pragma unroll
+      for (int r = 0; r < 8; ++r) block();
     }
+#pragma unroll 1
+    for (; L < nl; ++L) block();
     acc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), (int)(nl - 1)));
   }
   for (uint32_t t = n4; t < n; ++t) acc = acc + s[t];
