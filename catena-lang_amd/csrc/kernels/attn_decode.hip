@@ -17,11 +17,12 @@
 // lens[b] - (Tq - 1 - tq) positions.  Tq = 1 is the decode step.
 //
 // K pass: each wave takes 64-row blocks (blocks w, w+4, ...).  A block is
-// moved in four 32-wide d segments: a coalesced 16-byte-per-lane global load
-// (4 lanes per 64-byte row segment), a write into the wave's private LDS
-// slice, and a read back in which lane l owns row l, so every score is one
-// lane's d-ascending chain of v_mul_f32 + v_add_f32.  Two register sets keep
-// the next two segments' loads in flight while one is folded.
+// moved in two 64-wide d halves: a coalesced 16-byte-per-lane non-temporal
+// global load (8 lanes per 128-byte row half, so every request is a whole
+// 128-byte line), a write into the wave's private LDS slice, and a read back
+// in which lane l owns row l, so every score is one lane's d-ascending chain
+// of v_mul_f32 + v_add_f32.  Two register sets keep the next two halves'
+// loads in flight while one is folded.
 // Softmax: the max is the exact parallel form of the sequential fold (see
 // FirstMax in common.h); exp~ is elementwise; the denominator is the one
 // truly sequential fold and runs as one lane-to-lane chain in wave 0
@@ -36,15 +37,22 @@
 
 namespace {
 constexpr int D = 128;
-// K stage: per wave [64 rows][64 B]; 16-byte chunk c of row t sits at
-// position c ^ ((t >> 2) & 3).  Measured with SQ_LDS_BANK_CONFLICT on
-// gfx950, both the staging writes (4 lanes per row) and the read-back (lane
-// t: row t) are then conflict-free; the earlier 80-byte padded rows made
-// every staging write take 3x its LDS cycles.
-constexpr int KSTAGE_ROW = 64;
-constexpr int KSTAGE_WAVE = 64 * KSTAGE_ROW;  // 4096 B per wave
+// K stage: per wave [32 rows][128 B] (one d half of a 32-row block);
+// 16-byte chunk c of row t sits at position c ^ (t & 7) ^ ((t >> 3) & 1).
+// A staging write (8 rows x 128 B) puts its four even rows in banks 0-31 and
+// its four odd rows in banks 32-63; a read-back instruction (lane t: chunk c
+// of row t) covers all 64 banks with every 16 consecutive rows: both take
+// the minimum LDS cycles for their bytes.
+constexpr int KSTAGE_ROW = 128;
+constexpr int KSTAGE_WAVE = 32 * KSTAGE_ROW;  // 4096 B per wave
 constexpr int STAGE_BYTES = 4 * KSTAGE_WAVE;  // 16384 B (V pass uses 2 x 8192)
-CATENA_DEV uint32_t kswz(uint32_t row, uint32_t chunk) { return 16u * (chunk ^ ((row >> 2) & 3u)); }
+// Raw buffer descriptor word 3 (stride 0, bounds-checked by byte offset) and
+// the non-temporal cache policy of a load.
+constexpr int kRsrcWord3 = 0x00020000;
+constexpr int kCpolNt = 2;
+CATENA_DEV uint32_t kswz(uint32_t row, uint32_t chunk) {
+  return 16u * (chunk ^ (row & 7u) ^ ((row >> 3) & 1u));
+}
 
 CATENA_DEV void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -76,9 +84,11 @@ CATENA_DEV FirstMax wave_first_max(FirstMax a) {
 }
 }  // namespace
 
-// K-pass loads are plain (cached): each 128-byte line of K is read as two
-// 64-byte halves by consecutive steps, so the line must stay in L2 between
-// them (a non-temporal hint measured slower).
+// K and V are streamed with the non-temporal hint, always as whole 128-byte
+// lines per request: measured on gfx950, a plain read of 2 GiB runs at
+// 6.0-6.3 TB/s and a non-temporal one at 7.1-7.3 TB/s, but non-temporal
+// reads of 64-byte half lines in consecutive steps fetch the line twice
+// (5.2-5.7 TB/s).
 template <bool OUT_BF16>
 CATENA_DEV void attn_body(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                           const uint16_t* __restrict__ v, const uint32_t* __restrict__ lens,
@@ -93,7 +103,7 @@ CATENA_DEV void attn_body(const uint16_t* __restrict__ q, const uint16_t* __rest
   float* sp = reinterpret_cast<float*>(smem + D * 4 + STAGE_BYTES + 64);  // [L]
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint64_t qi = blockIdx.x;  // (b * Tq + tq) * H + h
   const uint32_t row = (uint32_t)(qi / H), h = (uint32_t)(qi % H);
   const uint32_t b = row / Tq, tq = row % Tq;
@@ -109,46 +119,53 @@ CATENA_DEV void attn_body(const uint16_t* __restrict__ q, const uint16_t* __rest
   __syncthreads();
 
   // ---------------------------------------------------------------- K pass
+  // Blocks of 32 rows, each moved as two 64-wide d halves (32 rows x 128 B:
+  // whole lines).  Lane l (and l + 32, which repeats its work) folds row l
+  // of the block; the K fold's VALU work is small beside the stream.
   {
     unsigned char* st = stage + wave * KSTAGE_WAVE;
-    const uint32_t nblk = (len + 63) / 64;
-    // this wave's (block, segment) steps, flattened
+    const uint32_t nblk = (len + 31) / 32;
+    // this wave's (block, half) steps, flattened
     const uint32_t my_blocks = nblk > (uint32_t)wave ? (nblk - wave + 3) / 4 : 0;
-    const uint32_t steps = my_blocks * 4;
-    const int lrow = lane >> 2, lchunk = lane & 3;
+    const uint32_t steps = my_blocks * 2;
+    const int lrow = lane >> 3, lchunk = lane & 7;
+    const uint32_t frow = (uint32_t)lane & 31u;
+    // the (b, h) slice's first len rows as a bounds-checked buffer: rows past
+    // len read as zeros without a branch around the load
+    const __amdgpu_buffer_rsrc_t krs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)kb, (short)0, (int)(len * (uint32_t)D * 2u), kRsrcWord3);
+    const int kvoff = lrow * D * 2 + lchunk * 16;
     auto gload = [&](uint32_t step, u32x4_t r[4]) {
-      const uint32_t blk = wave + 4 * (step >> 2), seg = step & 3;
+      const uint32_t blk = wave + 4 * (step >> 1), half = step & 1;
+      const int soff = (int)(blk * 32u * D * 2u + half * 128u);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t t = blk * 64 + lrow + 16 * i;
-        const u32x4_t* src =
-            reinterpret_cast<const u32x4_t*>(kb + (uint64_t)t * D + seg * 32 + lchunk * 8);
-        if (t < len)
-          r[i] = *src;
-        else
-          r[i] = u32x4_t{0u, 0u, 0u, 0u};
-      }
+      for (int i = 0; i < 4; ++i)
+        r[i] = __builtin_amdgcn_raw_buffer_load_b128(krs, kvoff, soff + i * 8 * D * 2, kCpolNt);
     };
-    // Two register sets: while segment `step` is folded, segments step+1 and
-    // step+2 are in flight.  steps is a multiple of 4, so the pair loop is exact.
+    // Two register sets: while half `step` is folded, halves step+1 and
+    // step+2 are in flight.  steps is even, so the pair loop is exact.
     u32x4_t ra[4], rb[4];
     if (steps > 0) gload(0, ra);
     if (steps > 1) gload(1, rb);
     float acc = __uint_as_float(0u);
     auto process = [&](uint32_t step, u32x4_t* r) {
-      const uint32_t seg = step & 3;
+      const uint32_t half = step & 1;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        *reinterpret_cast<u32x4_t*>(st + (lrow + 16 * i) * KSTAGE_ROW + kswz(lrow, lchunk)) = r[i];
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t srow = lrow + 8 * i;
+        *reinterpret_cast<u32x4_t*>(st + srow * KSTAGE_ROW + kswz(srow, lchunk)) = r[i];
+      }
       wave_sync();
       if (step + 2 < steps) gload(step + 2, r);
-      if (seg == 0) acc = __uint_as_float(0u);
-      const unsigned char* myrow = st + lane * KSTAGE_ROW;
-#pragma unroll
-      for (int ch = 0; ch < 4; ++ch) {
-        const u32x4_t kv = *reinterpret_cast<const u32x4_t*>(myrow + kswz(lane, ch));
-        const f32x4_t q0 = *reinterpret_cast<const f32x4_t*>(qf + seg * 32 + ch * 8);
-        const f32x4_t q1 = *reinterpret_cast<const f32x4_t*>(qf + seg * 32 + ch * 8 + 4);
+      if (half == 0) acc = __uint_as_float(0u);
+      const unsigned char* myrow = st + frow * KSTAGE_ROW;
+      // two chunks per iteration: the q and K reads of a whole half at once
+      // would not fit beside the register sets in flight
+#pragma unroll 2
+      for (int ch = 0; ch < 8; ++ch) {
+        const u32x4_t kv = *reinterpret_cast<const u32x4_t*>(myrow + kswz(frow, ch));
+        const f32x4_t q0 = *reinterpret_cast<const f32x4_t*>(qf + half * 64 + ch * 8);
+        const f32x4_t q1 = *reinterpret_cast<const f32x4_t*>(qf + half * 64 + ch * 8 + 4);
         float p;
         p = q0[0] * bf16lo(kv[0]); acc = acc + p;
         p = q0[1] * bf16hi(kv[0]); acc = acc + p;
@@ -159,8 +176,8 @@ CATENA_DEV void attn_body(const uint16_t* __restrict__ q, const uint16_t* __rest
         p = q1[2] * bf16lo(kv[3]); acc = acc + p;
         p = q1[3] * bf16hi(kv[3]); acc = acc + p;
       }
-      if (seg == 3) {
-        const uint32_t t = (wave + 4 * (step >> 2)) * 64 + lane;
+      if (half == 1 && lane < 32) {
+        const uint32_t t = (wave + 4 * (step >> 1)) * 32 + frow;
         if (t < len) sp[t] = acc * scale;
       }
       wave_sync();
