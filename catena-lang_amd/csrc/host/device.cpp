@@ -68,6 +68,7 @@ const KernelSpec kKernels[] = {
     {KernelId::GemmBf16DecodeSilu, "gemm_bf16_decode", "catena_gemm_bf16_decode_silu"},
     {KernelId::GemmBf16DecodeArgmax, "gemm_bf16_decode", "catena_gemm_bf16_decode_argmax"},
     {KernelId::GemmBf16DecodeParts, "gemm_bf16_decode", "catena_gemm_bf16_decode_parts"},
+    {KernelId::GemmBf16DecodePartsNt, "gemm_bf16_decode", "catena_gemm_bf16_decode_parts_nt"},
     {KernelId::ArgmaxCompose, "gemm_bf16_decode", "catena_argmax_compose"},
     {KernelId::DecodeReduce, "gemm_bf16_decode", "catena_decode_reduce"},
     {KernelId::AttnDecodeD128, "attn_decode", "catena_attn_decode_bf16_d128"},

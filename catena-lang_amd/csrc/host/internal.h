@@ -30,6 +30,7 @@ enum class KernelId : int {
   GemmBf16DecodeSilu,
   GemmBf16DecodeArgmax,
   GemmBf16DecodeParts,
+  GemmBf16DecodePartsNt,
   ArgmaxCompose,
   DecodeReduce,
   AttnDecodeD128,

@@ -163,10 +163,11 @@ int gemm_bf16_decode(const uint16_t* a, const uint16_t* b, void* c, uint64_t n, 
   void* args[] = {&X, &W, &Y, &P, &tickets, (void*)&M, &N, &K, (void*)&kw, &stream_lds, &e};
   if (lds > d.max_lds) return fail(CATENA_ERR_UNSUPPORTED, "decode GEMM needs %zu B of LDS", lds);
   if (S > 1 && (epi == DecodeEpilogue::StoreF32 || epi == DecodeEpilogue::StoreBf16)) {
-    // plain output: the partials kernel, then the reduction as a launch of
-    // its own (the same adds in the same order, ordered by the launch
-    // boundary instead of a completion ticket)
-    st = launch(KernelId::GemmBf16DecodeParts, dim3((unsigned)gx, (unsigned)S), dim3(256), lds, args);
+    // plain output: the partials kernel (W streamed non-temporally, as the
+    // plain-output kernels do), then the reduction as a launch of its own
+    // (the same adds in the same order, ordered by the launch boundary
+    // instead of a completion ticket)
+    st = launch(KernelId::GemmBf16DecodePartsNt, dim3((unsigned)gx, (unsigned)S), dim3(256), lds, args);
     if (st) return st;
     uint64_t part_elems = (uint64_t)M * m, n4 = part_elems / 4;
     uint32_t S32 = (uint32_t)S, bf16 = epi == DecodeEpilogue::StoreBf16 ? 1u : 0u;

@@ -237,7 +237,7 @@ CATENA_DEV void argmax_compose_rows(__amdgpu_buffer_rsrc_t ars, uint32_t M, uint
   }
 }
 
-template <int EPI>
+template <int EPI, int WAUX>
 CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __restrict__ W,
                             void* __restrict__ Y, float* __restrict__ P,
                             uint32_t* __restrict__ tickets, uint32_t M, uint64_t N, uint64_t K,
@@ -299,12 +299,15 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
     const uint32_t xr = lane >> 2, xq = (uint32_t)(lane & 3) ^ ((xr >> 1) & 3u);
     const bool xl = xr < M;
     const char* wsrc = reinterpret_cast<const char*>(W) + (kw0 * N + n0) * 2;
-    // The LM head (argmax epilogue) streams its weight, the largest tensor
-    // of a decode step and read once per step, with the non-temporal hint:
-    // measured in the C5 step, the Infinity Cache then keeps the block
-    // weights and the KV cache between steps (W_qkv 13.7 -> 12.4 us, W_down
-    // 12.0 -> 10.5 us, the LM head itself 31.2 -> 31.6 us).
-    constexpr int kWAux = EPI == EPI_ARGMAX ? 2 : 0;  // cache policy: nt
+    // W's cache policy (WAUX, 2 = non-temporal).  A non-temporal stream
+    // reads faster (a long read on gfx950: 7.1 against 6.1 TB/s; the C3
+    // shapes 21.2 -> 20.4 and 20.7 -> 19.3 us per call) but leaves nothing
+    // in the Infinity Cache: the plain-output kernels and the LM head
+    // (argmax), whose weights are read once, use it; the decode step's
+    // block projections do not, so that the cache keeps the block weights
+    // and the KV cache between steps (C5 decode step 94.6 us against 104.9
+    // with every weight stream non-temporal).
+    constexpr int kWAux = WAUX;
     auto issue_w = [&](uint32_t t, int slot) {  // slab t of this wave = k kw0 + 128 t
       unsigned char* st = ring + slot * STAGE_BYTES;
       const char* w = wsrc + (uint64_t)t * 128 * N * 2;
@@ -638,23 +641,26 @@ CATENA_DEV void decode_body(const uint16_t* __restrict__ X, const uint16_t* __re
 
 // grid = (ceil(N/128), S), block = 256.  KW = k per wave (multiple of 32).
 // tickets[ceil(N/128)] start at zero and are left at zero.
-#define CATENA_DECODE_KERNEL(NAME, EPI)                                                          \
+#define CATENA_DECODE_KERNEL(NAME, EPI, WAUX)                                                    \
   extern "C" __global__ __launch_bounds__(256) void NAME(                                        \
       const uint16_t* __restrict__ X, const uint16_t* __restrict__ W, void* __restrict__ Y,     \
       float* __restrict__ P, uint32_t* __restrict__ tickets, uint32_t M, uint64_t N, uint64_t K, \
       uint32_t KW, uint32_t stream_lds, DecodeEpi ep) {                                          \
-    decode_body<EPI>(X, W, Y, P, tickets, M, N, K, KW, stream_lds, ep);                          \
+    decode_body<EPI, WAUX>(X, W, Y, P, tickets, M, N, K, KW, stream_lds, ep);                    \
   }
 
-CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_f32out, EPI_STORE)
-CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_bf16out, EPI_STORE_BF16)
-CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_rope, EPI_ROPE)
-CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_silu, EPI_SILU)
-CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_argmax, EPI_ARGMAX)
-CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_parts, EPI_PARTIALS)
+// plain outputs (the decode GEMM entry point): W non-temporal
+CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_f32out, EPI_STORE, 2)
+CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_bf16out, EPI_STORE_BF16, 2)
+CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_parts_nt, EPI_PARTIALS, 2)
+// the decoder's step
+CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_rope, EPI_ROPE, 0)
+CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_silu, EPI_SILU, 0)
+CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_argmax, EPI_ARGMAX, 2)
+CATENA_DECODE_KERNEL(catena_gemm_bf16_decode_parts, EPI_PARTIALS, 0)
 
 // The split-K reduction of a plain decode GEMM, as a launch of its own after
-// the partials kernel (EPI_PARTIALS): Y = ((P[0] + P[1]) + ...) + P[S-1]
+// the partials kernel (catena_gemm_bf16_decode_parts_nt): Y = ((P[0] + P[1]) + ...) + P[S-1]
 // elementwise, ascending s -- the adds the last-arriving workgroup of the
 // ticketed form makes, so the same bits -- stored as f32 or as bf16 (RNE).
 // The launch boundary orders the partials before these loads, which takes
