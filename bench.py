@@ -479,7 +479,8 @@ def bench_ceilings(ev: HipEvents) -> dict:
     the measurement kernels in csrc/kernels/calibrate.hip (a code object the
     library itself never loads): bf16 MFMA throughput and clock on random
     operands (registers only, then fed from LDS at the bf16 GEMM's read
-    ratio), plain HBM read rate, and the 4096^2 bf16 C-store write rate."""
+    ratio), HBM read rate with plain and with non-temporal loads, and the
+    4096^2 bf16 C-store write rate."""
     hip = ctypes.CDLL("libamdhip64.so")
     vp = ctypes.c_void_p
 
@@ -537,6 +538,10 @@ def bench_ceilings(ev: HipEvents) -> dict:
                   [vp(src.ptr), ctypes.c_uint64(nbytes // 16 // rgrid), vp(flag.ptr), ctypes.c_uint32(0x12345678)])
     us = time_us(go, 5, 50)
     out["hbm_read"] = {"GB/s": round(nbytes / us / 1e3, 1), "bytes": nbytes, "us_per_launch": round(us, 2)}
+    go = launcher(kernel("catena_calib_read_nt"), rgrid, 512,
+                  [vp(src.ptr), ctypes.c_uint64(nbytes // 16 // rgrid), vp(flag.ptr), ctypes.c_uint32(0x12345678)])
+    us = time_us(go, 5, 50)
+    out["hbm_read_nt"] = {"GB/s": round(nbytes / us / 1e3, 1), "bytes": nbytes, "us_per_launch": round(us, 2)}
     del src
     cbytes = 4096 * 4096 * 2
     cbuf = ca.Buffer(cbytes)

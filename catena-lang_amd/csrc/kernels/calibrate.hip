@@ -10,6 +10,7 @@
 //                               ds_read_b64, two fragment sets alternating).
 //   catena_calib_read           plain HBM read, one contiguous chunk per
 //                               workgroup, four 16-byte loads in flight.
+//   catena_calib_read_nt        the same with non-temporal loads.
 //   catena_calib_write_tile     the 4096^2 bf16 GEMM's C store: 256 x 256
 //                               tiles, 128-byte rows, all workgroups at once.
 //
@@ -178,6 +179,22 @@ extern "C" __global__ __launch_bounds__(512) void catena_calib_read(const u32x4_
   const u32x4_t* p = src + (uint64_t)blockIdx.x * per_wg;
   for (uint64_t i = threadIdx.x; i + 1536 < per_wg; i += 2048) {
     const u32x4_t a = p[i], b = p[i + 512], c = p[i + 1024], d = p[i + 1536];
+    acc ^= a ^ b ^ c ^ d;
+  }
+  if ((acc[0] ^ acc[1] ^ acc[2] ^ acc[3]) == never) flag[0] = 1u;
+}
+
+// The same read with the non-temporal hint on every 16-byte load (whole
+// 128-byte lines per wave instruction): the rate the decode attention's K and
+// V streams and the plain decode GEMM's weight stream are built for.
+extern "C" __global__ __launch_bounds__(512) void catena_calib_read_nt(const u32x4_t* __restrict__ src,
+                                                                        uint64_t per_wg, uint32_t* flag,
+                                                                        uint32_t never) {
+  u32x4_t acc = {0u, 0u, 0u, 0u};
+  const u32x4_t* p = src + (uint64_t)blockIdx.x * per_wg;
+  for (uint64_t i = threadIdx.x; i + 1536 < per_wg; i += 2048) {
+    const u32x4_t a = __builtin_nontemporal_load(p + i), b = __builtin_nontemporal_load(p + i + 512),
+                  c = __builtin_nontemporal_load(p + i + 1024), d = __builtin_nontemporal_load(p + i + 1536);
     acc ^= a ^ b ^ c ^ d;
   }
   if ((acc[0] ^ acc[1] ^ acc[2] ^ acc[3]) == never) flag[0] = 1u;
