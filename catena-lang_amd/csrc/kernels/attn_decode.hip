@@ -54,6 +54,21 @@ CATENA_DEV uint32_t kswz(uint32_t row, uint32_t chunk) {
   return 16u * (chunk ^ (row & 7u) ^ ((row >> 3) & 1u));
 }
 
+// Wave priority p & 3 for the SQ's issue arbitration.  The workgroups of the
+// C4 grid that share a CU are blockIdx.x 256 apart; with one priority for
+// all, the oldest wins the memory-issue ties and they finish in dispatch
+// order (medians 258, 275, 288, 304 us), so the last CUs end late.  Each
+// workgroup's priority therefore rotates with its progress, offset by
+// blockIdx.x >> 8 (measured 323 -> 317 us; the same bits).
+CATENA_DEV void set_prio(uint32_t p) {
+  switch (p & 3u) {
+    case 0: __builtin_amdgcn_s_setprio(0); break;
+    case 1: __builtin_amdgcn_s_setprio(1); break;
+    case 2: __builtin_amdgcn_s_setprio(2); break;
+    default: __builtin_amdgcn_s_setprio(3); break;
+  }
+}
+
 CATENA_DEV void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -150,6 +165,7 @@ CATENA_DEV void attn_body(const uint16_t* __restrict__ q, const uint16_t* __rest
     float acc = __uint_as_float(0u);
     auto process = [&](uint32_t step, u32x4_t* r) {
       const uint32_t half = step & 1;
+      set_prio((uint32_t)(qi >> 8) + (step >> 1));
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const uint32_t srow = lrow + 8 * i;
@@ -263,6 +279,7 @@ CATENA_DEV void attn_body(const uint16_t* __restrict__ q, const uint16_t* __rest
     const uint32_t tr_j = (uint32_t)(lane & 15) >> 2;  // row within a group of 4
     const uint32_t tr_col = 16u * ((uint32_t)lane >> 4) + 4u * ((uint32_t)lane & 3);
     auto process = [&](uint32_t bt, u32x4_t* r) {
+      set_prio((uint32_t)(qi >> 8) + bt);
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         *reinterpret_cast<u32x4_t*>(vst + (vrow + 8 * i) * 128 + vchunk * 16) = r[i];
