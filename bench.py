@@ -583,7 +583,10 @@ def main(argv=None) -> int:
     ev = HipEvents(ca.stream())
     print("[bench] bf16 GEMM 4096^3", file=sys.stderr, flush=True)
     g = bench_gemm(args.steps, args.warmup, ev)
-    extra = {}
+    extra = {"roofline_traffic_source": "every roofline.traffic figure is read from "
+                                        "profiles/hbm_traffic.json (rocprofv3 FETCH_SIZE / WRITE_SIZE "
+                                        "passes of their own, scaled by a copy kernel of known size), "
+                                        "not measured in this run"}
     core = args.only in ("core", "all")
     dec = c1 = at = dg = None
     if args.only in ("decoder", "all"):
