@@ -95,6 +95,31 @@ def test_attention_full_shape_bitwise_and_run_to_run():
     _bitwise(got, want)
 
 
+def test_attention_many_pairs_ragged():
+    """1,028 (batch, head) pairs (more than four per CU): bitwise equal to
+    the oracle with ragged lengths around the 32-row K blocks and 64-row V
+    batches (0, 1, 31, 32, 33, 699 and 700 positions) and a NaN score."""
+    B, H, L = 4, 257, 700
+    lens = [0, 33, 699, 700]
+    rng = np.random.default_rng(17)
+    q16 = oracle.f32_to_bf16_bits_np(rng.normal(0, 1, (B, H, D)).astype(np.float32))
+    k32 = rng.normal(0, 1, (B, H, L, D)).astype(np.float32)
+    k32[2, 5, 300, 7] = np.nan
+    k16 = oracle.f32_to_bf16_bits_np(k32)
+    v16 = oracle.f32_to_bf16_bits_np(rng.normal(0, 1, (B, H, L, D)).astype(np.float32))
+    say("attention many pairs B=4 H=257 L=700")
+    qb, kb, vb = ca.Buffer.from_array(q16), ca.Buffer.from_array(k16), ca.Buffer.from_array(v16)
+    scale = float(np.float32(1.0 / math.sqrt(D)))
+    got = _run(qb, kb, vb, lens, B, H, L, scale)
+    want = oracle.attn_decode(q16, k16, v16, np.array(lens, np.uint32), scale)
+    _bitwise(got, want)
+    say("attention many pairs, lengths 1 / 31 / 32")
+    lens2 = [1, 31, 32, 700]
+    got2 = _run(qb, kb, vb, lens2, B, H, L, scale)
+    want2 = oracle.attn_decode(q16, k16, v16, np.array(lens2, np.uint32), scale)
+    _bitwise(got2, want2)
+
+
 def test_attention_program_abi():
     rt = ca.Runtime([])
     B, H, L = 2, 2, 50
