@@ -575,8 +575,8 @@ def main(argv=None) -> int:
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
-              "(the GEMM would shard by output columns and attention by (batch, head); "
-              "see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "(the GEMM would shard by output columns and attention by (batch, head)). "
+              "Run with --gpus 1.", file=sys.stderr)
         return 2
 
     ca.init(0)
