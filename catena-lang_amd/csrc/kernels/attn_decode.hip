@@ -16,11 +16,12 @@
 // its last Tq positions (causal): query tq attends to the first
 // lens[b] - (Tq - 1 - tq) positions.  Tq = 1 is the decode step.
 //
-// K pass: each wave takes 64-row blocks (blocks w, w+4, ...).  A block is
+// K pass: each wave takes 32-row blocks (blocks w, w+4, ...).  A block is
 // moved in two 64-wide d halves: a coalesced 16-byte-per-lane non-temporal
-// global load (8 lanes per 128-byte row half, so every request is a whole
-// 128-byte line), a write into the wave's private LDS slice, and a read back
-// in which lane l owns row l, so every score is one lane's d-ascending chain
+// buffer load (8 lanes per 128-byte row half, so every request is a whole
+// 128-byte line; rows past the sequence read as zeros), a write into the
+// wave's private LDS slice, and a read back in which lane l (and l + 32,
+// repeating it) owns row l, so every score is one lane's d-ascending chain
 // of v_mul_f32 + v_add_f32.  Two register sets keep the next two halves'
 // loads in flight while one is folded.
 // Softmax: the max is the exact parallel form of the sequential fold (see
