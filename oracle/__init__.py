@@ -49,6 +49,8 @@ def lib():
         L.or_round_to_u32.restype = ctypes.c_uint32
         L.or_exp_approx.argtypes = [ctypes.c_float]
         L.or_exp_approx.restype = ctypes.c_float
+        L.or_exp_approx_n.argtypes = [_f32p, _f32p, ctypes.c_uint64]
+        L.or_exp_approx_n.restype = None
         L.or_exp_approx_nonneg.argtypes = [ctypes.c_float]
         L.or_exp_approx_nonneg.restype = ctypes.c_float
         L.or_f32_to_bf16.argtypes = [ctypes.c_float]
@@ -112,8 +114,10 @@ def exp_approx(x: float) -> float:
 
 
 def exp_approx_vec(x: np.ndarray) -> np.ndarray:
-    f = lib().or_exp_approx
-    return np.array([f(float(v)) for v in np.asarray(x, np.float32).ravel()], np.float32)
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    y = np.empty_like(x)
+    lib().or_exp_approx_n(_p(x, _f32p), _p(y, _f32p), x.size)
+    return y
 
 
 def f32_to_bf16(x: np.ndarray) -> np.ndarray:

@@ -86,6 +86,11 @@ float or_exp_approx(float x) {
   return is_negative ? reciprocal : base;
 }
 
+/* or_exp_approx over an array (for sweeps: one call instead of n). */
+void or_exp_approx_n(const float *x, float *y, uint64_t n) {
+  for (uint64_t i = 0; i < n; ++i) y[i] = or_exp_approx(x[i]);
+}
+
 /* f32 -> bf16, round to nearest even.  NaN keeps its sign and top payload
  * bits and is forced quiet.  This conversion has no reference counterpart
  * (catena has no bf16, catena-lang/src/codegen/lower_types.rs:13-22); it is

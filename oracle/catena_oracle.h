@@ -18,13 +18,18 @@
  *   or_exp_approx         pinned: reference tolerance test
  *                         (tests/runtime.rs:742-761), closed-form specials
  *                         (exp~(0)=c0, k=128 -> inf, k=129 -> -0 bits),
- *                         libm relative-error bound over a dense sweep.
+ *                         libm relative-error bound over a dense sweep, and
+ *                         bitwise over all 2^32 inputs against an independent
+ *                         numpy float32 transcription of math.hex:148-199
+ *                         (tests/test_oracle_exp_sweep.py).
  *   or_softmax_f32        pinned: reference test (tests/runtime.rs:971-1009),
  *                         sum-to-one, permutation/shift invariants.
  *   or_fold_*_f32         pinned: reference known answers
  *                         (tests/cases/reducec.rs:50-90).
  *   or_f32_to_bf16        pinned: torch's RNE float->bfloat16 conversion.
- *   or_matmul_bf16_*      pinned: float64 error bound, exact integer cases.
+ *   or_matmul_bf16_*      pinned: bitwise or_matmul_f32_seq on exactly
+ *                         widened inputs (ragged shapes), float64 error
+ *                         bound, exact integer cases.
  *   or_attn_decode        pinned: float64 attention within the softmax
  *                         tolerance, brute-force composition of the pinned
  *                         pieces on tiny shapes, uniform-V / one-hot cases.
@@ -54,6 +59,7 @@ float or_bits_f32(uint32_t b);
 uint32_t or_round_to_u32(float x);
 float or_exp_approx_nonneg(float x);
 float or_exp_approx(float x);
+void or_exp_approx_n(const float *x, float *y, uint64_t n);
 uint16_t or_f32_to_bf16(float x);
 float or_bf16_to_f32(uint16_t h);
 

@@ -237,6 +237,27 @@ def test_bf16_gemm_integer_exact_and_bound():
     assert np.array_equal(sub32, c32[[5, 0, 7]])
 
 
+@pytest.mark.parametrize("n,m,k", [(1, 1, 1), (5, 3, 0), (7, 33, 129), (19, 64, 300),
+                                   (3, 200, 4096)])
+def test_bf16_gemm_is_f32_fold_on_widened_inputs(n, m, k):
+    """or_matmul_bf16_seq is defined as the pinned f32 fold (or_matmul_f32_seq:
+    k ascending from +0, separate * and +) on exactly widened inputs, then
+    RNE to bf16: bitwise, on ragged shapes and with N(0,1) data whose partial
+    sums round at almost every step (a wrong k order or a dropped term would
+    change the bits)."""
+    rng = np.random.default_rng(n * 7919 + m * 31 + k)
+    a = oracle.f32_to_bf16_bits_np(rng.normal(0, 1, (n, k)).astype(np.float32))
+    b = oracle.f32_to_bf16_bits_np(rng.normal(0, 1, (k, m)).astype(np.float32))
+    c32, c16 = oracle.matmul_bf16(a, b)
+    ref = oracle.matmul_f32(oracle.bf16_bits_to_f32(a), oracle.bf16_bits_to_f32(b))
+    assert np.array_equal(c32.view(np.uint32), ref.view(np.uint32))
+    assert np.array_equal(c16, oracle.f32_to_bf16_bits_np(ref))
+    if k >= 2:  # the k order matters for these inputs: reversing it changes bits
+        rev = oracle.matmul_f32(oracle.bf16_bits_to_f32(a)[:, ::-1].copy(),
+                                oracle.bf16_bits_to_f32(b)[::-1].copy())
+        assert not np.array_equal(rev.view(np.uint32), ref.view(np.uint32)) or k < 8
+
+
 # ---------------------------------------------------------------- attention
 def _rand_bf16(rng, shape, scale=1.0):
     return oracle.f32_to_bf16_bits_np((rng.normal(0, 1, shape) * scale).astype(np.float32))
