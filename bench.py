@@ -40,6 +40,8 @@ import catena_amd as ca  # noqa: E402
 METRIC = "det. bf16 GEMM TFLOP/s (%MFMA peak); KV-cache decode attention HBM GB/s"
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
+# non-packed, non-fused f32 VALU issue: 256 CUs x 64 lane-ops per clock x 2.4 GHz
+PEAK_VALU_F32_TFLOPS = 256 * 64 * 2.4e9 / 1e12
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
 
 
@@ -175,8 +177,14 @@ def bench_c1(steps: int, ev):
             "kernel_us": round(k_ms * 1e3, 3),
             "kernel_GFLOP/s": round(flop / (k_ms * 1e-3) / 1e9, 1),
             "bitwise_run_to_run": len(hashes) == 1,
-            "roofline": None,
-            "bound": "neither (plumbing and parity: 33.5 Mflop, 786 KB)",
+            "roofline": {"bound": "valu", "achieved": round(flop / (k_ms * 1e-3) / 1e12, 3),
+                         "peak": PEAK_VALU_F32_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(flop / (k_ms * 1e-3) / 1e12 / PEAK_VALU_F32_TFLOPS, 4),
+                         "traffic": None,
+                         "work": "2 flop per multiply-add, each one VALU lane-op (v_mul_f32 then "
+                                 "v_add_f32: the reference's separately rounded chain, no packed or "
+                                 "fused ops); peak = 256 CUs x 64 f32 lane-ops per clock x 2.4 GHz"},
+            "bound": "VALU issue (33.5 Mflop, 786 KB: far below HBM time)",
             "inputs": (a.read(np.float32, (n, k)), b.read(np.float32, (k, m)), got)}
 
 

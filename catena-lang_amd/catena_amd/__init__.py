@@ -130,6 +130,7 @@ SIGNATURES = {
     "catena_mi355x_attn_decode_bf16": (_int, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _f32]),
     "catena_mi355x_softmax_f32": (_int, [_vp, _vp, _u64, _u64]),
     "catena_mi355x_exp_approx_f32": (_int, [_vp, _vp, _u64]),
+    "catena_mi355x_map_f32": (_int, [_u32, _vp, _vp, _u64]),
     "catena_mi355x_fill_normal_bf16": (_int, [_vp, _u64, _u64, _u64, _f32]),
     "catena_mi355x_fill_uniform_f32": (_int, [_vp, _u64, _u64, _u64]),
     "catena_mi355x_copy_bytes": (_int, [_vp, _vp, _u64]),
@@ -172,6 +173,12 @@ SIGNATURES = {
     "program_matmul_left_identity_2x2_via_mem": (None, [Mem, _u64, _u64, ctypes.POINTER(Mem)]),
     "program_nn_softmax": (None, [Mem, ctypes.POINTER(Mem)]),
     "program_math_exp_approx": (None, [_f32, ctypes.POINTER(_f32)]),
+    "program_math_sqrt": (None, [_f32, ctypes.POINTER(_f32)]),
+    "program_nn_sigmoid": (None, [_f32, ctypes.POINTER(_f32)]),
+    "program_nn_silu": (None, [_f32, ctypes.POINTER(_f32)]),
+    "program_math_sin_approx": (None, [_f32, ctypes.POINTER(_f32)]),
+    "program_math_cos_approx": (None, [_f32, ctypes.POINTER(_f32)]),
+    "program_math_sin_approx_full": (None, [_f32, ctypes.POINTER(_f32)]),
     "program_bf16_matmul_via_mem": (None, [Mem, Mem] + [_u64] * 6 + [ctypes.POINTER(Mem)]),
     "program_attn_decode_via_mem": (None, [Mem, Mem, Mem, Mem] + [_u64] * 4 + [_f32, ctypes.POINTER(Mem)]),
     "catena_runtime_from_sources": (_int, [ctypes.POINTER(ctypes.c_char_p), ctypes.c_size_t,
@@ -345,6 +352,16 @@ def softmax_f32(x, y, rows: int, n: int) -> None:
 
 def exp_approx_f32(x, y, n: int) -> None:
     check(lib().catena_mi355x_exp_approx_f32(_p(x), _p(y), n))
+
+
+# catena_map_op_t
+(MAP_EXP_APPROX, MAP_SQRT, MAP_SIGMOID, MAP_SILU, MAP_SIN_APPROX, MAP_COS_APPROX,
+ MAP_SIN_APPROX_FULL) = range(7)
+
+
+def map_f32(op: int, x, y, n: int) -> None:
+    """A scalar stdlib program elementwise (catena_mi355x_map_f32)."""
+    check(lib().catena_mi355x_map_f32(op, _p(x), _p(y), n))
 
 
 def fill_normal_bf16(out, n: int, seed: int, stream_id: int, scale: float = 1.0) -> None:

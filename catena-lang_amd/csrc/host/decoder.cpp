@@ -30,6 +30,10 @@ struct catena_decoder {
   // rebuilt before a forward when the embedding may have changed
   void* embed_norm = nullptr;
   bool embed_norm_stale = true;
+  // set once decoder_tensor has handed out the embedding: the caller may
+  // write through that handle at any time, so from then on every prefill
+  // and generate call rebuilds the table first
+  bool embed_exposed = false;
   void* w_lm = nullptr;
   void* inv_freq = nullptr;
   void* rope_tab = nullptr;  // [max_len][head_dim / 2][2] f32: (cos, sin) per position and pair
@@ -462,6 +466,7 @@ int catena_mi355x_decoder_tensor(catena_decoder_t* dec, uint32_t which, uint32_t
       // normalized table before the next forward
       *out = {m.embed, (uint64_t)c.vocab * d * 2};
       m.embed_norm_stale = true;
+      m.embed_exposed = true;
       break;
     case CATENA_DEC_EMBED_NORM: *out = {m.embed_norm, ((uint64_t)c.vocab + 1) * d * 2}; break;
     case CATENA_DEC_W_QKV: *out = {m.w_qkv[layer], d * 3 * d * 2}; break;
@@ -515,6 +520,7 @@ int catena_mi355x_decoder_prefill(catena_decoder_t* dec, const uint32_t* tokens,
   if (t == 0 || t > c.max_len)
     return fail(CATENA_ERR_INVALID_ARGUMENT, "prefill length %u outside 1..%u", t, c.max_len);
   Device& dv = device();
+  if (m.embed_exposed) m.embed_norm_stale = true;
   // the staging buffer is pinned, so the copy below reads it when the stream
   // reaches it: wait for the previous prefill's copy before rewriting it
   if (m.rows_pending) TRY(hip_check(hipEventSynchronize(m.rows_copied), "hipEventSynchronize"));
@@ -546,6 +552,7 @@ int catena_mi355x_decoder_generate(catena_decoder_t* dec, uint32_t steps, uint32
     return fail(CATENA_ERR_INVALID_ARGUMENT, "%u steps after %u positions overflow the %u-position cache",
                 steps, m.cur_len, c.max_len);
   if (steps == 0) return CATENA_OK;
+  if (m.embed_exposed) m.embed_norm_stale = true;
   const uint32_t B = m.batch;
   // Each step's argmax is composed by the next step's first GEMM, from the
   // LM head's column-block summaries (the LM head then ends without its

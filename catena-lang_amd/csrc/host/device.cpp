@@ -52,6 +52,7 @@ struct KernelSpec {
 
 const KernelSpec kKernels[] = {
     {KernelId::GemmF32Exact, "gemm_f32_exact", "catena_gemm_f32_exact"},
+    {KernelId::GemmF32ExactT16, "gemm_f32_exact", "catena_gemm_f32_exact_t16"},
     {KernelId::GemmBf16EdgeBf16, "gemm_bf16", "catena_gemm_bf16_edge_bf16out"},
     {KernelId::GemmBf16EdgeF32, "gemm_bf16", "catena_gemm_bf16_edge_f32out"},
     {KernelId::GemmBf16LdsBf16, "gemm_bf16_lds", "catena_gemm_bf16_lds_bf16out"},
@@ -92,6 +93,7 @@ const KernelSpec kKernels[] = {
     {KernelId::SumRowsU64, "tensor", "catena_sum_rows_u64"},
     {KernelId::SoftmaxRows, "softmax", "catena_softmax_rows_f32"},
     {KernelId::ExpApprox, "softmax", "catena_exp_approx_f32"},
+    {KernelId::MapF32, "softmax", "catena_map_f32"},
     {KernelId::FillNormalBf16, "fill", "catena_fill_normal_bf16"},
     {KernelId::FillUniformF32, "fill", "catena_fill_uniform_f32"},
     {KernelId::Copy16, "fill", "catena_copy_16b"},

@@ -14,6 +14,7 @@ namespace catena {
 
 enum class KernelId : int {
   GemmF32Exact = 0,
+  GemmF32ExactT16,  // 16x16 tiles for small outputs (gemm_f32_exact.hip)
   GemmBf16EdgeBf16,  // general shapes, bounds-checked (gemm_bf16.hip)
   GemmBf16EdgeF32,
   GemmBf16LdsBf16,  // aligned tiles with K % 128 != 0: two 64-k stages (gemm_bf16_lds.hip)
@@ -54,6 +55,7 @@ enum class KernelId : int {
   SumRowsU64,
   SoftmaxRows,
   ExpApprox,
+  MapF32,
   FillNormalBf16,
   FillUniformF32,
   Copy16,

@@ -247,9 +247,16 @@ int catena_mi355x_gemm_f32_exact(const float* a, const float* b, float* c, uint6
   if (st) return st;
   if (n == 0 || m == 0) return CATENA_OK;
   if (!c || (k > 0 && (!a || !b))) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
-  const uint64_t gx = ceil_div(m, 64), gy = ceil_div(n, 64);
-  if (gx > 0x7FFFFFFFu || gy > 65535u) return fail(CATENA_ERR_UNSUPPORTED, "matrix too large");
   void* args[] = {&a, &b, &c, &n, &m, &k};
+  // 64x64 tiles (16 cells per thread) unless they would leave CUs idle; then
+  // 16x16 tiles (one cell per thread).  Every cell is the same k-ascending
+  // chain in both, so the choice never changes the bits.
+  const uint64_t gx = ceil_div(m, 64), gy = ceil_div(n, 64);
+  if (gx * gy < kDecodeSpread) {
+    const uint64_t sx = ceil_div(m, 16), sy = ceil_div(n, 16);
+    return launch(KernelId::GemmF32ExactT16, dim3((unsigned)sx, (unsigned)sy), dim3(256), 0, args);
+  }
+  if (gx > 0x7FFFFFFFu || gy > 65535u) return fail(CATENA_ERR_UNSUPPORTED, "matrix too large");
   return launch(KernelId::GemmF32Exact, dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, args);
 }
 
@@ -391,6 +398,18 @@ int catena_mi355x_exp_approx_f32(const float* x, float* y, uint64_t n) {
   if (g > 0x7FFFFFFFull) return fail(CATENA_ERR_UNSUPPORTED, "too many elements");
   void* args[] = {&x, &y, &n};
   return launch(KernelId::ExpApprox, dim3((unsigned)g), dim3(256), 0, args);
+}
+
+int catena_mi355x_map_f32(uint32_t op, const float* x, float* y, uint64_t n) {
+  if (op > CATENA_MAP_SIN_APPROX_FULL) return fail(CATENA_ERR_INVALID_ARGUMENT, "unknown map op %u", op);
+  int st = ensure_init();
+  if (st) return st;
+  if (n == 0) return CATENA_OK;
+  if (!x || !y) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
+  const uint64_t g = ceil_div(n, 256);
+  if (g > 0x7FFFFFFFull) return fail(CATENA_ERR_UNSUPPORTED, "too many elements");
+  void* args[] = {&x, &y, &n, &op};
+  return launch(KernelId::MapF32, dim3((unsigned)g), dim3(256), 0, args);
 }
 
 int catena_mi355x_fill_normal_bf16(uint16_t* out, uint64_t n, uint64_t seed, uint64_t stream,

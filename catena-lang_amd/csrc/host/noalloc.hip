@@ -14,20 +14,22 @@
 // noalloc_setup, with the device current) looks up the array's device
 // address once per device with hipGetSymbolAddress, and the entry point
 // passes that address to the kernels.  Every call on a device shares that
-// device's array: calls that overlap on one device race.  The completion
-// counters the split-K hand-off uses live in the block catena_mi355x_init
-// zeroes once; each call returns them to zero.  The partials need no clearing
-// (every one is written before it is read).
+// device's array: calls that overlap on one device race.  With a k split the
+// plain-output path writes every workgroup's f32 partial to the array and a
+// second launch adds them (ascending k group): no completion counters, and
+// the partials need no clearing (every one is written before it is read).
+// Shapes whose partials exceed the array are refused before any launch
+// (catena_mi355x_gemm_bf16_decode_plan reports the partials' size).
 #include <hip/hip_runtime.h>
 
 #include "internal.h"
 
 namespace catena {
 namespace {
-// Largest split-K partial set the decode kernel forms for n <= 16: at most
-// 256 column blocks x k groups of 128 columns each on the streaming path
-// (2 MiB of f32 partials at 16 rows) and ~384 x 128 on the register path
-// (3 MiB), so 4 MiB covers every shape.
+// Partials of S k groups x n rows x m columns (f32).  The k split spreads
+// about 256 workgroups, so most decode shapes stay near 2 MiB at 16 rows,
+// but the rounding of the split can exceed 4 MiB (16 x 24224 x 2056 needs
+// 4.4 MiB): such shapes are refused.
 constexpr uint64_t kScratchBytes = 4ull << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 

@@ -68,6 +68,17 @@ catena_mem_t identity_f32(uint64_t n) {
   return m;
 }
 
+// A scalar (f32) -> (f32) program on the device: the value goes up, one
+// thread applies the op, the result comes back.
+void scalar_map(uint32_t op, float x, float* out, const char* what) {
+  catena_mem_t buf = alloc_out(8);
+  check(catena_mem_write(buf, 0, &x, 4), "upload");
+  float* p = static_cast<float*>(buf.data);
+  check(catena_mi355x_map_f32(op, p, p + 1, 1), what);
+  check(catena_mem_read(buf, 4, out, 4), "download");
+  catena_mem_free(&buf);
+}
+
 void matmul_f32_mem(const void* a, const void* b, uint64_t n, uint64_t m, uint64_t k,
                     catena_mem_t* out) {
   catena_mem_t c = alloc_out(mul_or_trap(mul_or_trap(n, m), 4));
@@ -129,6 +140,19 @@ void program_math_exp_approx(float x, float* out) {
   check(catena_mi355x_exp_approx_f32(p, p + 1, 1), "math.exp-approx");
   check(catena_mem_read(buf, 4, out, 4), "download");
   catena_mem_free(&buf);
+}
+
+void program_math_sqrt(float x, float* out) { scalar_map(CATENA_MAP_SQRT, x, out, "math.sqrt"); }
+void program_nn_sigmoid(float x, float* out) { scalar_map(CATENA_MAP_SIGMOID, x, out, "nn.sigmoid"); }
+void program_nn_silu(float x, float* out) { scalar_map(CATENA_MAP_SILU, x, out, "nn.silu"); }
+void program_math_sin_approx(float x, float* out) {
+  scalar_map(CATENA_MAP_SIN_APPROX, x, out, "math.sin-approx");
+}
+void program_math_cos_approx(float x, float* out) {
+  scalar_map(CATENA_MAP_COS_APPROX, x, out, "math.cos-approx");
+}
+void program_math_sin_approx_full(float x, float* out) {
+  scalar_map(CATENA_MAP_SIN_APPROX_FULL, x, out, "math.sin-approx-full");
 }
 
 void program_bf16_matmul_via_mem(catena_mem_t a, catena_mem_t b, uint64_t n, uint64_t m,

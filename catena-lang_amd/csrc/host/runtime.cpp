@@ -8,8 +8,9 @@
 // has no front end (out of scope) and instead binds source programs BY NAME
 // to native lowerings, checking the kinds of the declared type against the
 // lowering's signature.  The stdlib programs on and around the hot path
-// (nn.softmax, math.exp-approx, nn.rmsnorm, tensor.*, sum-f32, mean-f32,
-// max-f32) and this build's new programs are built in; user sources declare
+// (nn.softmax, math.exp-approx, math.sqrt, nn.sigmoid, nn.silu,
+// math.sin-approx(-full), math.cos-approx, nn.rmsnorm, tensor.*, sum-f32,
+// mean-f32, max-f32) and this build's new programs are built in; user sources declare
 // the rest (e.g. matmul-2x2-via-mem, sum-u64, dot-u64).
 #include <cctype>
 #include <cstring>
@@ -67,6 +68,13 @@ void inv_softmax(const catena_value_t* in, catena_value_t* out) {
 void inv_exp(const catena_value_t* in, catena_value_t* out) {
   float r;
   program_math_exp_approx(in[0].as.f32, &r);
+  out[0].kind = kF32;
+  out[0].as.f32 = r;
+}
+template <void (*Program)(float, float*)>
+void inv_scalar(const catena_value_t* in, catena_value_t* out) {
+  float r;
+  Program(in[0].as.f32, &r);
   out[0].kind = kF32;
   out[0].as.f32 = r;
 }
@@ -157,6 +165,12 @@ const std::vector<Lowering>& lowerings() {
       {"matmul-left-identity-2x2-via-mem", false, {kMem, kU64, kU64}, {kMem}, inv_left_id},
       {"nn.softmax", true, {kMem}, {kMem}, inv_softmax},
       {"math.exp-approx", true, {kF32}, {kF32}, inv_exp},
+      {"math.sqrt", true, {kF32}, {kF32}, inv_scalar<program_math_sqrt>},
+      {"nn.sigmoid", true, {kF32}, {kF32}, inv_scalar<program_nn_sigmoid>},
+      {"nn.silu", true, {kF32}, {kF32}, inv_scalar<program_nn_silu>},
+      {"math.sin-approx", true, {kF32}, {kF32}, inv_scalar<program_math_sin_approx>},
+      {"math.cos-approx", true, {kF32}, {kF32}, inv_scalar<program_math_cos_approx>},
+      {"math.sin-approx-full", true, {kF32}, {kF32}, inv_scalar<program_math_sin_approx_full>},
       {"nn.rmsnorm", true, {kMem}, {kMem}, inv_rmsnorm},
       {"tensor.argmax-f32", true, {kMem}, {kU64}, inv_argmax},
       {"tensor.broadcast-f32", true, {kF32, kU64}, {kMem}, inv_broadcast},

@@ -88,3 +88,115 @@ extern "C" __global__ __launch_bounds__(256) void catena_gemm_f32_exact(
     }
   }
 }
+
+// The same contraction for small outputs, where 64x64 tiles would leave most
+// CUs idle (256^3 is 16 tiles of 64x64 on a 256-CU device): a 16x16 output
+// tile per workgroup of 256 threads, one cell per thread, so 256^3 launches
+// 256 workgroups.  A 16-row x 128-k slab of A and a 128-k x 16-column slab of
+// B are staged in LDS k-contiguous per row / per column ([row][k] and
+// [col][k], rows padded by 4 floats), so each thread reads the next four k
+// values of its row and of its column with one 16-byte read each.  Every
+// global load is issued unconditionally from an in-range address (element 0
+// stands in for one past the edge, and its value is replaced by 0), so the
+// slab's 16 loads per thread are in flight together, and the next slab is
+// requested into registers before the current one is folded.  The cell's
+// chain is the one above: acc = +0, then for kk ascending
+// acc = acc + fl(A[i,kk] * B[kk,j]), separately rounded -- bitwise the same
+// result as the 64x64 instance and the reference.
+namespace {
+constexpr int S_T = 16, S_K = 128, S_PAD = 4;
+
+struct Slab {
+  float a[8], b[8];
+  uint32_t live;  // bit e: a[e] in range, bit 8 + e: b[e] in range
+};
+
+// thread tid's share of the slab at k0: A row tid / 16, k 8 (tid % 16) .. +7;
+// B k (tid + 256 e) / 16, column (tid + 256 e) % 16 for e = 0 .. 7.  The
+// out-of-range values are zeroed when the slab is stored, not here, so no
+// instruction waits on the loads until then.
+CATENA_DEV void load_slab(Slab& sl, const float* __restrict__ A, const float* __restrict__ B,
+                          uint64_t n, uint64_t m, uint64_t k, uint64_t row0, uint64_t col0,
+                          uint64_t k0, int tid) {
+  const int r = tid / 16, q = tid % 16;
+  const uint64_t gi = row0 + r;
+  uint32_t live = 0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint64_t kk = k0 + 8 * q + e;
+    const bool ok = gi < n && kk < k;
+    sl.a[e] = A[ok ? gi * k + kk : 0];
+    live |= (ok ? 1u : 0u) << e;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int idx = tid + 256 * e;
+    const uint64_t kk = k0 + idx / S_T, gj = col0 + idx % S_T;
+    const bool ok = gj < m && kk < k;
+    sl.b[e] = B[ok ? kk * m + gj : 0];
+    live |= (ok ? 1u : 0u) << (8 + e);
+  }
+  sl.live = live;
+}
+
+CATENA_DEV float live_or_zero(float v, uint32_t live, int bit) {
+  return (live >> bit) & 1u ? v : 0.0f;
+}
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(256) void catena_gemm_f32_exact_t16(
+    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
+    uint64_t n, uint64_t m, uint64_t k) {
+  __shared__ __align__(16) float As[S_T][S_K + S_PAD];
+  __shared__ __align__(16) float Bs[S_T][S_K + S_PAD];
+
+  const int tid = threadIdx.x;
+  const int tx = tid % S_T;  // column of the cell
+  const int ty = tid / S_T;  // row of the cell
+  const uint64_t row0 = (uint64_t)blockIdx.y * S_T;
+  const uint64_t col0 = (uint64_t)blockIdx.x * S_T;
+
+  float acc = __uint_as_float(0u);
+  Slab sl;
+  if (k > 0) load_slab(sl, A, B, n, m, k, row0, col0, 0, tid);
+  for (uint64_t k0 = 0; k0 < k; k0 += S_K) {
+    const int kt = (k - k0) < (uint64_t)S_K ? (int)(k - k0) : S_K;
+    {
+      const int r = tid / 16, q = tid % 16;
+      float a[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) a[e] = live_or_zero(sl.a[e], sl.live, e);
+      *reinterpret_cast<float4*>(&As[r][8 * q]) = make_float4(a[0], a[1], a[2], a[3]);
+      *reinterpret_cast<float4*>(&As[r][8 * q + 4]) = make_float4(a[4], a[5], a[6], a[7]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int idx = tid + 256 * e;
+        Bs[idx % S_T][idx / S_T] = live_or_zero(sl.b[e], sl.live, 8 + e);
+      }
+    }
+    __syncthreads();
+    if (k0 + S_K < k) load_slab(sl, A, B, n, m, k, row0, col0, k0 + S_K, tid);
+    // only the kt live k values enter the chain, in ascending order
+    int kk = 0;
+#pragma unroll 4
+    for (; kk + 4 <= kt; kk += 4) {
+      const float4 a = *reinterpret_cast<const float4*>(&As[ty][kk]);
+      const float4 b = *reinterpret_cast<const float4*>(&Bs[tx][kk]);
+      float prod = a.x * b.x;
+      acc = acc + prod;
+      prod = a.y * b.y;
+      acc = acc + prod;
+      prod = a.z * b.z;
+      acc = acc + prod;
+      prod = a.w * b.w;
+      acc = acc + prod;
+    }
+    for (; kk < kt; ++kk) {
+      const float prod = As[ty][kk] * Bs[tx][kk];
+      acc = acc + prod;
+    }
+    __syncthreads();
+  }
+  const uint64_t gi = row0 + ty, gj = col0 + tx;
+  if (gi < n && gj < m) C[gi * m + gj] = acc;
+}

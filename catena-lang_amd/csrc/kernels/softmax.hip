@@ -1,4 +1,4 @@
-// nn.softmax and math.exp-approx as device kernels.
+// nn.softmax, math.exp-approx and the scalar stdlib maps as device kernels.
 //
 // nn.softmax (catena-lang/stdlib/nn.hex:93-122) over each of `rows` f32
 // vectors of length n:
@@ -93,4 +93,32 @@ extern "C" __global__ __launch_bounds__(256) void catena_exp_approx_f32(
     const float* __restrict__ x, float* __restrict__ y, uint64_t n) {
   const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
   if (i < n) y[i] = exp_approx(x[i]);
+}
+
+// The scalar stdlib programs applied elementwise, one device function each
+// (common.h), selected by `op` (catena_map_op_t; uniform across the grid):
+//   0 math.exp-approx       catena-lang/stdlib/math.hex:185-199
+//   1 math.sqrt             catena-lang/stdlib/math.hex:235-272
+//   2 nn.sigmoid            catena-lang/stdlib/nn.hex:1-12
+//   3 nn.silu               catena-lang/stdlib/nn.hex:15-21
+//   4 math.sin-approx       catena-lang/stdlib/math.hex:1-23
+//   5 math.cos-approx       catena-lang/stdlib/math.hex:25-47
+//   6 math.sin-approx-full  catena-lang/stdlib/math.hex:49-103
+// The host rejects any other op before the launch.
+extern "C" __global__ __launch_bounds__(256) void catena_map_f32(
+    const float* __restrict__ x, float* __restrict__ y, uint64_t n, uint32_t op) {
+  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float v = x[i];
+  float r;
+  switch (op) {
+    case 0: r = exp_approx(v); break;
+    case 1: r = sqrt_newton(v); break;
+    case 2: r = sigmoid_approx(v); break;
+    case 3: r = silu_approx(v); break;
+    case 4: r = sin_taylor(v); break;
+    case 5: r = cos_taylor(v); break;
+    default: r = sin_full(v); break;
+  }
+  y[i] = r;
 }

@@ -169,6 +169,20 @@ int catena_mi355x_softmax_f32(const float *x, float *y, uint64_t rows, uint64_t 
 /* math.exp-approx elementwise (catena-lang/stdlib/math.hex:185-199). */
 int catena_mi355x_exp_approx_f32(const float *x, float *y, uint64_t n);
 
+/* The scalar stdlib programs elementwise, bitwise the reference's op order
+ * (each is one generated __host__ __device__ function in the reference,
+ * rendered from these hexpr sources).  y may equal x. */
+typedef enum catena_map_op {
+  CATENA_MAP_EXP_APPROX = 0,     /* math.exp-approx, catena-lang/stdlib/math.hex:185-199 */
+  CATENA_MAP_SQRT = 1,           /* math.sqrt, catena-lang/stdlib/math.hex:235-272 */
+  CATENA_MAP_SIGMOID = 2,        /* nn.sigmoid, catena-lang/stdlib/nn.hex:1-12 */
+  CATENA_MAP_SILU = 3,           /* nn.silu, catena-lang/stdlib/nn.hex:15-21 */
+  CATENA_MAP_SIN_APPROX = 4,     /* math.sin-approx, catena-lang/stdlib/math.hex:1-23 */
+  CATENA_MAP_COS_APPROX = 5,     /* math.cos-approx, catena-lang/stdlib/math.hex:25-47 */
+  CATENA_MAP_SIN_APPROX_FULL = 6 /* math.sin-approx-full, catena-lang/stdlib/math.hex:49-103 */
+} catena_map_op_t;
+int catena_mi355x_map_f32(uint32_t op, const float *x, float *y, uint64_t n);
+
 /* Seeded synthetic inputs (counter-based splitmix64; see fill.hip). */
 int catena_mi355x_fill_normal_bf16(uint16_t *out, uint64_t n, uint64_t seed, uint64_t stream,
                                    float scale);
@@ -295,6 +309,20 @@ void program_matmul_left_identity_2x2_via_mem(catena_mem_t a, uint64_t n, uint64
 void program_nn_softmax(catena_mem_t x, catena_mem_t *out);
 /* catena-lang/stdlib/math.hex:185-199 "math.exp-approx": (f32) -> (f32). */
 void program_math_exp_approx(float x, float *out);
+/* The scalar stdlib programs, (f32) -> (f32) each, as the reference's
+ * generated module exports them (catena-lang/src/codegen/gpu.rs:235-285):
+ *   "math.sqrt"            catena-lang/stdlib/math.hex:235-272
+ *   "nn.sigmoid"           catena-lang/stdlib/nn.hex:1-12
+ *   "nn.silu"              catena-lang/stdlib/nn.hex:15-21
+ *   "math.sin-approx"      catena-lang/stdlib/math.hex:1-23
+ *   "math.cos-approx"      catena-lang/stdlib/math.hex:25-47
+ *   "math.sin-approx-full" catena-lang/stdlib/math.hex:49-103 */
+void program_math_sqrt(float x, float *out);
+void program_nn_sigmoid(float x, float *out);
+void program_nn_silu(float x, float *out);
+void program_math_sin_approx(float x, float *out);
+void program_math_cos_approx(float x, float *out);
+void program_math_sin_approx_full(float x, float *out);
 /* bf16 analogue of matmul-2x2-via-mem (no reference counterpart):
  * (mem A bf16, mem B bf16, n, m, k, nk, km, nm) -> (mem C bf16). */
 void program_bf16_matmul_via_mem(catena_mem_t a, catena_mem_t b, uint64_t n, uint64_t m,
@@ -390,9 +418,11 @@ typedef enum catena_decoder_tensor {
   CATENA_DEC_LOGITS,    /* [batch][vocab] f32 */
   CATENA_DEC_LENS,      /* [batch] u32: cache positions per sequence */
   /* [vocab + 1][d] bf16: bf16(rmsnorm(widen(embed[t]))) for every token t,
-   * row vocab all NaN (the row of a token out of range); rebuilt before the
-   * next forward whenever the embedding may have changed (a
-   * decoder_tensor(CATENA_DEC_EMBED) call, init_weights).  A decode step
+   * row vocab all NaN (the row of a token out of range); rebuilt by
+   * init_weights and, once decoder_tensor(CATENA_DEC_EMBED) has handed out
+   * the embedding (which the caller may then write through at any time), at
+   * the start of every prefill and generate call (one pass over vocab rows
+   * per call, not per step).  A decode step
    * gathers layer 0's normalized input from it, so in a decode step layer
    * 0 writes neither CATENA_DEC_X nor CATENA_DEC_XN. */
   CATENA_DEC_EMBED_NORM,

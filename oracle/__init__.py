@@ -78,6 +78,8 @@ def lib():
                      "or_sin_full", "or_cos_full"):
             getattr(L, name).argtypes = [ctypes.c_float]
             getattr(L, name).restype = ctypes.c_float
+        L.or_map_f32.argtypes = [ctypes.c_int, _f32p, _f32p, ctypes.c_uint64]
+        L.or_map_f32.restype = None
         L.or_rmsnorm_f32.argtypes = [_f32p, _f32p, ctypes.c_uint64]
         L.or_rmsnorm_f32.restype = None
         L.or_argmax_f32.argtypes = [_f32p, ctypes.c_uint64]
@@ -214,6 +216,18 @@ def scalar(name: str, x: float) -> float:
 def scalar_vec(name: str, x: np.ndarray) -> np.ndarray:
     f = getattr(lib(), "or_" + name)
     return np.array([f(float(v)) for v in np.asarray(x, np.float32).ravel()], np.float32)
+
+
+MAP_OPS = {"exp_approx": 0, "sqrt_newton": 1, "sigmoid": 2, "silu": 3, "sin_approx": 4,
+           "cos_approx": 5, "sin_full": 6}
+
+
+def map_f32(name: str, x: np.ndarray) -> np.ndarray:
+    """A scalar program over an array (or_map_f32; name as in MAP_OPS)."""
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    y = np.empty_like(x)
+    lib().or_map_f32(MAP_OPS[name], _p(x, _f32p), _p(y, _f32p), x.size)
+    return y
 
 
 def rmsnorm_f32(x: np.ndarray) -> np.ndarray:

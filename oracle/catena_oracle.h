@@ -97,6 +97,8 @@ float or_sin_approx(float x);    /* math.sin-approx */
 float or_cos_approx(float x);    /* math.cos-approx */
 float or_sin_full(float x);      /* math.sin-approx-full */
 float or_cos_full(float x);      /* this build's full-range cosine */
+/* ops 0..6: exp-approx, sqrt, sigmoid, silu, sin-approx, cos-approx, sin-approx-full */
+void or_map_f32(int op, const float *x, float *y, uint64_t n);
 void or_rmsnorm_f32(const float *x, float *y, uint64_t n);   /* nn.rmsnorm */
 uint64_t or_argmax_f32(const float *x, uint64_t n);           /* tensor.argmax-f32 */
 void or_rope_inv_freq(float *inv_freq, uint32_t d, double base);

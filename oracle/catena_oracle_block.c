@@ -124,6 +124,24 @@ float or_cos_full(float x) {
 
 /* nn.rmsnorm, catena-lang/stdlib/nn.hex:154-182 (no gain: the Llama gain
  * of ones is the identity). */
+/* The scalar programs over an array, selected by op (the numbering of
+ * catena_map_op_t in the library's header): 0 exp-approx, 1 sqrt,
+ * 2 sigmoid, 3 silu, 4 sin-approx, 5 cos-approx, 6 sin-approx-full. */
+void or_map_f32(int op, const float *x, float *y, uint64_t n) {
+  for (uint64_t i = 0; i < n; ++i) {
+    const float v = x[i];
+    switch (op) {
+      case 0: y[i] = or_exp_approx(v); break;
+      case 1: y[i] = or_sqrt_newton(v); break;
+      case 2: y[i] = or_sigmoid(v); break;
+      case 3: y[i] = or_silu(v); break;
+      case 4: y[i] = or_sin_approx(v); break;
+      case 5: y[i] = or_cos_approx(v); break;
+      default: y[i] = or_sin_full(v); break;
+    }
+  }
+}
+
 void or_rmsnorm_f32(const float *x, float *y, uint64_t n) {
   float sum_sq = or_bits_f32(0u);
   for (uint64_t i = 0; i < n; ++i) {

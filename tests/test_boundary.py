@@ -78,6 +78,12 @@ HOT = {
     "matmul-left-identity-2x2-via-mem": ([_MEM, _U64, _U64], 1),
     "nn.softmax": ([_MEM], 1),
     "math.exp-approx": ([_F32], 1),
+    "math.sqrt": ([_F32], 1),
+    "nn.sigmoid": ([_F32], 1),
+    "nn.silu": ([_F32], 1),
+    "math.sin-approx": ([_F32], 1),
+    "math.cos-approx": ([_F32], 1),
+    "math.sin-approx-full": ([_F32], 1),
     "nn.rmsnorm": ([_MEM], 1),
     "tensor.argmax-f32": ([_MEM], 1),
     "tensor.broadcast-f32": ([_F32, _U64], 1),

@@ -127,6 +127,33 @@ def _check_forward(dec, cfg, w, tokens, tq, cache_len):
     return np.array([oracle.argmax_f32(LG[b]) for b in range(B)], np.uint32)
 
 
+def _check_step_qkv_token(dec, cfg, tab, w_qkv_f64, tokens_in, cache_len, token_out):
+    """The per-step check of a decode step that needs no attention oracle:
+    the step's W_qkv product (of the rows of `tab`, the normalized embedding
+    table, that the step's input tokens select) within the GEMM bound; q and the new K / V cache
+    rows at pos = cache_len - 1 bitwise the oracle's RoPE of that product;
+    the greedy token the oracle's argmax of the GPU logits."""
+    d, B, H = cfg.d, cfg.B, cfg.H
+    toks = np.asarray(tokens_in, np.int64).ravel()
+    XN = tab[np.minimum(toks, cfg.V)]
+    QKV = dec.read(ca.DEC_QKV, np.float32).reshape(B, 3 * d)
+    af = as_f32(XN).astype(np.float64)
+    bound = 8 * (d / 32 + 1) * 2.0 ** -24 * (np.abs(af) @ np.abs(w_qkv_f64))
+    assert np.all(np.abs(QKV.astype(np.float64) - af @ w_qkv_f64) <= bound)
+    lens = np.full(B, cache_len, np.int64)
+    inv = dec.read(ca.DEC_INV_FREQ, np.float32)
+    q, k, v, pos = od.rope_qkv(QKV, inv, lens, B, 1, H, D)
+    assert np.all(pos == cache_len - 1)
+    _bitwise(dec.read(ca.DEC_Q, np.uint16).reshape(B, d), q)
+    kc = dec.read(ca.DEC_K_CACHE, np.uint16).reshape(B, H, cfg.L, D)
+    vc = dec.read(ca.DEC_V_CACHE, np.uint16).reshape(B, H, cfg.L, D)
+    _bitwise(kc[:, :, cache_len - 1], k.reshape(B, H, D))
+    _bitwise(vc[:, :, cache_len - 1], v.reshape(B, H, D))
+    LG = dec.read(ca.DEC_LOGITS, np.float32).reshape(B, cfg.V)
+    want = np.array([oracle.argmax_f32(LG[b]) for b in range(B)], np.uint32)
+    assert np.array_equal(np.asarray(token_out, np.uint32), want)
+
+
 def test_decoder_stagewise_prefill_and_steps():
     cfg = Tiny
     dec = ca.Decoder(cfg.d, cfg.H, cfg.F, cfg.layers, cfg.V, cfg.B, cfg.L)
@@ -191,6 +218,101 @@ def test_decoder_embed_norm_table_and_rebuild():
     want = _check_forward(dec, cfg, w, prev, 1, cfg.T + 1)
     assert np.array_equal(out.read(np.uint32), want)
     dec.close()
+
+
+def test_decoder_embedding_written_through_retained_handle():
+    """A handle to the embedding taken before any forward and written after
+    one (no further decoder_tensor call): the next generate call rebuilds the
+    normalized table, so the decode step's gathered layer-0 input and its
+    residual both follow the new embedding (checked stage by stage)."""
+    cfg = Tiny
+    dec = ca.Decoder(cfg.d, cfg.H, cfg.F, cfg.layers, cfg.V, cfg.B, cfg.L)
+    dec.init_weights(seed=23, std=0.02)
+    handle = dec.tensor(ca.DEC_EMBED)
+    rng = np.random.default_rng(23)
+    tokens = rng.integers(0, cfg.V, (cfg.B, cfg.T)).astype(np.uint32)
+    nxt = ca.Buffer(cfg.B * 4)
+    say("prefill, then write the embedding through a handle kept from before it")
+    dec.prefill(ca.Buffer.from_array(tokens), cfg.B, cfg.T, nxt)
+    prev = nxt.read(np.uint32)
+    for s_ in range(2):
+        new = oracle.f32_to_bf16_bits_np(
+            (rng.normal(0, 1, (cfg.V, cfg.d)) * np.exp(rng.normal(0, 2, (cfg.V, 1)))).astype(np.float32))
+        ca.mem_write(handle, new)
+        out = ca.Buffer(cfg.B * 4)
+        say(f"decode step {s_} after the write")
+        dec.generate(1, out)
+        w = _weights(dec, cfg)
+        assert np.array_equal(w["embed"], new)
+        want = _check_forward(dec, cfg, w, prev, 1, cfg.T + s_ + 1)
+        got = out.read(np.uint32)
+        assert np.array_equal(got, want)
+        prev = got
+    dec.close()
+
+
+class FewPartial(Tiny):
+    """max_len >= 64, so a decode step runs the eight-wave attention on
+    W_qkv's partials; T = 37 puts the new positions inside a partial 64-row
+    V batch and at many rows of the score blocks."""
+    H, F, V, B, T, L, layers = 2, 512, 512, 2, 37, 100, 1
+    d = H * D
+
+
+def test_decoder_few_pair_attention_partial_batches_stagewise():
+    """Decode steps at positions 37 .. 66 (the new key and value put into the
+    registers / the LDS batch at every row of a partial block, and across the
+    64-position boundary), each checked stage by stage."""
+    cfg = FewPartial
+    dec = ca.Decoder(cfg.d, cfg.H, cfg.F, cfg.layers, cfg.V, cfg.B, cfg.L)
+    dec.init_weights(seed=29, std=0.02)
+    w = _weights(dec, cfg)
+    tokens = np.random.default_rng(29).integers(0, cfg.V, (cfg.B, cfg.T)).astype(np.uint32)
+    nxt = ca.Buffer(cfg.B * 4)
+    say("prefill (max_len 100, T 37)")
+    dec.prefill(ca.Buffer.from_array(tokens), cfg.B, cfg.T, nxt)
+    prev = nxt.read(np.uint32)
+    for s_ in range(30):
+        out = ca.Buffer(cfg.B * 4)
+        say(f"decode step at position {cfg.T + s_} (max_len 100)")
+        dec.generate(1, out)
+        want = _check_forward(dec, cfg, w, prev, 1, cfg.T + s_ + 1)
+        got = out.read(np.uint32)
+        assert np.array_equal(got, want)
+        prev = got
+    dec.close()
+
+
+@pytest.mark.parametrize("cfg", [Tiny, FewPartial], ids=["tiny", "few_pair"])
+def test_decoder_generate_n_equals_n_single_steps(cfg):
+    """generate(N) composes each step's token from the LM head's column-block
+    summaries inside the next step's W_qkv (the deferred argmax); generate(1)
+    composes it in its own launch.  Two decoders from the same seeds: the
+    tokens of one generate(6) and the logits after it equal those of six
+    generate(1) calls bit for bit."""
+    tokens = np.random.default_rng(31).integers(0, cfg.V, (cfg.B, cfg.T)).astype(np.uint32)
+    runs = []
+    for mode in ("one call", "single steps"):
+        dec = ca.Decoder(cfg.d, cfg.H, cfg.F, cfg.layers, cfg.V, cfg.B, cfg.L)
+        dec.init_weights(seed=31, std=0.02)
+        nxt = ca.Buffer(cfg.B * 4)
+        dec.prefill(ca.Buffer.from_array(tokens), cfg.B, cfg.T, nxt)
+        say(f"generate 6 steps ({mode})")
+        if mode == "one call":
+            out = ca.Buffer(6 * cfg.B * 4)
+            dec.generate(6, out)
+            toks = out.read(np.uint32, (6, cfg.B))
+        else:
+            toks = []
+            for _ in range(6):
+                out = ca.Buffer(cfg.B * 4)
+                dec.generate(1, out)
+                toks.append(out.read(np.uint32))
+            toks = np.stack(toks)
+        runs.append((toks, dec.read(ca.DEC_LOGITS, np.float32)))
+        dec.close()
+    assert np.array_equal(runs[0][0], runs[1][0])
+    assert np.array_equal(runs[0][1].view(np.uint32), runs[1][1].view(np.uint32))
 
 
 class C5Step(Tiny):
@@ -353,15 +475,22 @@ class C5:
 def test_decoder_c5_full_workload_stagewise():
     """The C5 workload as bench.py runs it (same seeds): the 4096-row prefill
     (the 256-row-tile GEMMs, the SwiGLU-fused W_gu GEMM, the 16-query-block
-    prefill attention over 512 positions) checked stage by stage; all 128
-    greedy steps run on the device, and the last one (cache length 640)
-    checked stage by stage, its tokens equal to the oracle's argmax of the
-    GPU logits."""
+    prefill attention over 512 positions) checked stage by stage; then the
+    128 greedy steps one generate(1) call at a time, each one's W_qkv
+    product, q, appended K / V cache rows (positions 512 .. 639) and token
+    checked against the oracle, and the first and last steps checked stage
+    by stage.  A second decoder from the same seeds runs the steps as one
+    generate(127) call (the deferred argmax inside W_qkv) and one
+    generate(1): its tokens and final logits equal the first one's bit for
+    bit."""
     cfg = C5
     say("C5 decoder: create + init weights")
     dec = ca.Decoder(cfg.d, cfg.H, cfg.F, cfg.layers, cfg.V, cfg.B, cfg.L)
     dec.init_weights(seed=51, std=0.02)
     w = _weights(dec, cfg)
+    w_qkv64 = as_f32(w["w_qkv"][0]).astype(np.float64)
+    tab = dec.read(ca.DEC_EMBED_NORM, np.uint16).reshape(cfg.V + 1, cfg.d)
+    _bitwise(tab[:cfg.V], od.residual_rmsnorm_bf16(as_f32(w["embed"]))[1])
     tokens = np.random.default_rng(51).integers(0, cfg.V, (cfg.B, cfg.T)).astype(np.uint32)
     tb = ca.Buffer.from_array(tokens)
     nxt = ca.Buffer(cfg.B * 4)
@@ -369,16 +498,38 @@ def test_decoder_c5_full_workload_stagewise():
     dec.prefill(tb, cfg.B, cfg.T, nxt)
     say("C5 decoder: prefill stagewise check")
     want = _check_forward(dec, cfg, w, tokens, cfg.T, cfg.T)
-    first = nxt.read(np.uint32)
-    assert np.array_equal(first, want)
-    out = ca.Buffer((cfg.steps - 1) * cfg.B * 4)
-    say("C5 decoder: 127 greedy steps")
-    dec.generate(cfg.steps - 1, out)
-    toks = out.read(np.uint32, (cfg.steps - 1, cfg.B))
+    prev = nxt.read(np.uint32)
+    assert np.array_equal(prev, want)
+    toks = []
+    for s_ in range(cfg.steps):
+        out = ca.Buffer(cfg.B * 4)
+        if s_ % 16 == 0:
+            say(f"C5 decoder: step {s_ + 1} of {cfg.steps} (cache length {cfg.T + s_ + 1})")
+        dec.generate(1, out)
+        got = out.read(np.uint32)
+        if s_ in (0, cfg.steps - 1):
+            want = _check_forward(dec, cfg, w, prev, 1, cfg.T + s_ + 1)
+            assert np.array_equal(got, want)
+        else:
+            _check_step_qkv_token(dec, cfg, tab, w_qkv64, prev, cfg.T + s_ + 1, got)
+        toks.append(got)
+        prev = got
+    toks = np.stack(toks)
     assert toks.max() < cfg.V
+    final_logits = dec.read(ca.DEC_LOGITS, np.float32)
+    dec.close()
+
+    say("C5 decoder B: prefill, generate(127) + generate(1)")
+    dec = ca.Decoder(cfg.d, cfg.H, cfg.F, cfg.layers, cfg.V, cfg.B, cfg.L)
+    dec.init_weights(seed=51, std=0.02)
+    dec.prefill(tb, cfg.B, cfg.T, nxt)
+    out = ca.Buffer((cfg.steps - 1) * cfg.B * 4)
+    dec.generate(cfg.steps - 1, out)
     last = ca.Buffer(cfg.B * 4)
-    say("C5 decoder: step 128 (cache length 640)")
     dec.generate(1, last)
-    want = _check_forward(dec, cfg, w, toks[-1], 1, cfg.L)
-    assert np.array_equal(last.read(np.uint32), want)
+    toks_b = np.concatenate([out.read(np.uint32, (cfg.steps - 1, cfg.B)),
+                             last.read(np.uint32, (1, cfg.B))])
+    assert np.array_equal(toks_b, toks)
+    assert np.array_equal(dec.read(ca.DEC_LOGITS, np.float32).view(np.uint32),
+                          final_logits.view(np.uint32))
     dec.close()

@@ -50,6 +50,60 @@ def test_exp_approx_bitwise_sweep():
     assert _bits_equal_nan_aware(got, want)
 
 
+_MAP = {  # catena_map_op_t -> oracle name
+    ca.MAP_EXP_APPROX: "exp_approx", ca.MAP_SQRT: "sqrt_newton", ca.MAP_SIGMOID: "sigmoid",
+    ca.MAP_SILU: "silu", ca.MAP_SIN_APPROX: "sin_approx", ca.MAP_COS_APPROX: "cos_approx",
+    ca.MAP_SIN_APPROX_FULL: "sin_full",
+}
+
+
+@pytest.mark.parametrize("op", sorted(_MAP), ids=[_MAP[k] for k in sorted(_MAP)])
+def test_scalar_map_bitwise_sweep(op):
+    """Each scalar stdlib program elementwise on the GPU against the pinned
+    oracle, bit for bit: 2M random bit patterns, a dense sweep of [-300, 300]
+    and the special values."""
+    rng = np.random.default_rng(100 + op)
+    x = np.concatenate([
+        np.linspace(-300, 300, 1_000_001).astype(np.float32),
+        rng.integers(0, 2 ** 32, 2_000_000, dtype=np.uint64).astype(np.uint32).view(np.float32),
+        np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40, -1e-40, 3.4e38, -3.4e38],
+                 np.float32),
+    ]).astype(np.float32)
+    say(f"scalar map {_MAP[op]} sweep n={x.size}")
+    xb, yb = ca.Buffer.from_array(x), ca.Buffer(x.nbytes)
+    ca.map_f32(op, xb, yb, x.size)
+    assert _bits_equal_nan_aware(yb.read(np.float32), oracle.map_f32(_MAP[op], x))
+    # in place (y == x)
+    ca.map_f32(op, xb, xb, x.size)
+    assert _bits_equal_nan_aware(xb.read(np.float32), oracle.map_f32(_MAP[op], x))
+
+
+def test_runtime_scalar_programs_reference_tests():
+    """math.sqrt, nn.sigmoid, nn.silu, math.sin-approx, math.cos-approx and
+    math.sin-approx-full through Runtime::exec (built-in stdlib programs,
+    (f32) -> (f32)): bitwise the oracle, and within the reference's own
+    tolerance on its own test inputs (fixtures cite catena-lang/tests/
+    runtime.rs)."""
+    rt = ca.Runtime([])
+    cases = [("math.sqrt", "sqrt_newton", "sqrt"), ("nn.sigmoid", "sigmoid", "sigmoid"),
+             ("nn.silu", "silu", "silu"), ("math.sin-approx", "sin_approx", "sin_approx"),
+             ("math.sin-approx-full", "sin_full", "sin_approx_full"),
+             ("math.cos-approx", "cos_approx", None)]
+    for program, name, key in cases:
+        g = GOLDEN[key] if key else {"inputs": [0.0, 0.5, 1.0, -0.5, -1.0]}
+        for i, v in enumerate(g["inputs"]):
+            say(f"runtime exec {program}({v})")
+            [r] = rt.exec(program, [ca.Value.f32(v)], 1)
+            assert r.kind == ca.KIND_F32
+            want = oracle.scalar(name, v)
+            assert np.float32(r.get()).view(np.uint32) == np.float32(want).view(np.uint32), (program, v)
+            if key:
+                assert abs(r.get() - g["expected"][i]) < g["absolute_tolerance"], (program, v)
+            else:  # math.cos-approx has no reference test: libm on its Taylor range
+                assert abs(r.get() - np.cos(v)) < 1e-3, (program, v)
+    rt.close()
+
+
 @pytest.mark.parametrize("n", [1, 2, 3, 255, 256, 257, 4096, 100003])
 def test_softmax_bitwise(n):
     rng = np.random.default_rng(n)
@@ -81,7 +135,9 @@ def test_softmax_rows_in_place_and_specials():
 
 
 @pytest.mark.parametrize("n,m,k", [(256, 256, 256), (1, 1, 1), (65, 33, 17), (130, 70, 300),
-                                   (64, 64, 0), (3, 200, 5), (257, 129, 64)])
+                                   (64, 64, 0), (3, 200, 5), (257, 129, 64), (100, 77, 131),
+                                   # 64x64 tiles (at least 256 of them)
+                                   (1040, 1030, 37), (1024, 1024, 130)])
 def test_gemm_f32_exact_bitwise(n, m, k):
     rng = np.random.default_rng(n + m + k)
     a = rng.uniform(-1, 1, (n, k)).astype(np.float32)
@@ -92,6 +148,23 @@ def test_gemm_f32_exact_bitwise(n, m, k):
     got = cb.read(np.float32, (n, m))
     want = oracle.matmul_f32(a, b) if k else np.zeros((n, m), np.float32)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_gemm_f32_exact_tile_instances_agree():
+    """Rows 256..511 of a 1024 x 1024 x 300 product (64x64 tiles: 256 of
+    them) computed alone as a 256 x 1024 product (16x16 tiles: 64 tiles of
+    64x64 would leave CUs idle): the same bits, since every cell is one
+    k-ascending chain in both instances."""
+    n, m, k = 1024, 1024, 300
+    rng = np.random.default_rng(77)
+    a = rng.uniform(-1, 1, (n, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (k, m)).astype(np.float32)
+    ab, bb = ca.Buffer.from_array(a), ca.Buffer.from_array(b)
+    full, part = ca.Buffer(n * m * 4), ca.Buffer(256 * m * 4)
+    say("gemm f32 exact 1024x1024x300 (64x64 tiles) and rows 256..511 alone (16x16 tiles)")
+    ca.gemm_f32_exact(ab, bb, full, n, m, k)
+    ca.gemm_f32_exact(ca.Buffer.from_array(np.ascontiguousarray(a[256:512])), bb, part, 256, m, k)
+    assert np.array_equal(full.read(np.uint32, (n, m))[256:512], part.read(np.uint32, (256, m)))
 
 
 def test_gemm_f32_exact_run_to_run():

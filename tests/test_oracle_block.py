@@ -157,3 +157,15 @@ def test_row_forms_equal_the_elementwise_composition():
     x = rng.standard_normal((4, 300)).astype(np.float32)
     want = np.stack([oracle.rmsnorm_f32(r) for r in x])
     assert np.array_equal(oracle.rmsnorm_f32(x).view(np.uint32), want.view(np.uint32))
+
+
+def test_scalar_programs_reference_vectors():
+    """The reference's own tests of the scalar programs (inputs, expected
+    libm values and tolerances as fixtures, each citing its test):
+    math.sin-approx, math.sin-approx-full, nn.sigmoid, nn.silu, math.sqrt."""
+    for key, name in [("sin_approx", "sin_approx"), ("sin_approx_full", "sin_full"),
+                      ("sigmoid", "sigmoid"), ("silu", "silu"), ("sqrt", "sqrt_newton")]:
+        g = GOLDEN[key]
+        got = oracle.map_f32(name, np.array(g["inputs"], np.float32))
+        err = np.abs(got.astype(np.float64) - np.array(g["expected"], np.float64))
+        assert np.all(err < g["absolute_tolerance"]), (key, float(err.max()))

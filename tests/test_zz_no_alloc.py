@@ -26,26 +26,40 @@ def _pair(m, n, k, seed):
 
 
 def test_noalloc_decode_gemm_equals_the_allocating_entry_point():
+    """shutdown + init first: that releases the split-K workspace the
+    allocating entry point keeps, so a call that fell back to it would have
+    to allocate.  The allocation-free calls then run before any allocating
+    call, and the pool must not change across them."""
     L = ca.lib()
-    # two calls in a row, the second with a smaller input; both split K
-    # (8 and 2 k groups), so both write partials into the scratch
-    for (m, n, k, seed) in [(16, 4096, 11008, 61), (5, 1024, 2048, 62)]:
+    say("shutdown + init (releases the library's split-K workspace)")
+    ca.shutdown()
+    ca.init(0)
+    # two calls in a row per output type, the second with a smaller input;
+    # both split K (8 and 2 k groups), so both write partials into the scratch
+    shapes = [(16, 4096, 11008, 61), (5, 1024, 2048, 62)]
+    cases = []
+    for (m, n, k, seed) in shapes:
         groups, pbytes = ca.gemm_bf16_decode_plan(m, n, k)
         assert groups > 1 and 0 < pbytes <= 4 << 20
         x, w = _pair(m, n, k, seed)
         for out_f32, dt, es in ((False, np.uint16, 2), (True, np.uint32, 4)):
-            want, got = ca.Buffer(m * n * es), ca.Buffer(m * n * es)
-            say(f"decode GEMM M={m} N={n} K={k} out_f32={out_f32}: allocating entry point")
-            ca.gemm_bf16(x, w, want, m, n, k, out_f32=out_f32)
-            ca.synchronize()
-            allocs = ca.pool_stats()["device_allocs"]
-            say(f"decode GEMM M={m} N={n} K={k} out_f32={out_f32}: allocation-free entry point")
-            st = L.catena_mi355x_gemm_bf16_decode_noalloc(x.ptr, w.ptr, got.ptr, m, n, k,
-                                                          1 if out_f32 else 0)
-            assert st == 0, ca.last_error()
-            ca.synchronize()
-            assert ca.pool_stats()["device_allocs"] == allocs
-            assert np.array_equal(got.read(dt), want.read(dt)), (m, n, k, out_f32)
+            cases.append((m, n, k, x, w, out_f32, dt, ca.Buffer(m * n * es), ca.Buffer(m * n * es)))
+    ca.synchronize()
+    before = ca.pool_stats()
+    for (m, n, k, x, w, out_f32, dt, got, _) in cases:
+        say(f"decode GEMM M={m} N={n} K={k} out_f32={out_f32}: allocation-free entry point")
+        st = L.catena_mi355x_gemm_bf16_decode_noalloc(x.ptr, w.ptr, got.ptr, m, n, k,
+                                                      1 if out_f32 else 0)
+        assert st == 0, ca.last_error()
+    ca.synchronize()
+    after = ca.pool_stats()
+    assert after["device_allocs"] == before["device_allocs"]
+    assert after["bytes_live"] == before["bytes_live"]
+    for (m, n, k, x, w, out_f32, dt, got, want) in cases:
+        say(f"decode GEMM M={m} N={n} K={k} out_f32={out_f32}: allocating entry point")
+        ca.gemm_bf16(x, w, want, m, n, k, out_f32=out_f32)
+        ca.synchronize()
+        assert np.array_equal(got.read(dt), want.read(dt)), (m, n, k, out_f32)
 
 
 def test_noalloc_decode_gemm_limits():
