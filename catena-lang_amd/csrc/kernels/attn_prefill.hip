@@ -13,12 +13,23 @@
 // Query tq of sequence b attends to the first lens[b] - (Tq - 1 - tq)
 // positions (clamped to [0, L]).
 //
-// Scores: waves take 64-key blocks round robin.  Lane l owns key kb*64 + l:
-// its 128 K values are widened into registers once and folded against each
-// of the 16 queries, whose f32 values are LDS broadcasts; the next block's
-// row is loaded while the current one is folded.  Scores go to
-// sT[key][query] (row stride QB + 1 floats: the writes of 64 keys and the
-// per-query reads of softmax are bank-conflict free).
+// Scores: waves take 64-key blocks round robin; lane l owns key kb*64 + l
+// and holds its K row in registers (the next block's row is loaded while the
+// current one is folded).  The fold over d runs on the matrix cores:
+// v_mfma_f32_16x16x1_4b_f32 with A = the 16 queries' q_d (lane l: query
+// l % 16, every block) and B = the 64 keys' k_d (lane l: key l) adds
+// q_d * k_{t,d} to each of the 16 x 64 accumulators with one rounding, d
+// ascending from +0.  The product of two bf16 values is exact in f32 unless
+// it leaves the normal range, so one rounding of acc + q_d k_{t,d} is the
+// reference's fl(acc + fl(q_d * k_{t,d})) bit for bit whenever every nonzero
+// q and k value has magnitude in [2^-63, 2^63) (products in [2^-126, 2^126)).
+// That range is checked on the same registers while the MFMAs run (packed
+// u16 min / max of the magnitude bits); if any value of the workgroup's q
+// rows or K rows lies outside it (tiny, huge, inf or NaN), the workgroup
+// recomputes its scores with the VALU fold (v_mul_f32 + v_add_f32 per
+// product) before anything reads them.  Scores go to sT[key][query] (row
+// stride QB + 1 floats: the per-query reads of softmax are bank-conflict
+// free).
 // Softmax: per query, the exact parallel form of the max fold (FirstMax,
 // common.h) by one wave; exp~ elementwise; the denominators are 16
 // independent serial folds, one lane per query; p = e / den elementwise.
@@ -31,11 +42,22 @@
 
 namespace {
 constexpr int D = 128;
+constexpr int QS = D + 4;            // qf row stride (floats)
+constexpr int QH = D + 8;            // qh row stride (bf16): the MFMA A-operand reads (16 rows,
+                                     // 16 bytes each) cover the 64 banks once
 constexpr int QB = 16;               // queries per workgroup
 constexpr int HALF = QB / 2;         // queries per score item / output thread
 constexpr int ST = QB + 1;           // sT row stride (floats)
 constexpr int VBLK = 64;             // keys per V stage
 constexpr int VSTAGE = VBLK * D * 2; // bytes (bf16)
+
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+
+// Magnitude bits (sign cleared) of two bf16 values; a nonzero value is safe
+// for the MFMA fold when its bits lie in [0x2000, 0x5F00): exponent field
+// 64 .. 189, i.e. magnitude in [2^-63, 2^63).
+constexpr uint32_t kSafeLo = 0x2000u, kSafeHi = 0x5F00u;
 
 CATENA_DEV FirstMax wave_first_max(FirstMax a) {
 #pragma unroll
@@ -61,8 +83,9 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
                              void* __restrict__ o, uint32_t B, uint32_t H, uint32_t L,
                              uint32_t Tq, float scale) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  float* qf = reinterpret_cast<float*>(smem);                      // [QB][D]
-  unsigned char* vstage = smem + QB * D * 4;                       // [VBLK][D] bf16
+  float* qf = reinterpret_cast<float*>(smem);                      // [QB][QS]
+  uint16_t* qh = reinterpret_cast<uint16_t*>(smem + QB * QS * 4);  // [QB][QH] bf16
+  unsigned char* vstage = smem + QB * QS * 4 + QB * QH * 2;        // [VBLK][D] bf16
   float* red = reinterpret_cast<float*>(vstage + VSTAGE);          // [QB] max, [QB] den
   float* sT = red + 3 * QB;                                        // [Lmax][ST] (after qlen)
 
@@ -84,24 +107,90 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
 
   const uint16_t* kb = k + (uint64_t)bh * L * D;
   const uint16_t* vb = v + (uint64_t)bh * L * D;
-  // q rows of this block, widened (rows past nq are zero and never used)
+  // q rows of this block, widened (rows past nq are zero and never used);
+  // `unsafe` notes a value outside the MFMA fold's exact range
+  int unsafe = 0;
   for (uint32_t e = tid; e < (uint32_t)QB * D; e += 256) {
     const uint32_t i = e / D, d = e % D;
-    float val = 0.0f;
-    if (i < nq) val = bf16_to_f32(q[(((uint64_t)b * Tq + t0 + i) * H + h) * D + d]);
-    qf[e] = val;
+    uint16_t bits = 0;
+    if (i < nq) bits = q[(((uint64_t)b * Tq + t0 + i) * H + h) * D + d];
+    const uint32_t mag = bits & 0x7FFFu;
+    unsafe |= (mag != 0u && mag < kSafeLo) || mag >= kSafeHi;
+    qf[i * QS + d] = bf16_to_f32(bits);
+    qh[i * QH + d] = bits;
   }
   __syncthreads();
 
   // ---------------------------------------------------------------- scores
-  {
-    const uint32_t nkb = (lmax + 63) / 64;
-    auto kload = [&](uint32_t kblk, u32x4_t r[D / 8]) {
-      const uint32_t j = kblk * 64 + lane;
-      const u32x4_t* src = reinterpret_cast<const u32x4_t*>(kb + (uint64_t)j * D);
+  const uint32_t nkb = (lmax + 63) / 64;
+  auto kload = [&](uint32_t kblk, u32x4_t r[D / 8]) {
+    const uint32_t j = kblk * 64 + lane;
+    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(kb + (uint64_t)j * D);
 #pragma unroll
-      for (int c = 0; c < D / 8; ++c) r[c] = j < lmax ? src[c] : u32x4_t{0u, 0u, 0u, 0u};
-    };
+    for (int c = 0; c < D / 8; ++c) r[c] = j < lmax ? src[c] : u32x4_t{0u, 0u, 0u, 0u};
+  };
+  // the MFMA path's form: every lane loads a row in use (a key past lmax
+  // reads row lmax - 1; its scores are never stored), so the loads need no
+  // branch and the range check sees only rows the scores use
+  auto kload_rows = [&](uint32_t kblk, u32x4_t r[D / 8]) {
+    const uint32_t j = kblk * 64 + lane;
+    const uint32_t jr = j < lmax ? j : lmax - 1u;
+    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(kb + (uint64_t)jr * D);
+#pragma unroll
+    for (int c = 0; c < D / 8; ++c) r[c] = src[c];
+  };
+  {
+    // matrix-core fold: lane l, accumulator r holds key kblk*64 + 16 (r / 4)
+    // + l % 16 against query 4 (l / 16) + r % 4
+    uint32_t ql[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) ql[u] = qlen[4 * (lane >> 4) + u];
+    // lane l's A operand: query l % 16's row, packed bf16 in LDS, eight d
+    // values per read, the next read issued before the current MFMAs
+    const u32x4_t* qrow = reinterpret_cast<const u32x4_t*>(qh + (lane & 15) * QH);
+    u16x2_t mn = {0xFFFF, 0xFFFF}, mx = {0, 0};
+    const u16x2_t one = {1, 1};
+    u32x4_t raw[D / 8];
+    if ((uint32_t)wave < nkb) kload_rows(wave, raw);
+    for (uint32_t kblk = wave; kblk < nkb; kblk += 4) {
+      u32x4_t cur[D / 8];
+#pragma unroll
+      for (int c = 0; c < D / 8; ++c) cur[c] = raw[c];
+      if (kblk + 4 < nkb) kload_rows(kblk + 4, raw);
+      f32x16_t acc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = __uint_as_float(0u);
+      u32x4_t qnext = qrow[0];
+#pragma unroll
+      for (int c = 0; c < D / 8; ++c) {
+        const u32x4_t qcur = qnext;
+        if (c + 1 < D / 8) qnext = qrow[c + 1];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const uint32_t word = cur[c][w], qword = qcur[w];
+          const u16x2_t mag = __builtin_bit_cast(u16x2_t, word & 0x7FFF7FFFu);
+          mn = __builtin_elementwise_min(mn, mag - one);
+          mx = __builtin_elementwise_max(mx, mag);
+          acc = __builtin_amdgcn_mfma_f32_16x16x1f32(bf16lo(qword), bf16lo(word), acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x1f32(bf16hi(qword), bf16hi(word), acc, 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const uint32_t j = kblk * 64 + 16 * (r >> 2) + (lane & 15);
+        if (j < ql[r & 3]) sT[j * ST + 4 * (lane >> 4) + (r & 3)] = acc[r] * scale;
+      }
+    }
+    // x - 1 wraps a zero to 0xFFFF: a minimum below kSafeLo - 1 is a nonzero
+    // value below the range
+    const uint32_t lo = mn[0] < mn[1] ? mn[0] : mn[1];
+    const uint32_t hi = mx[0] > mx[1] ? mx[0] : mx[1];
+    unsafe |= lo < kSafeLo - 1u || hi >= kSafeHi;
+  }
+  if (__syncthreads_or(unsafe)) {
+    // the VALU fold: lane l owns key kb*64 + l, its 128 K values widened into
+    // registers once and folded against each of the 16 queries (LDS
+    // broadcasts), v_mul_f32 then v_add_f32 per product
     u32x4_t raw[D / 8];
     if ((uint32_t)wave < nkb) kload(wave, raw);
     for (uint32_t kblk = wave; kblk < nkb; kblk += 4) {
@@ -119,7 +208,7 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
       for (int i = 0; i < QB; ++i) {
         const uint32_t li = qlen[i];
         if (kblk * 64 >= li) continue;
-        const f32x4_t* q4 = reinterpret_cast<const f32x4_t*>(qf + i * D);
+        const f32x4_t* q4 = reinterpret_cast<const f32x4_t*>(qf + i * QS);
         float acc = __uint_as_float(0u);
 #pragma unroll
         for (int c = 0; c < D / 4; ++c) {
@@ -371,7 +460,7 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
 }
 
 // grid = B * H * ceil(Tq / 16), block = 256, dynamic LDS =
-// 16*128*4 + 64*128*2 + 3*16*4 + Lmax*17*4 with Lmax >= min(max lens, L).
+// 16*132*4 + 16*136*2 + 64*128*2 + 3*16*4 + Lmax*17*4 with Lmax >= min(max lens, L).
 extern "C" __global__ __launch_bounds__(256) void catena_attn_prefill_bf16_d128_f32out(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint32_t* __restrict__ lens, float* __restrict__ o, uint32_t B, uint32_t H, uint32_t L,

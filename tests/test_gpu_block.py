@@ -285,6 +285,40 @@ def test_attention_causal_prefill_nan_inf_tie_scores():
     _bitwise(o32.read(np.float32, (B * Tq, H * D)), want)
 
 
+def test_attention_prefill_mfma_fold_range_guard():
+    """The prefill kernel folds q.k on the matrix cores (one rounding per
+    step, exact products) only while every nonzero q / k magnitude is in
+    [2^-63, 2^63); otherwise the workgroup refolds with v_mul_f32 +
+    v_add_f32.  Heads scaled so that products fall in the denormal range
+    (head 1: fused and separately rounded steps differ there) or overflow
+    (head 2), beside heads inside the range (0, 3) and at its edges (4:
+    2^-63 and just below 2^63): all bitwise the oracle."""
+    B, Tq, H, L, D = 2, 40, 5, 64, 128
+    lens = [64, 40]
+    rng = np.random.default_rng(33)
+    q32 = rng.normal(0, 1, (B, Tq, H, D)).astype(np.float32)
+    k32 = rng.normal(0, 1, (B, H, L, D)).astype(np.float32)
+    q32[:, :, 1] *= 2.0 ** -68
+    k32[:, 1] *= 2.0 ** -68
+    q32[:, :, 2] *= 2.0 ** 66
+    k32[:, 2] *= 2.0 ** 64
+    q32[:, :, 3] *= 2.0 ** -30
+    k32[:, 3] *= 2.0 ** 30
+    edge = np.where(rng.random((B, H, L, D)) < 0.5, 2.0 ** -63, np.float32(1.99) * 2.0 ** 62)
+    k32[:, 4] = (np.sign(k32[:, 4]) * edge[:, 4]).astype(np.float32)
+    q16 = oracle.f32_to_bf16_bits_np(q32).reshape(-1)
+    k16 = oracle.f32_to_bf16_bits_np(k32)
+    v16 = oracle.f32_to_bf16_bits_np(rng.normal(0, 1, (B, H, L, D)).astype(np.float32))
+    q, k, v = ca.Buffer.from_array(q16), ca.Buffer.from_array(k16), ca.Buffer.from_array(v16)
+    lb = ca.Buffer.from_array(np.array(lens, np.uint32))
+    scale = 1.0 / math.sqrt(D)
+    o32 = ca.Buffer(B * Tq * H * D * 4)
+    say("prefill attention: MFMA fold range guard (denormal / overflow / edge heads)")
+    ca.attn_causal_bf16(q, k, v, lb, o32, B, Tq, H, L, D, scale, out_f32=True)
+    want = od.attn_causal(q16, k16, v16, lens, B, Tq, H, D, scale)
+    _bitwise(o32.read(np.float32, (B * Tq, H * D)), want)
+
+
 def test_attention_causal_tq1_equals_decode_kernel():
     B, H, L, D = 4, 8, 1024, 128
     q, k, v = _attn_inputs(B, 1, H, L, 99)
