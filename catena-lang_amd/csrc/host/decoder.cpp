@@ -241,6 +241,11 @@ int forward(catena_decoder& m, const uint32_t* tokens, uint32_t batch, uint32_t 
       } else {
         TRY(gemm_bf16_decode(xn, wqkv, QKV, rows, 3 * d, d, DecodeEpilogue::Rope, e));
       }
+    } else if (gemm_bf16_rope_fits(rows, d, tq, c.n_heads, XN, wqkv, Q, kc, vc, m.rope_tab)) {
+      // RoPE, bf16 q and the cache append in the projection's epilogue: the
+      // f32 product (3d floats per row) is never written
+      TRY(gemm_bf16_rope_qkv(XN, wqkv, static_cast<const float*>(m.rope_tab), lens, Q, kc, vc, rows, d,
+                             tq, c.n_heads, c.max_len));
     } else {
       TRY(catena_mi355x_gemm_bf16(XN, wqkv, QKV, rows, 3 * d, d, 1));
       TRY(catena_mi355x_rope_qkv_bf16(QKV, inv, lens, Q, kc, vc, batch, tq, c.n_heads, c.head_dim,

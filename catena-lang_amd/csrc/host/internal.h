@@ -25,6 +25,7 @@ enum class KernelId : int {
   GemmBf16K32N128F32,
   GemmBf16K32Silu,  // the 32-k kernels with the SwiGLU epilogue
   GemmBf16K32N128Silu,
+  GemmBf16K32N128Rope,  // the 256 x 128 tile kernel with the RoPE + cache epilogue
   GemmBf16DecodeF32,
   GemmBf16DecodeBf16,
   GemmBf16DecodeRope,
@@ -223,6 +224,20 @@ uint64_t noalloc_scratch_bytes();
 // kernels: n % 256, m % 128, k % 128 == 0, aligned operands).
 bool gemm_bf16_silu_fits(uint64_t n, uint64_t m, uint64_t k, const void* a, const void* b,
                          const void* act);
+// Fused q / k / v projection of a prefill: rows x (3 heads 128) from a
+// k-deep bf16 input and weight, then RoPE (the rotation read from tab,
+// [positions][64][2] cos / sin), bf16 q [rows][heads 128] and the K / V cache
+// rows [batch][heads][max_len][128] at pos = lens[b] - tq + t -- the bits of
+// catena_mi355x_gemm_bf16 followed by catena_mi355x_rope_qkv_bf16, without
+// the f32 product.  gemm_bf16_rope_fits says whether the 256 x 128 tile
+// kernel takes the shape (rows % 256 == 0, rows % tq == 0, k % 128 == 0,
+// 16-byte aligned operands).
+bool gemm_bf16_rope_fits(uint64_t rows, uint64_t k, uint32_t tq, uint32_t heads, const void* a,
+                         const void* w, const void* q_out, const void* kc, const void* vc,
+                         const void* tab);
+int gemm_bf16_rope_qkv(const uint16_t* a, const uint16_t* w, const float* tab, const uint32_t* lens,
+                       uint16_t* q_out, uint16_t* kc, uint16_t* vc, uint64_t rows, uint64_t k,
+                       uint32_t tq, uint32_t heads, uint32_t max_len);
 // nn.rmsnorm rows whose input is an embedding gather (x = widen(table[tok]))
 // written to x_out, bf16 output.
 int embed_rmsnorm_bf16(const uint32_t* tokens, const uint16_t* table, uint32_t vocab,

@@ -237,6 +237,35 @@ bool gemm_bf16_silu_fits(uint64_t n, uint64_t m, uint64_t k, const void* a, cons
          (n / 256) * (m / 128) <= 0x7FFFFFFFull;
 }
 
+bool gemm_bf16_rope_fits(uint64_t rows, uint64_t k, uint32_t tq, uint32_t heads, const void* a,
+                         const void* w, const void* q_out, const void* kc, const void* vc,
+                         const void* tab) {
+  const uint64_t m = 3ull * heads * 128;
+  return tq > 0 && heads > 0 && rows % 256 == 0 && rows % tq == 0 && k % 128 == 0 && k > 0 &&
+         k <= (1ull << 22) && m <= (1ull << 24) && aligned16(a) && aligned16(w) && aligned16(q_out) &&
+         aligned16(kc) && aligned16(vc) && aligned16(tab) && (rows / 256) * (m / 128) <= 0x7FFFFFFFull;
+}
+
+int gemm_bf16_rope_qkv(const uint16_t* a, const uint16_t* w, const float* tab, const uint32_t* lens,
+                       uint16_t* q_out, uint16_t* kc, uint16_t* vc, uint64_t rows, uint64_t k,
+                       uint32_t tq, uint32_t heads, uint32_t max_len) {
+  int st = ensure_init();
+  if (st) return st;
+  if (rows == 0) return CATENA_OK;
+  if (!a || !w || !tab || !lens || !q_out || !kc || !vc)
+    return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
+  if (!gemm_bf16_rope_fits(rows, k, tq, heads, a, w, q_out, kc, vc, tab))
+    return fail(CATENA_ERR_UNSUPPORTED, "fused q / k / v projection: shape or alignment not taken");
+  // the stages (4 x (256 + 128) x 32 bf16) hold the epilogue's staging,
+  // 8 waves x 64 rows x 128 bytes
+  const size_t lds = 4ull * (256 + 128) * 32 * sizeof(uint16_t);
+  if (lds > device().max_lds) return fail(CATENA_ERR_UNSUPPORTED, "device LDS %zu < %zu", device().max_lds, lds);
+  uint64_t n = rows, m = 3ull * heads * 128;
+  const uint64_t grid = (n / 256) * (m / 128);
+  void* args[] = {&a, &w, &n, &m, &k, &tab, &lens, &q_out, &kc, &vc, &tq, &heads, &max_len};
+  return launch(KernelId::GemmBf16K32N128Rope, dim3((unsigned)grid), dim3(512), lds, args);
+}
+
 }  // namespace catena
 
 extern "C" {

@@ -83,9 +83,23 @@ CATENA_DEV void tile_of(uint32_t bid, uint32_t tiles_m, uint32_t tiles_n, uint32
 // buffer descriptor word 3 for raw (unswizzled, stride 0) 32-bit access
 constexpr int kRsrcWord3 = 0x00020000;
 
-template <bool OUT_BF16, int BN, bool SILU = false>
+// The RoPE epilogue's operands (a fused q / k / v projection, one head per
+// 128-column tile): the rotation table [positions][64][2] (cos, sin), the
+// per-sequence lengths, q [M][H * 128] and the caches [B][H][L][128], bf16.
+struct RopeQkv {
+  const float* tab;
+  const uint32_t* lens;
+  uint16_t* q_out;
+  uint16_t* kc;
+  uint16_t* vc;
+  uint32_t Tq, H, L;
+};
+
+template <bool OUT_BF16, int BN, bool SILU = false, bool ROPE = false>
 CATENA_DEV void gemm_k32_body(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
-                              void* __restrict__ C, uint64_t M, uint64_t N, uint64_t K) {
+                              void* __restrict__ C, uint64_t M, uint64_t N, uint64_t K,
+                              const RopeQkv& rq = RopeQkv{}) {
+  static_assert(!ROPE || BN == 128, "the RoPE epilogue pairs the two column waves of a 128-wide tile");
   static_assert(BN == 256 || BN == 128, "tile widths 256 and 128");
   constexpr int B_ST = BK * BN;                // elements per B stage
   constexpr int WI = BN == 256 ? 8 : 4;        // 16-row MFMA blocks per wave
@@ -137,6 +151,33 @@ CATENA_DEV void gemm_k32_body(const uint16_t* __restrict__ A, const uint16_t* __
     }
   };
 
+  // RoPE epilogue: this wave's rotation values (its half of the pair's rows,
+  // its 16 columns per col block), requested now so they land during the
+  // main loop.  Row blocks (wn * WI / 2 + ii) of the wave's 64 rows.
+  f32x4_t rcs[ROPE ? WI : 1][2][2];
+  uint32_t rsect = 0;
+  if constexpr (ROPE) {
+    const int G_ = lane >> 4, s_ = lane & 15;
+    rsect = (uint32_t)(n0 / 128) / rq.H;
+    if (rsect != 2) {
+#pragma unroll
+      for (int i = 0; i < WI; ++i) {
+        const uint64_t gr = m0 + wm * 64 + 16 * i + s_;
+        const uint32_t b = (uint32_t)(gr / rq.Tq), tq = (uint32_t)(gr % rq.Tq);
+        const uint32_t len = rq.lens[b];
+        const bool ok = len >= rq.Tq && len - rq.Tq + tq < rq.L;
+        const uint32_t pos = ok ? len - rq.Tq + tq : 0u;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const f32x4_t* cs =
+              reinterpret_cast<const f32x4_t*>(rq.tab + ((uint64_t)pos * 64 + 32 * wn + 16 * j + 4 * G_) * 2);
+          rcs[i][j][0] = cs[0];
+          rcs[i][j][1] = cs[1];
+        }
+      }
+    }
+  }
+
   f32x4_t acc[WI][4];  // [row block i][col block j], transposed blocks
 #pragma unroll
   for (int i = 0; i < WI; ++i)
@@ -149,13 +190,19 @@ CATENA_DEV void gemm_k32_body(const uint16_t* __restrict__ A, const uint16_t* __
   // 16 j + 4 (s % 4)), so lane i of a 16-lane group receives 4 consecutive k
   // of one column, matching A's k order.
   const int G = lane >> 4, s = lane & 15;
+  auto wave_col = [&](int j) -> uint32_t {
+    return ROPE ? (uint32_t)((j >> 1) * 64 + wn * 32 + 16 * (j & 1)) : (uint32_t)(wn * 64 + 16 * j);
+  };
   const uint32_t a_lds = (wm * 16 * WI + s) * BK * 2 + 16 * ((uint32_t)G ^ ((uint32_t)(s >> 1) & 3u));
   const uint32_t b_krow = 8 * G + (s >> 2);
   const uint32_t hb = hB(b_krow);
   uint32_t b_lds[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const uint32_t col = wn * 64 + 16 * j + 4 * (s & 3);
+    // col block j of the wave: 16 columns from wave_col(j); the RoPE
+    // instance gives wave wn columns 32 wn .. +31 and 64 + 32 wn .. +31, so
+    // that each wave holds both members (i, i + 64) of its rotation pairs
+    const uint32_t col = wave_col(j) + 4 * (s & 3);
     b_lds[j] = S * A_ST * 2 + b_krow * BN * 2 + 16 * ((col >> 3) ^ hb) + 2 * (col & 7);
   }
 
@@ -353,6 +400,74 @@ CATENA_DEV void gemm_k32_body(const uint16_t* __restrict__ A, const uint16_t* __
       const uint64_t gc = (n0 + (wn & ~1) * 64) / 2 + 8 * cc;
       *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(C) + gr * F + gc) = v;
     }
+  } else if constexpr (ROPE) {
+    // RoPE + bf16 + cache append (catena_rope_qkv_store's arithmetic, the
+    // rotation read from the table the same functions built, requested
+    // before the main loop).  The tile is one head: section n0 / 128 / H
+    // (0 q, 1 k, 2 v), head n0 / 128 % H.  Col blocks 0, 1 of a wave hold x1
+    // of pairs i = 32 wn + 16 j + .., blocks 2, 3 the matching x2 (columns
+    // i + 64), so every lane rotates its own values:
+    //   y1 = x1 c - x2 s, y2 = x2 c + x1 s (q and k; v unrotated), each op
+    //   rounded, c / s at the row's position pos = lens[b] - Tq + tq.
+    // Each wave stages its 64 rows x (32 + 32) bf16 (row r, 16-byte chunk c
+    // at r * 128 + 16 (c ^ ((r >> 1) & 7)); chunks 0-3 the y1 columns, 4-7
+    // the y2 columns) and stores 64-byte runs: q rows always, cache rows when
+    // pos < L (a row before the cache start reads the table at position 0
+    // and writes q only).  No barrier: each wave uses its own LDS.
+    const uint32_t hcol = (uint32_t)(n0 / 128);
+    const uint32_t sect = rsect, head = hcol % rq.H;
+    char* wt = reinterpret_cast<char*>(smem) + wave * (WI * 16 * 128);
+#pragma unroll
+    for (int i = 0; i < WI; ++i) {
+      const uint32_t r = 16 * i + s;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const f32x4_t x1 = acc[i][j], x2 = acc[i][j + 2];
+        f32x4_t y1, y2;
+        if (sect == 2) {
+          y1 = x1;
+          y2 = x2;
+        } else {
+          const f32x4_t cs0 = rcs[i][j][0], cs1 = rcs[i][j][1];  // (c, s) of pairs i .. i + 3
+          const float cv[4] = {cs0[0], cs0[2], cs1[0], cs1[2]};
+          const float sv[4] = {cs0[1], cs0[3], cs1[1], cs1[3]};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float t1 = x1[q] * cv[q], t2 = x2[q] * sv[q], t3 = x2[q] * cv[q], t4 = x1[q] * sv[q];
+            y1[q] = t1 - t2;
+            y2[q] = t3 + t4;
+          }
+        }
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+          const f32x4_t yv = w ? y2 : y1;
+          uint2 p;
+          p.x = pack_bf16x2(yv[0], yv[1]);
+          p.y = pack_bf16x2(yv[2], yv[3]);
+          const uint32_t c = (uint32_t)(4 * w + 2 * j + (G >> 1)) ^ ((r >> 1) & 7u);
+          *reinterpret_cast<uint2*>(wt + r * 128 + 16 * c + 8 * (G & 1)) = p;
+        }
+      }
+    }
+    const uint64_t HD = (uint64_t)rq.H * 128;
+#pragma unroll
+    for (int t = 0; t < WI * 2; ++t) {
+      const uint32_t idx = 64 * t + lane;
+      const uint32_t r = idx >> 3, c = idx & 7;
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(wt + r * 128 + 16 * (c ^ ((r >> 1) & 7u)));
+      const uint64_t gr = m0 + wm * 64 + r;
+      const uint32_t col = (c >> 2) * 64 + wn * 32 + 8 * (c & 3);
+      const uint32_t b = (uint32_t)(gr / rq.Tq), tq = (uint32_t)(gr % rq.Tq);
+      const uint32_t len = rq.lens[b];
+      const bool ok = len >= rq.Tq && len - rq.Tq + tq < rq.L;
+      if (sect == 0) {
+        *reinterpret_cast<u32x4_t*>(rq.q_out + gr * HD + (uint64_t)head * 128 + col) = v;
+      } else if (ok) {
+        const uint32_t pos = len - rq.Tq + tq;
+        uint16_t* cache = sect == 1 ? rq.kc : rq.vc;
+        *reinterpret_cast<u32x4_t*>(cache + (((uint64_t)b * rq.H + head) * rq.L + pos) * 128 + col) = v;
+      }
+    }
   } else if constexpr (OUT_BF16) {
     // Stage the wave's (16 WI) x 64 bf16 tile in its own LDS (row r, 16-byte
     // chunk c at r * 128 + 16 * (c ^ ((r >> 1) & 7))), then store whole
@@ -419,3 +534,16 @@ CATENA_GEMM_K32_KERNEL(catena_gemm_bf16_k32n128_f32out, false, 128)
   }
 CATENA_GEMM_K32_SILU_KERNEL(catena_gemm_bf16_k32_silu, 256)
 CATENA_GEMM_K32_SILU_KERNEL(catena_gemm_bf16_k32n128_silu, 128)
+
+// RoPE + cache append fused (256 x 128 tiles, one head each): no C output;
+// q_out [M][H * 128], kc / vc [B][H][L][128] bf16 (N = 3 H 128, M = B Tq).
+// Dynamic LDS: the stages (96 KiB), which cover the 8 waves' 64 x 128-byte
+// staging.
+extern "C" __global__ __launch_bounds__(512) void catena_gemm_bf16_k32n128_rope(
+    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, uint64_t M, uint64_t N,
+    uint64_t K, const float* __restrict__ tab, const uint32_t* __restrict__ lens,
+    uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+    uint32_t Tq, uint32_t H, uint32_t L) {
+  const RopeQkv rq{tab, lens, q_out, kc, vc, Tq, H, L};
+  gemm_k32_body<false, 128, false, true>(A, B, nullptr, M, N, K, rq);
+}

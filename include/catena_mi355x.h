@@ -404,13 +404,17 @@ typedef enum catena_decoder_tensor {
    * sequence; the last layer's values when n_layers > 1) */
   CATENA_DEC_X,         /* [rows][d] f32: residual stream into the last layer */
   CATENA_DEC_XN,        /* [rows][d] bf16 */
-  CATENA_DEC_QKV,       /* [rows][3d] f32 */
+  CATENA_DEC_QKV,       /* [rows][3d] f32; not written by a prefill of rows % 256 == 0
+                         * (its projection applies RoPE and fills q and the caches in its
+                         * epilogue) */
   CATENA_DEC_Q,         /* [rows][d] bf16 (rotated) */
   CATENA_DEC_ATTN,      /* [rows][d] bf16 */
   CATENA_DEC_ATTN_PROJ, /* [rows][d] f32 */
   CATENA_DEC_H,         /* [rows][d] f32 */
   CATENA_DEC_HN,        /* [rows][d] bf16 */
-  CATENA_DEC_GU,        /* [rows][2F] f32, gate / up interleaved by 64 */
+  CATENA_DEC_GU,        /* [rows][2F] f32, gate / up interleaved by 64; not written by a
+                         * prefill of rows % 256 == 0 (the SwiGLU gate runs in the GEMM's
+                         * epilogue) */
   CATENA_DEC_ACT,       /* [rows][F] bf16 */
   CATENA_DEC_FFN_OUT,   /* [rows][d] f32 */
   CATENA_DEC_FINAL_H,   /* [batch][d] f32: residual stream at the last rows */

@@ -84,6 +84,58 @@ def test_rmsnorm_specials(n):
     _bitwise(yb.read(np.float32, (6, n)), oracle.rmsnorm_f32(x))
 
 
+@pytest.mark.parametrize("n", [2048, 12, 5632])
+def test_rmsnorm_many_rows(n):
+    """2,100 rows (more than one round of workgroups on the device): bitwise
+    the oracle on normal and special rows (zero, NaN, inf, overflowing and
+    underflowing squares, -0), and bitwise the same rows computed as a small
+    batch."""
+    rows = 2100
+    x = _rows(rows, n, n + 17, scale=2.0)
+    x[0] = 0.0
+    x[1, 3] = np.nan
+    x[2, 7] = np.inf
+    x[3] = 3e19
+    x[4] = 1e-30
+    x[5, ::2] = -0.0
+    xb, yb = ca.Buffer.from_array(x), ca.Buffer(x.nbytes)
+    say(f"rmsnorm {rows} rows n={n}")
+    ca.rmsnorm_f32(xb, yb, rows, n)
+    got = yb.read(np.float32, (rows, n))
+    _bitwise(got, oracle.rmsnorm_f32(x))
+    few = ca.Buffer.from_array(np.ascontiguousarray(x[:9]))
+    yf = ca.Buffer(9 * n * 4)
+    ca.rmsnorm_f32(few, yf, 9, n)
+    assert np.array_equal(yf.read(np.uint32, (9, n)), got[:9].view(np.uint32))
+
+
+@pytest.mark.parametrize("rows", [3000, 2049])
+def test_residual_rmsnorm_many_rows(rows):
+    """The residual add, h output and bf16 output over many rows, then the
+    same with a row index selecting 100 fewer rows: both bitwise the
+    oracle."""
+    n = 2048
+    x = _rows(rows, n, 71)
+    r = _rows(rows, n, 72, scale=0.5)
+    x[5, 9] = np.nan
+    r[6] = 3e19
+    xb, rb = ca.Buffer.from_array(x), ca.Buffer.from_array(r)
+    hb, yb = ca.Buffer(rows * n * 4), ca.Buffer(rows * n * 2)
+    say(f"residual rmsnorm {rows} rows")
+    ca.residual_rmsnorm_bf16(xb, rb, None, hb, yb, rows, n)
+    h, y = od.residual_rmsnorm_bf16(x, r)
+    _bitwise(hb.read(np.float32, (rows, n)), h)
+    _bitwise(yb.read(np.uint16, (rows, n)), y)
+    rows_out = rows - 100
+    idx = np.random.default_rng(73).permutation(rows)[:rows_out].astype(np.uint32)
+    ib = ca.Buffer.from_array(idx)
+    say(f"residual rmsnorm {rows_out} indexed rows")
+    ca.residual_rmsnorm_bf16(xb, rb, ib, hb, yb, rows_out, n)
+    h, y = od.residual_rmsnorm_bf16(x[idx.astype(np.int64)], r[idx.astype(np.int64)])
+    _bitwise(hb.read(np.float32, (rows_out, n)), h)
+    _bitwise(yb.read(np.uint16, (rows_out, n)), y)
+
+
 @pytest.mark.parametrize("use_resid,use_index,n", [(True, False, 2048), (False, False, 256),
                                                    (True, True, 2048), (True, True, 10)])
 def test_residual_rmsnorm_bf16(use_resid, use_index, n):

@@ -80,7 +80,17 @@ def _check_forward(dec, cfg, w, tokens, tq, cache_len):
             _bitwise(X, as_f32(w["embed"][toks]))
         XN = rd(ca.DEC_XN, np.uint16, (R, d))
     _bitwise(XN, od.residual_rmsnorm_bf16(X)[1])
-    QKV = rd(ca.DEC_QKV, np.float32, (R, 3 * d))
+    if tq > 1 and R % 256 == 0 and d % 128 == 0:
+        # prefill with RoPE and the cache append in W_qkv's GEMM epilogue:
+        # the f32 product is never written; the plain GEMM recomputes it
+        # (the same tile kernel's order, so the same bits) to check q and
+        # the caches against
+        qkv = ca.Buffer(R * 3 * d * 4)
+        ca.gemm_bf16(ca.Buffer.from_array(XN), ca.Buffer.from_array(w["w_qkv"][lay]), qkv, R, 3 * d,
+                     d, out_f32=True)
+        QKV = qkv.read(np.float32, (R, 3 * d))
+    else:
+        QKV = rd(ca.DEC_QKV, np.float32, (R, 3 * d))
     gemm_within_bound(XN, w["w_qkv"][lay], QKV)
     inv = dec.read(ca.DEC_INV_FREQ, np.float32)
     q, k, v, pos = od.rope_qkv(QKV, inv, lens, B, tq, H, D)
