@@ -42,6 +42,10 @@ struct catena_decoder {
   // the RMSNorms)
   void* parts = nullptr;
   uint64_t parts_bytes = 0;
+  // a prefill's W_down k-split partials ([2][rows][d] f32), added by the norm
+  // that consumes them; grown on first use
+  void* pf_parts = nullptr;
+  uint64_t pf_parts_bytes = 0;
   // the generate loop's deferred LM-head argmax: per-column-block summaries
   // ([max_batch][ceil(vocab / 128)][4] u32) composed by the next step
   void* arg_sums = nullptr;
@@ -117,6 +121,7 @@ void release(catena_decoder* m) {
   pool_free(m->inv_freq);
   pool_free(m->rope_tab);
   pool_free(m->parts);
+  pool_free(m->pf_parts);
   pool_free(m->arg_sums);
   pool_free(m->lens_table);
   for (auto* v : {&m->w_qkv, &m->w_o, &m->w_gu, &m->w_down, &m->kc, &m->vc})
@@ -174,6 +179,22 @@ int forward(catena_decoder& m, const uint32_t* tokens, uint32_t batch, uint32_t 
   }
 
   uint32_t parts_down = 0;  // k groups of the last W_down partials (decode step)
+  // a prefill's W_down as two k-half partials on 256 x 256 tiles (the whole
+  // chip at C5, where one pass fills half of it with those tiles): the norm
+  // that consumes them adds P0 + P1 and writes the sum to FO for its rows
+  const uint32_t kPfSplits = 2;
+  const bool down_split = !step && (uint64_t)(rows / 256) * (d / 256) <= 128 &&
+                          gemm_bf16_ksplit_fits(rows, d, f, kPfSplits, A(CATENA_DEC_ACT), m.w_down[0],
+                                                A(CATENA_DEC_ACT));
+  if (down_split && m.pf_parts_bytes < kPfSplits * rows * d * 4) {
+    TRY(hip_check(hipStreamSynchronize(device().stream), "hipStreamSynchronize"));
+    pool_free(m.pf_parts);
+    m.pf_parts = nullptr;
+    m.pf_parts_bytes = 0;
+    TRY(alloc(kPfSplits * rows * d * 4, &m.pf_parts));
+    m.pf_parts_bytes = kPfSplits * rows * d * 4;
+  }
+  float* PF = static_cast<float*>(m.pf_parts);
   // a decode step whose attention is the eight-wave kernel takes q / k / v
   // as W_qkv's partials
   const bool few_attn = step && attn_few_fits(batch, 1, c.n_heads, c.max_len);
@@ -189,6 +210,8 @@ int forward(catena_decoder& m, const uint32_t* tokens, uint32_t batch, uint32_t 
       // the previous layer's W_down arrives as k-group partials
       TRY(residual_parts_rmsnorm_bf16(H, static_cast<const float*>(m.parts), parts_down, FO, nullptr,
                                       X, XN, rows, rows, d));
+    else if (l > 0 && down_split)
+      TRY(residual_parts_rmsnorm_bf16(H, PF, kPfSplits, FO, nullptr, X, XN, rows, rows, d));
     else if (l > 0)
       TRY(catena_mi355x_residual_rmsnorm_bf16(H, FO, nullptr, X, XN, rows, d));
     uint16_t* kc = static_cast<uint16_t*>(m.kc[l]);
@@ -292,6 +315,8 @@ int forward(catena_decoder& m, const uint32_t* tokens, uint32_t batch, uint32_t 
       // norm or the final norm)
       TRY(gemm_bf16_decode_parts(ACT, static_cast<const uint16_t*>(m.w_down[l]), static_cast<float*>(m.parts),
                                  m.parts_bytes, rows, d, f, &parts_down));
+    else if (down_split)
+      TRY(gemm_bf16_f32_ksplit(ACT, static_cast<const uint16_t*>(m.w_down[l]), PF, rows, d, f, kPfSplits));
     else
       TRY(catena_mi355x_gemm_bf16(ACT, static_cast<const uint16_t*>(m.w_down[l]), FO, rows, d, f, 1));
   }
@@ -301,6 +326,8 @@ int forward(catena_decoder& m, const uint32_t* tokens, uint32_t batch, uint32_t 
   if (step)
     TRY(residual_parts_rmsnorm_bf16(H, static_cast<const float*>(m.parts), parts_down, FO, final_rows, FH,
                                     FXN, batch, rows, d));
+  else if (down_split)
+    TRY(residual_parts_rmsnorm_bf16(H, PF, kPfSplits, FO, final_rows, FH, FXN, batch, rows, d));
   else
     TRY(catena_mi355x_residual_rmsnorm_bf16(H, FO, final_rows, FH, FXN, batch, d));
   const uint16_t* wlm = static_cast<const uint16_t*>(m.w_lm);

@@ -64,6 +64,7 @@ const KernelSpec kKernels[] = {
     {KernelId::GemmBf16K32Silu, "gemm_bf16_k32", "catena_gemm_bf16_k32_silu"},
     {KernelId::GemmBf16K32N128Silu, "gemm_bf16_k32", "catena_gemm_bf16_k32n128_silu"},
     {KernelId::GemmBf16K32N128Rope, "gemm_bf16_k32", "catena_gemm_bf16_k32n128_rope"},
+    {KernelId::GemmBf16K32F32Parts, "gemm_bf16_k32", "catena_gemm_bf16_k32_f32parts"},
     {KernelId::GemmBf16DecodeF32, "gemm_bf16_decode", "catena_gemm_bf16_decode_f32out"},
     {KernelId::GemmBf16DecodeBf16, "gemm_bf16_decode", "catena_gemm_bf16_decode_bf16out"},
     {KernelId::GemmBf16DecodeRope, "gemm_bf16_decode", "catena_gemm_bf16_decode_rope"},

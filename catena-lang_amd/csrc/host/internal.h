@@ -26,6 +26,7 @@ enum class KernelId : int {
   GemmBf16K32Silu,  // the 32-k kernels with the SwiGLU epilogue
   GemmBf16K32N128Silu,
   GemmBf16K32N128Rope,  // the 256 x 128 tile kernel with the RoPE + cache epilogue
+  GemmBf16K32F32Parts,  // 256 x 256 tiles, k split over grid.y, f32 partials
   GemmBf16DecodeF32,
   GemmBf16DecodeBf16,
   GemmBf16DecodeRope,
@@ -235,6 +236,14 @@ bool gemm_bf16_silu_fits(uint64_t n, uint64_t m, uint64_t k, const void* a, cons
 bool gemm_bf16_rope_fits(uint64_t rows, uint64_t k, uint32_t tq, uint32_t heads, const void* a,
                          const void* w, const void* q_out, const void* kc, const void* vc,
                          const void* tab);
+// f32 partials of a k-split GEMM on 256 x 256 tiles: parts[z] [n][m] for
+// z < splits, split z folding k in [z k / splits, (z + 1) k / splits); the
+// consumer adds them in ascending z.  gemm_bf16_ksplit_fits: n % 256 == 0,
+// m % 256 == 0, k % (128 splits) == 0, aligned operands.
+bool gemm_bf16_ksplit_fits(uint64_t n, uint64_t m, uint64_t k, uint32_t splits, const void* a,
+                           const void* b, const void* parts);
+int gemm_bf16_f32_ksplit(const uint16_t* a, const uint16_t* b, float* parts, uint64_t n, uint64_t m,
+                         uint64_t k, uint32_t splits);
 int gemm_bf16_rope_qkv(const uint16_t* a, const uint16_t* w, const float* tab, const uint32_t* lens,
                        uint16_t* q_out, uint16_t* kc, uint16_t* vc, uint64_t rows, uint64_t k,
                        uint32_t tq, uint32_t heads, uint32_t max_len);

@@ -246,6 +246,29 @@ bool gemm_bf16_rope_fits(uint64_t rows, uint64_t k, uint32_t tq, uint32_t heads,
          aligned16(kc) && aligned16(vc) && aligned16(tab) && (rows / 256) * (m / 128) <= 0x7FFFFFFFull;
 }
 
+bool gemm_bf16_ksplit_fits(uint64_t n, uint64_t m, uint64_t k, uint32_t splits, const void* a,
+                           const void* b, const void* parts) {
+  return splits > 0 && splits <= 64 && n % 256 == 0 && m % 256 == 0 && k > 0 &&
+         k % (128ull * splits) == 0 && k <= (1ull << 22) && m <= (1ull << 24) && aligned16(a) &&
+         aligned16(b) && aligned16(parts) && (n / 256) * (m / 256) <= 0x7FFFFFFFull;
+}
+
+int gemm_bf16_f32_ksplit(const uint16_t* a, const uint16_t* b, float* parts, uint64_t n, uint64_t m,
+                         uint64_t k, uint32_t splits) {
+  int st = ensure_init();
+  if (st) return st;
+  if (n == 0 || m == 0) return CATENA_OK;
+  if (!a || !b || !parts) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
+  if (!gemm_bf16_ksplit_fits(n, m, k, splits, a, b, parts))
+    return fail(CATENA_ERR_UNSUPPORTED, "k-split GEMM: shape or alignment not taken");
+  const size_t lds = 4ull * (256 + 256) * 32 * sizeof(uint16_t);
+  if (lds > device().max_lds) return fail(CATENA_ERR_UNSUPPORTED, "device LDS %zu < %zu", device().max_lds, lds);
+  uint64_t k_len = k / splits;
+  void* args[] = {&a, &b, &parts, &n, &m, &k, &k_len};
+  return launch(KernelId::GemmBf16K32F32Parts, dim3((unsigned)((n / 256) * (m / 256)), splits), dim3(512), lds,
+                args);
+}
+
 int gemm_bf16_rope_qkv(const uint16_t* a, const uint16_t* w, const float* tab, const uint32_t* lens,
                        uint16_t* q_out, uint16_t* kc, uint16_t* vc, uint64_t rows, uint64_t k,
                        uint32_t tq, uint32_t heads, uint32_t max_len) {

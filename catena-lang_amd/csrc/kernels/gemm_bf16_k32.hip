@@ -95,10 +95,14 @@ struct RopeQkv {
   uint32_t Tq, H, L;
 };
 
+// K is the depth this workgroup folds; lda (0: K) is A's row stride, which a
+// k-split launch sets to the whole depth (A and B then start at the split's
+// first k).
 template <bool OUT_BF16, int BN, bool SILU = false, bool ROPE = false>
 CATENA_DEV void gemm_k32_body(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                               void* __restrict__ C, uint64_t M, uint64_t N, uint64_t K,
-                              const RopeQkv& rq = RopeQkv{}) {
+                              const RopeQkv& rq = RopeQkv{}, uint64_t lda = 0) {
+  const uint64_t LDA = lda ? lda : K;
   static_assert(!ROPE || BN == 128, "the RoPE epilogue pairs the two column waves of a 128-wide tile");
   static_assert(BN == 256 || BN == 128, "tile widths 256 and 128");
   constexpr int B_ST = BK * BN;                // elements per B stage
@@ -126,7 +130,7 @@ CATENA_DEV void gemm_k32_body(const uint16_t* __restrict__ A, const uint16_t* __
   {
     const uint32_t r = 32 * wave + (lane >> 2);
     const uint32_t q = (uint32_t)(lane & 3) ^ ((r >> 1) & 3u);
-    aoff = (uint32_t)((r * K + 8 * q) * 2);
+    aoff = (uint32_t)((r * LDA + 8 * q) * 2);
     const uint32_t kr = (64 / B_LANES) * wave + (uint32_t)lane / B_LANES;
     const uint32_t qb = (uint32_t)(lane % B_LANES) ^ hB(kr);
     boff = (uint32_t)((kr * N + 8 * qb) * 2);
@@ -137,10 +141,10 @@ CATENA_DEV void gemm_k32_body(const uint16_t* __restrict__ A, const uint16_t* __
     const bool live = k0 < K;
     if (idx < 2) {
       const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)(A + m0 * K + (live ? k0 : 0)), (short)0, live ? (int)(BM * K * 2) : 0, kRsrcWord3);
+          (void*)(A + m0 * LDA + (live ? k0 : 0)), (short)0, live ? (int)(BM * LDA * 2) : 0, kRsrcWord3);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rs, (lds_void*)(smem + stage * A_ST + (32 * wave + 16 * idx) * BK), 16, (int)aoff,
-          idx ? (int)(16 * K * 2) : 0, 0, 0);
+          idx ? (int)(16 * LDA * 2) : 0, 0, 0);
     } else {
       const int b = idx - 2;
       const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
@@ -546,4 +550,16 @@ extern "C" __global__ __launch_bounds__(512) void catena_gemm_bf16_k32n128_rope(
     uint32_t Tq, uint32_t H, uint32_t L) {
   const RopeQkv rq{tab, lens, q_out, kc, vc, Tq, H, L};
   gemm_k32_body<false, 128, false, true>(A, B, nullptr, M, N, K, rq);
+}
+
+// k-split f32 partials (256 x 256 tiles): grid (tiles, splits); split z folds
+// k in [z k_len, (z + 1) k_len) of the K_total-deep product in the tile
+// kernel's order and writes P[z] = its [M][N] f32 partial.  The consumer adds
+// P[0] + P[1] + ... in ascending z.  Dynamic LDS as the 256 x 256 kernel.
+extern "C" __global__ __launch_bounds__(512) void catena_gemm_bf16_k32_f32parts(
+    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, float* __restrict__ P,
+    uint64_t M, uint64_t N, uint64_t K_total, uint64_t k_len) {
+  const uint64_t z = blockIdx.y;
+  gemm_k32_body<false, 256>(A + z * k_len, B + z * k_len * N, P + z * M * N, M, N, k_len, RopeQkv{},
+                            K_total);
 }

@@ -416,7 +416,10 @@ typedef enum catena_decoder_tensor {
                          * prefill of rows % 256 == 0 (the SwiGLU gate runs in the GEMM's
                          * epilogue) */
   CATENA_DEC_ACT,       /* [rows][F] bf16 */
-  CATENA_DEC_FFN_OUT,   /* [rows][d] f32 */
+  CATENA_DEC_FFN_OUT,   /* [rows][d] f32; after a prefill whose W_down runs as k-half
+                         * partials (rows % 256 == 0, d % 256 == 0, d_ff % 256 == 0, at
+                         * most 128 tiles of 256 x 256) only the rows the final norm reads
+                         * (each sequence's last) hold the sum */
   CATENA_DEC_FINAL_H,   /* [batch][d] f32: residual stream at the last rows */
   CATENA_DEC_FINAL_XN,  /* [batch][d] bf16 */
   CATENA_DEC_LOGITS,    /* [batch][vocab] f32 */

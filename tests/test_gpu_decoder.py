@@ -125,8 +125,13 @@ def _check_forward(dec, cfg, w, tokens, tq, cache_len):
     ACT = rd(ca.DEC_ACT, np.uint16, (R, F))
     _bitwise(ACT, od.silu_mul_bf16(GU, F, 64))
     FO = rd(ca.DEC_FFN_OUT, np.float32, (R, d))
-    gemm_within_bound(ACT, w["w_down"][lay], FO)
     last = np.arange(B) * tq + (tq - 1)
+    if tq > 1 and R % 256 == 0 and d % 256 == 0 and F % 256 == 0 and (R // 256) * (d // 256) <= 128:
+        # prefill with W_down as two k-half partials, added by the final norm,
+        # which writes the sums of the rows it reads (each sequence's last)
+        gemm_within_bound(ACT[last], w["w_down"][lay], FO[last])
+    else:
+        gemm_within_bound(ACT, w["w_down"][lay], FO)
     fh, fxn = od.residual_rmsnorm_bf16(Hh[last], FO[last])
     _bitwise(rd(ca.DEC_FINAL_H, np.float32, (B, d)), fh)
     FXN = rd(ca.DEC_FINAL_XN, np.uint16, (B, d))
