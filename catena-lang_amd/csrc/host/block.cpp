@@ -110,11 +110,12 @@ int catena_mi355x_attn_causal_bf16(const uint16_t* q, const uint16_t* k, const u
   if (blocks > 0x7FFFFFFFu) return fail(CATENA_ERR_UNSUPPORTED, "too many queries");
   // Many queries per sequence: the block-of-16-queries kernel, which reads
   // each K / V row once per block (its score buffer grows with max_len, so
-  // it is used while two workgroups still fit a CU); otherwise the
-  // one-query-per-workgroup kernel.  Both give the same bits.
+  // it is used while two workgroups still fit a CU; it reads q rows with
+  // 16-byte loads); otherwise the one-query-per-workgroup kernel.  Both give
+  // the same bits.
   const size_t lds_pf =
       16 * 132 * 4 + 16 * 136 * 2 + 64 * 128 * 2 + 3 * 16 * 4 + (size_t)max_len * 17 * 4;
-  if (tq >= 8 && lds_pf <= 80 * 1024) {
+  if (tq >= 8 && lds_pf <= 80 * 1024 && aligned16(q)) {
     const uint64_t nqb = ceil_div(tq, 16);
     const uint64_t grid = (uint64_t)batch * heads * nqb;
     if (grid > 0x7FFFFFFFu) return fail(CATENA_ERR_UNSUPPORTED, "too many query blocks");

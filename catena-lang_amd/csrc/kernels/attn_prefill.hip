@@ -109,15 +109,20 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
   const uint16_t* vb = v + (uint64_t)bh * L * D;
   // q rows of this block, widened (rows past nq are zero and never used);
   // `unsafe` notes a value outside the MFMA fold's exact range
+  // thread t: row t / 16, values 8 (t % 16) .. +7 (one 16-byte load)
   int unsafe = 0;
-  for (uint32_t e = tid; e < (uint32_t)QB * D; e += 256) {
-    const uint32_t i = e / D, d = e % D;
-    uint16_t bits = 0;
-    if (i < nq) bits = q[(((uint64_t)b * Tq + t0 + i) * H + h) * D + d];
-    const uint32_t mag = bits & 0x7FFFu;
-    unsafe |= (mag != 0u && mag < kSafeLo) || mag >= kSafeHi;
-    qf[i * QS + d] = bf16_to_f32(bits);
-    qh[i * QH + d] = bits;
+  {
+    const uint32_t i = (uint32_t)tid / 16, d0 = 8 * ((uint32_t)tid % 16);
+    const u32x4_t w = i < nq ? *reinterpret_cast<const u32x4_t*>(q + (((uint64_t)b * Tq + t0 + i) * H + h) * D + d0)
+                             : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t lo = w[c] & 0x7FFFu, hi = (w[c] >> 16) & 0x7FFFu;
+      unsafe |= (lo != 0u && lo < kSafeLo) || lo >= kSafeHi || (hi != 0u && hi < kSafeLo) || hi >= kSafeHi;
+    }
+    *reinterpret_cast<f32x4_t*>(qf + i * QS + d0) = f32x4_t{bf16lo(w[0]), bf16hi(w[0]), bf16lo(w[1]), bf16hi(w[1])};
+    *reinterpret_cast<f32x4_t*>(qf + i * QS + d0 + 4) = f32x4_t{bf16lo(w[2]), bf16hi(w[2]), bf16lo(w[3]), bf16hi(w[3])};
+    *reinterpret_cast<u32x4_t*>(qh + i * QH + d0) = w;
   }
   __syncthreads();
 
