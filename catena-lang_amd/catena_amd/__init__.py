@@ -142,6 +142,9 @@ SIGNATURES = {
     "catena_mi355x_rope_qkv_bf16": (_int, [_vp] * 6 + [_u32] * 5),
     "catena_mi355x_silu_mul_bf16": (_int, [_vp, _vp, _u64, _u32, _u32]),
     "catena_mi355x_gemm_bf16_silu": (_int, [_vp, _vp, _vp, _u64, _u64, _u64]),
+    "catena_mi355x_rope_table_f32": (_int, [_vp, _vp, _u32, _u32]),
+    "catena_mi355x_gemm_bf16_rope_qkv": (_int, [_vp] * 7 + [_u32] * 4 + [_u64]),
+    "catena_mi355x_gemm_bf16_ksplit_f32": (_int, [_vp, _vp, _vp, _u64, _u64, _u64, _u32]),
     "catena_mi355x_argmax_f32": (_int, [_vp, _vp, _u64, _u64]),
     "catena_mi355x_broadcast_f32": (_int, [_vp, _u64, _f32]),
     "catena_mi355x_arange_f32": (_int, [_vp, _u64]),
@@ -418,6 +421,25 @@ def gemm_bf16_silu(a, b, act, n: int, m: int, k: int) -> None:
     """act[n][m/2] = bf16(silu(gate) * up) of A[n][k] x B[k][m] (gate / up in
     groups of 64 columns), the GEMM and catena_mi355x_silu_mul_bf16 in one."""
     check(lib().catena_mi355x_gemm_bf16_silu(_p(a), _p(b), _p(act), n, m, k))
+
+
+def rope_table_f32(inv_freq, tab, positions: int, head_dim: int) -> None:
+    """tab[pos][i] = (cos, sin) of (f32)pos * inv_freq[i], i < head_dim / 2."""
+    check(lib().catena_mi355x_rope_table_f32(_p(inv_freq), _p(tab), positions, head_dim))
+
+
+def gemm_bf16_rope_qkv(a, w, rope_tab, lens, q, k_cache, v_cache, batch: int, tq: int, heads: int,
+                       max_len: int, k: int) -> None:
+    """The q / k / v projection of a[batch*tq][k] by w[k][3*heads*128] with
+    RoPE and the cache append fused (gemm_bf16 f32 then rope_qkv_bf16)."""
+    check(lib().catena_mi355x_gemm_bf16_rope_qkv(_p(a), _p(w), _p(rope_tab), _p(lens), _p(q),
+                                                 _p(k_cache), _p(v_cache), batch, tq, heads,
+                                                 max_len, k))
+
+
+def gemm_bf16_ksplit_f32(a, b, parts, n: int, m: int, k: int, splits: int) -> None:
+    """parts[z][n][m] = A[:, kz] x B[kz, :] over the z-th of `splits` equal k ranges."""
+    check(lib().catena_mi355x_gemm_bf16_ksplit_f32(_p(a), _p(b), _p(parts), n, m, k, splits))
 
 
 def argmax_f32(x, idx, rows: int, n: int) -> None:

@@ -169,6 +169,12 @@ int catena_mi355x_rope_inv_freq(float* out_host, uint32_t head_dim, double base)
   return CATENA_OK;
 }
 
+int catena_mi355x_rope_table_f32(const float* inv_freq, float* tab, uint32_t positions,
+                                 uint32_t head_dim) {
+  if (head_dim % 2 != 0) return fail(CATENA_ERR_INVALID_ARGUMENT, "rope needs an even head_dim");
+  return rope_table_f32(inv_freq, tab, positions, head_dim / 2);
+}
+
 int catena_mi355x_rope_qkv_bf16(const float* qkv, const float* inv_freq, const uint32_t* lens,
                                 uint16_t* q, uint16_t* k_cache, uint16_t* v_cache,
                                 uint32_t batch, uint32_t tq, uint32_t heads, uint32_t head_dim,

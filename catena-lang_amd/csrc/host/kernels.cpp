@@ -393,6 +393,36 @@ int catena_mi355x_gemm_bf16_silu(const uint16_t* a, const uint16_t* b, uint16_t*
                 dim3(512), lds, args);
 }
 
+int catena_mi355x_gemm_bf16_rope_qkv(const uint16_t* a, const uint16_t* w, const float* rope_tab,
+                                     const uint32_t* lens, uint16_t* q, uint16_t* k_cache,
+                                     uint16_t* v_cache, uint32_t batch, uint32_t tq, uint32_t heads,
+                                     uint32_t max_len, uint64_t k) {
+  int st = ensure_init();
+  if (st) return st;
+  const uint64_t rows = (uint64_t)batch * tq;
+  if (rows == 0 || heads == 0) return CATENA_OK;
+  if (!a || !w || !rope_tab || !lens || !q || !k_cache || !v_cache)
+    return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
+  if (!gemm_bf16_rope_fits(rows, k, tq, heads, a, w, q, k_cache, v_cache, rope_tab))
+    return fail(CATENA_ERR_UNSUPPORTED,
+                "fused q / k / v projection needs batch * tq %% 256 == 0, k %% 128 == 0 (k <= 2^22) "
+                "and 16-byte aligned pointers");
+  return gemm_bf16_rope_qkv(a, w, rope_tab, lens, q, k_cache, v_cache, rows, k, tq, heads, max_len);
+}
+
+int catena_mi355x_gemm_bf16_ksplit_f32(const uint16_t* a, const uint16_t* b, float* parts,
+                                       uint64_t n, uint64_t m, uint64_t k, uint32_t splits) {
+  int st = ensure_init();
+  if (st) return st;
+  if (n == 0 || m == 0) return CATENA_OK;
+  if (!a || !b || !parts) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
+  if (!gemm_bf16_ksplit_fits(n, m, k, splits, a, b, parts))
+    return fail(CATENA_ERR_UNSUPPORTED,
+                "k-split GEMM needs 1 <= splits <= 64, n %% 256 == 0, m %% 256 == 0, "
+                "k %% (128 splits) == 0 (k <= 2^22) and 16-byte aligned pointers");
+  return gemm_bf16_f32_ksplit(a, b, parts, n, m, k, splits);
+}
+
 int catena_mi355x_gemm_bf16_argmax(const uint16_t* a, const uint16_t* b, float* c, uint32_t* idx,
                                    uint64_t n, uint64_t m, uint64_t k) {
   int st = ensure_init();

@@ -242,6 +242,36 @@ int catena_mi355x_rope_qkv_bf16(const float *qkv, const float *inv_freq, const u
                                 uint32_t batch, uint32_t tq, uint32_t heads, uint32_t head_dim,
                                 uint32_t max_len);
 
+/* The rotation table of catena_mi355x_rope_qkv_bf16 for positions 0 ..
+ * positions - 1: tab[pos][i] = (cos, sin) of theta = (f32)pos * inv_freq[i],
+ * i < head_dim / 2, f32 pairs -- the values that call computes per row.
+ * positions <= 65535.  No reference counterpart. */
+int catena_mi355x_rope_table_f32(const float *inv_freq, float *tab, uint32_t positions,
+                                 uint32_t head_dim);
+
+/* The decoder's prefill q / k / v projection in one kernel:
+ * catena_mi355x_gemm_bf16(a, w, qkv, batch * tq, 3 * heads * 128, k, out_f32 = 1)
+ * followed by catena_mi355x_rope_qkv_bf16(qkv, ..., head_dim = 128), bitwise,
+ * without writing the f32 product.  a[batch * tq][k], w[k][3 * heads * 128]
+ * bf16; rope_tab from catena_mi355x_rope_table_f32 with at least max_len
+ * positions.  Rows whose position lens[b] - tq + t falls outside [0, max_len)
+ * write q (rotated at position 0) and no cache row.  Needs batch * tq % 256
+ * == 0, k % 128 == 0, k <= 2^22, 16-byte aligned pointers; other shapes
+ * return CATENA_ERR_UNSUPPORTED.  No reference counterpart. */
+int catena_mi355x_gemm_bf16_rope_qkv(const uint16_t *a, const uint16_t *w, const float *rope_tab,
+                                     const uint32_t *lens, uint16_t *q, uint16_t *k_cache,
+                                     uint16_t *v_cache, uint32_t batch, uint32_t tq, uint32_t heads,
+                                     uint32_t max_len, uint64_t k);
+
+/* bf16 GEMM as f32 k-split partials (the decoder's prefill W_down):
+ * parts[z][n][m] = the product over k in [z k / splits, (z + 1) k / splits),
+ * each folded as catena_mi355x_gemm_bf16 folds a product; a consumer adds
+ * them in ascending z.  Needs 1 <= splits <= 64, n % 256 == 0, m % 256 == 0,
+ * k % (128 splits) == 0, k <= 2^22, 16-byte aligned pointers.  No reference
+ * counterpart. */
+int catena_mi355x_gemm_bf16_ksplit_f32(const uint16_t *a, const uint16_t *b, float *parts,
+                                       uint64_t n, uint64_t m, uint64_t k, uint32_t splits);
+
 /* SwiGLU gate: gu[rows][2F] f32 -> out[rows][F] = bf16(nn.silu(gate) * up)
  * (catena-lang/stdlib/nn.hex:1-21).  group = 0: columns gate | up; group =
  * G: gate and up interleaved in groups of G columns (gate 0..G-1, up

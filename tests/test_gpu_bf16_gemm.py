@@ -327,6 +327,94 @@ def test_gemm_swiglu_special_values():
     assert np.isnan(g[3]).all() and not np.isfinite(g[5]).all() and np.isnan(g[9, 64:128]).all()
 
 
+@pytest.mark.parametrize("B,Tq,H,L,k,lens", [
+    (2, 128, 2, 300, 256, [128, 300]),        # empty cache; a cached prefix of 172
+    (1, 256, 3, 200, 128, [256]),             # rows 200..255 past the cache end: q only
+    (4, 64, 1, 128, 384, [64, 10, 128, 100]),  # lens < Tq: no cache row for batch 1
+    (256, 1, 2, 64, 128, "random"),           # decode-shaped rows, lens 0 .. 80
+])
+def test_gemm_rope_qkv_fused_equals_gemm_then_rope(B, Tq, H, L, k, lens):
+    """The RoPE-fused q / k / v projection (the decoder's prefill W_qkv) gives
+    the bits of the f32 GEMM followed by catena_mi355x_rope_qkv_bf16: q for
+    every row, cache rows only at positions in [0, L), every other cache
+    element untouched -- with cached prefixes, rows past the cache end and
+    sequences shorter than Tq."""
+    D, R = 128, B * Tq
+    m = 3 * H * D
+    if lens == "random":
+        lens = np.random.default_rng(B + L).integers(0, 81, B).tolist()
+    a = dev_normal_bf16(R * k, 17 + k, 0, 1.0)
+    w = dev_normal_bf16(k * m, 17 + k, 1, 0.2)
+    inv = ca.Buffer.from_array(ca.rope_inv_freq(D, 10000.0))
+    tab = ca.Buffer(L * D * 4)
+    ca.rope_table_f32(inv, tab, L, D)
+    lb = ca.Buffer.from_array(np.array(lens, np.uint32))
+    sentinel = np.full(B * H * L * D, 0xABCD, np.uint16)
+    caches = [ca.Buffer.from_array(sentinel) for _ in range(4)]
+    q_f, q_u = ca.Buffer(R * H * D * 2), ca.Buffer(R * H * D * 2)
+    say(f"fused q/k/v + RoPE B={B} Tq={Tq} H={H} L={L} k={k} lens={lens[:6]}")
+    ca.gemm_bf16_rope_qkv(a, w, tab, lb, q_f, caches[0], caches[1], B, Tq, H, L, k)
+    qkv = ca.Buffer(R * m * 4)
+    ca.gemm_bf16(a, w, qkv, R, m, k, out_f32=True)
+    ca.rope_qkv_bf16(qkv, inv, lb, q_u, caches[2], caches[3], B, Tq, H, D, L)
+    assert np.array_equal(q_f.read(np.uint16), q_u.read(np.uint16))
+    for got, want in ((caches[0], caches[2]), (caches[1], caches[3])):
+        g, w_ = got.read(np.uint16, (B, H, L, D)), want.read(np.uint16, (B, H, L, D))
+        assert np.array_equal(g, w_), int(np.sum(g != w_))
+    written = (caches[2].read(np.uint16, (B, H, L, D)) != 0xABCD).any(axis=(1, 3))
+    for b, n_ in enumerate(lens):  # the positions a row of batch b lands on
+        want = np.zeros(L, bool)
+        if n_ >= Tq:
+            want[n_ - Tq:min(n_, L)] = True
+        assert np.array_equal(written[b], want), b
+
+
+def test_gemm_rope_qkv_rejects_untiled_shapes():
+    a, w = ca.Buffer(256 * 256 * 2), ca.Buffer(256 * 384 * 2)
+    tab, lb = ca.Buffer(64 * 128 * 4), ca.Buffer(4 * 4)
+    q, kc, vc = ca.Buffer(256 * 128 * 2), ca.Buffer(4 * 64 * 128 * 2), ca.Buffer(4 * 64 * 128 * 2)
+    with pytest.raises(ca.CatenaError):
+        ca.gemm_bf16_rope_qkv(a, w, tab, lb, q, kc, vc, 2, 100, 1, 64, 256)  # rows % 256
+    with pytest.raises(ca.CatenaError):
+        ca.gemm_bf16_rope_qkv(a, w, tab, lb, q, kc, vc, 1, 256, 1, 64, 96)   # k % 128
+
+
+@pytest.mark.parametrize("n,m,k,splits", [(256, 256, 256, 2), (256, 4096, 11008, 2),
+                                          (512, 512, 1536, 3), (256, 256, 128, 1)])
+def test_gemm_ksplit_parts_equal_gemm_of_each_k_range(n, m, k, splits):
+    """parts[z] of the k-split GEMM (the decoder's prefill W_down) is bitwise
+    the f32 GEMM of the z-th k range, and their ascending sum is within the
+    bf16 GEMM bound of the whole product."""
+    rng = np.random.default_rng(n + k + splits)
+    a16 = oracle.f32_to_bf16_bits_np(rng.standard_normal((n, k)).astype(np.float32))
+    b16 = oracle.f32_to_bf16_bits_np((rng.standard_normal((k, m)) * 0.1).astype(np.float32))
+    parts = ca.Buffer(splits * n * m * 4)
+    say(f"k-split GEMM n={n} m={m} k={k} splits={splits}")
+    ca.gemm_bf16_ksplit_f32(ca.Buffer.from_array(a16), ca.Buffer.from_array(b16), parts, n, m, k,
+                            splits)
+    got = parts.read(np.float32, (splits, n, m))
+    kl = k // splits
+    for z in range(splits):
+        az = ca.Buffer.from_array(np.ascontiguousarray(a16[:, z * kl:(z + 1) * kl]))
+        bz = ca.Buffer.from_array(np.ascontiguousarray(b16[z * kl:(z + 1) * kl]))
+        cz = ca.Buffer(n * m * 4)
+        ca.gemm_bf16(az, bz, cz, n, m, kl, out_f32=True)
+        assert np.array_equal(got[z].view(np.uint32), cz.read(np.uint32, (n, m))), z
+    total = got[0].copy()
+    for z in range(1, splits):
+        total = total + got[z]
+    rows = np.arange(0, n, max(1, n // 16))
+    gemm_within_bound(a16[rows], b16, total[rows])
+
+
+def test_gemm_ksplit_rejects_untiled_shapes():
+    a, b, p = ca.Buffer(256 * 384 * 2), ca.Buffer(384 * 256 * 2), ca.Buffer(2 * 256 * 256 * 4)
+    with pytest.raises(ca.CatenaError):
+        ca.gemm_bf16_ksplit_f32(a, b, p, 256, 256, 384, 2)   # k % 256
+    with pytest.raises(ca.CatenaError):
+        ca.gemm_bf16_ksplit_f32(a, b, p, 256, 256, 384, 0)   # splits == 0
+
+
 def _lm_head_case(x16, w16, n, m, k):
     """The fused LM head (catena_mi355x_gemm_bf16_argmax): its logits within
     the GEMM bound where finite, and every index equal to the oracle's
