@@ -105,11 +105,11 @@ inline size_t attn_lds_bytes(uint32_t max_len) { return kAttnLdsFixed + (size_t)
 
 // The eight-wave attention (attn_few.hip) for few (query, head) pairs, where
 // the four-wave kernel leaves CUs idle or underfed: one workgroup per pair,
-// at most one per CU.  LDS: six q copies and the max words, six 4 KiB K
-// stages and two 48 KiB V rings (124 KiB), then 64 f32 scores per 64-row
-// block.
+// at most one per CU.  LDS: six q copies and the max words, 64 KiB for the
+// six 4 KiB K stages and later the two product slots, two 40 KiB V rings
+// (148 KiB), then 64 f32 scores per 64-row block.
 constexpr uint64_t kAttnFewMaxQueries = 256;
-constexpr size_t kAttnFewFixed = 4096 + 6 * 4096 + 2 * 6 * 8192;
+constexpr size_t kAttnFewFixed = 4096 + 2 * 32768 + 2 * 5 * 8192;
 inline size_t attn_few_lds_bytes(uint32_t max_len) {
   return kAttnFewFixed + (size_t)((max_len + 63) / 64) * (64 * 4);
 }

@@ -28,15 +28,19 @@
 // Waves 6 and 7 own output columns 0-63 and 64-127.  Once the score waves
 // have requested their K rows (so that K, which is needed first, is ahead
 // of V in the memory queues) they stream their V rows (128 bytes per row)
-// straight into private LDS rings of 64-row batches, and once p is ready
-// fold their columns (lane = column) t ascending: each half batch is read
-// into registers while the previous one is folded, and a slot is refilled as
-// soon as its batch is in registers.
+// straight into LDS rings of 64-row batches.  Once p is ready the batches
+// go through rounds separated by workgroup barriers: in round b the score
+// waves make batch b + 1's rounded products p_t * v_{t,c} into one of two
+// product slots (16 units of 8 rows x 64 columns) while waves 6 and 7
+// add batch b's products from the other slot, lane = column, t ascending,
+// and refill the ring slot batch b came from.
 //
-// Cost (measured on MI355X at 2.4 GHz): one wave issues a VALU op about
-// every 4.1 cycles and a chain of dependent v_add_f32 runs at about 4.5
-// cycles per add, so the V fold (unpack, multiply, add per position and
-// column) is issue-bound at about 12.5 cycles per position.
+// Cost (measured on MI355X): a wave that runs alone on its SIMD issues an
+// instruction about every 4-5 cycles whatever its kind, so a fold that
+// unpacks, multiplies and adds per position and column in the same wave,
+// with its ring bookkeeping, took about 25 cycles per position.  Split this
+// way, the adding waves issue one v_add_f32 and a quarter of a 16-byte LDS
+// read per position, and the multiplies run on all four SIMDs.
 #include "common.h"
 
 namespace {
@@ -48,16 +52,20 @@ CATENA_DEV uint32_t kswz(uint32_t row, uint32_t chunk) { return 16u * (chunk ^ (
 
 constexpr int VB_ROWS = 64;              // rows per V batch
 constexpr int VB_BYTES = VB_ROWS * 128;  // 64 rows x 64 columns bf16
-constexpr int VRING = 6;                 // batches in flight per V wave (8 loads each)
+constexpr int VRING = 5;                 // batches in flight per V wave (8 loads each)
+constexpr int PSLOT_BYTES = 2 * 64 * 64 * 4;  // one batch's products, both column halves
 
 // LDS: q copies [6][128] f32 | den, last score, last NaN, max keys | new key
-// row | K stages [6][4 KiB] | V rings [2][VRING][8 KiB] | scores
+// row | K stages [6][4 KiB] until the scores are done, then the product
+// slots [2][PSLOT_BYTES] | V rings [2][VRING][8 KiB] | scores
 // sp[64 * ceil(L/64)]
 constexpr uint32_t kOffDen = KWAVES * 512;
 constexpr uint32_t kOffKNew = kOffDen + 256;  // the new key row (partials mode), 256 B
 constexpr uint32_t kOffK = 4096;
-constexpr uint32_t kOffV = kOffK + KWAVES * KSTAGE_WAVE;
+constexpr uint32_t kOffP = 4096;
+constexpr uint32_t kOffV = kOffP + 2 * PSLOT_BYTES;
 constexpr uint32_t kOffState = kOffV + 2 * VRING * VB_BYTES;
+static_assert(kOffK + KWAVES * KSTAGE_WAVE <= kOffV, "K stages inside the product slots' space");
 
 CATENA_DEV void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -78,6 +86,14 @@ CATENA_DEV void lds_barrier() {
 // s_waitcnt on vmcnt only (gfx9 encoding: vmcnt[3:0], vmcnt[5:4] at 15:14)
 #define FEW_WAIT_VMCNT(n) \
   __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | 0x0070 | 0x0F00)
+// s_waitcnt on lgkmcnt only (bits 11:8), pinned in place by scheduling
+// barriers so that the reads and adds around it keep their order
+#define FEW_WAIT_LGKM(n)                                   \
+  do {                                                     \
+    __builtin_amdgcn_sched_barrier(0);                     \
+    __builtin_amdgcn_s_waitcnt(0xC07F | ((n) << 8));       \
+    __builtin_amdgcn_sched_barrier(0);                     \
+  } while (0)
 
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
@@ -153,38 +169,57 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* k,
   const bool pos_ok = raw_len >= 1u && raw_len - 1u < L;
   const uint32_t pos = pos_ok ? raw_len - 1u : 0u;
   const uint64_t HD = (uint64_t)H * D;
-  // columns c and c2 of the fused row, parts added in ascending order; the
-  // first four parts' loads are all issued before the first add
-  auto part_sums = [&](uint64_t c, uint64_t c2, float& x, float& x2) {
+  // Columns c and c2 of the fused row, parts added in ascending order, in
+  // two steps so that callers can put other loads between them: part_loads
+  // issues the first four parts' loads, part_sums adds them (and loads and
+  // adds any further parts).
+  struct PartLoads {
+    uint64_t c, c2;
+    float v[4], v2[4];
+  };
+  auto part_loads = [&](uint64_t c, uint64_t c2, PartLoads& pl) {
     const float* p = qkv.parts + (uint64_t)row * 3 * HD;
     const uint32_t n = qkv.n_parts;
-    float v[4], v2[4];
+    pl.c = c;
+    pl.c2 = c2;
 #pragma unroll
     for (uint32_t u = 0; u < 4; ++u) {
       const uint64_t o = (u < n ? u : 0u) * qkv.part_stride;
-      v[u] = p[o + c];
-      v2[u] = p[o + c2];
+      pl.v[u] = p[o + c];
+      pl.v2[u] = p[o + c2];
     }
-    x = v[0];
-    x2 = v2[0];
+  };
+  auto part_sums = [&](const PartLoads& pl, float& x, float& x2) {
+    const float* p = qkv.parts + (uint64_t)row * 3 * HD;
+    const uint32_t n = qkv.n_parts;
+    x = pl.v[0];
+    x2 = pl.v2[0];
 #pragma unroll
     for (uint32_t u = 1; u < 4; ++u) {  // (selects, not branches: one straight sequence)
-      const float s1 = x + v[u], s2 = x2 + v2[u];
+      const float s1 = x + pl.v[u], s2 = x2 + pl.v2[u];
       x = u < n ? s1 : x;
       x2 = u < n ? s2 : x2;
     }
     for (uint32_t u = 4; u < n; ++u) {
-      x = x + p[u * qkv.part_stride + c];
-      x2 = x2 + p[u * qkv.part_stride + c2];
+      x = x + p[u * qkv.part_stride + pl.c];
+      x2 = x2 + p[u * qkv.part_stride + pl.c2];
     }
   };
-  // pair (lane, lane + 64) of head h's part 0 (q) or 1 (k), rotated:
+  // pair (lane, lane + 64) of head h's part 0 (q) or 1 (k): rope_loads
+  // issues its loads, rope_pair adds the parts and rotates,
   // y1 = x1 c - x2 s, y2 = x2 c + x1 s (each op rounded)
-  auto rope_pair = [&](uint32_t part, float& x1, float& x2, float& y1, float& y2) {
+  struct RopeLoads {
+    PartLoads pl;
+    float2 cp;
+  };
+  auto rope_loads = [&](uint32_t part, RopeLoads& rl) {
     const uint64_t c0 = part * HD + (uint64_t)h * D + (uint32_t)lane;
-    const float2 cp = reinterpret_cast<const float2*>(qkv.rope_tab)[(uint64_t)pos * 64 + (uint32_t)lane];
-    part_sums(c0, c0 + 64, x1, x2);
-    const float t1 = x1 * cp.x, t2 = x2 * cp.y, t3 = x2 * cp.x, t4 = x1 * cp.y;
+    rl.cp = reinterpret_cast<const float2*>(qkv.rope_tab)[(uint64_t)pos * 64 + (uint32_t)lane];
+    part_loads(c0, c0 + 64, rl.pl);
+  };
+  auto rope_pair = [&](const RopeLoads& rl, float& x1, float& x2, float& y1, float& y2) {
+    part_sums(rl.pl, x1, x2);
+    const float t1 = x1 * rl.cp.x, t2 = x2 * rl.cp.y, t3 = x2 * rl.cp.x, t4 = x1 * rl.cp.y;
     y1 = t1 - t2;
     y2 = t3 + t4;
   };
@@ -206,16 +241,14 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* k,
     const uint32_t vr = (uint32_t)lane >> 3, vc = (uint32_t)lane & 7u;
     const uint16_t* vlane = vb + (uint64_t)vr * D + colbase + 8 * vc;
     // partials mode: this wave's column of the new value row, to the cache
-    // now and into its V batch once that batch is in LDS
+    // and into its V batch once that batch is in LDS; its parts' loads go
+    // out now, the sum is taken once the first V batches are requested
     const bool new_val = qkv.parts && pos_ok;
     uint16_t vnew = 0;
+    PartLoads vpl;
     if (qkv.parts) {
-      float x, x_unused;
       const uint64_t cv = 2 * HD + (uint64_t)h * D + colbase + (uint32_t)lane;
-      part_sums(cv, cv, x, x_unused);
-      vnew = (uint16_t)f32_to_bf16_bits(x);
-      if (pos_ok) qkv.v_cache[(bh * L + pos) * D + colbase + lane] = vnew;
-      if (qkv.qkv_out) qkv.qkv_out[(uint64_t)row * 3 * HD + 2 * HD + (uint64_t)h * D + colbase + lane] = x;
+      part_loads(cv, cv, vpl);
     }
     const uint32_t bt_new = pos / (uint32_t)VB_ROWS;
     auto put_new_val = [&](uint32_t bt) {
@@ -246,6 +279,13 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* k,
     __builtin_amdgcn_s_barrier();  // (0) K requested, max words cleared
     const uint32_t pre = nblk < (uint32_t)VRING ? nblk : (uint32_t)VRING;
     for (uint32_t bt = 0; bt < pre; ++bt) issue(bt);
+    if (qkv.parts) {
+      float x, x_unused;
+      part_sums(vpl, x, x_unused);
+      vnew = (uint16_t)f32_to_bf16_bits(x);
+      if (pos_ok) qkv.v_cache[(bh * L + pos) * D + colbase + lane] = vnew;
+      if (qkv.qkv_out) qkv.qkv_out[(uint64_t)row * 3 * HD + 2 * HD + (uint64_t)h * D + colbase + lane] = x;
+    }
     lds_barrier();  // (1) scores, last NaN and first key written
     const uint32_t jn = *nan_word;
     if (jn != 0u && jn < len) lds_barrier();  // (1a) key after the last NaN
@@ -254,97 +294,63 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* k,
     __builtin_amdgcn_s_barrier();  // (4) p written
     asm volatile("" ::: "memory");
 
-    // batch bt's data has landed once the loads of the batches issued after
-    // it (bt+1 .. min(bt+VRING-1, nblk-1), 8 each) are all that is left
-    auto wait_batch = [&](uint32_t bt) {
-      const uint32_t after = nblk - 1 - bt < (uint32_t)(VRING - 1) ? nblk - 1 - bt : (uint32_t)(VRING - 1);
+    // Wait until at most `after` batches (8 loads each) are still in flight.
+    auto wait_after = [&](uint32_t after) {
       switch (after) {
         case 0: FEW_WAIT_VMCNT(0); break;
         case 1: FEW_WAIT_VMCNT(8); break;
         case 2: FEW_WAIT_VMCNT(16); break;
         case 3: FEW_WAIT_VMCNT(24); break;
-        case 4: FEW_WAIT_VMCNT(32); break;
-        default: FEW_WAIT_VMCNT(40); break;
+        default: FEW_WAIT_VMCNT(32); break;
       }
       asm volatile("" ::: "memory");
     };
-    // half a batch (32 rows) into registers: four rows of this lane's
-    // column per transposing read (lane 4j + a of a 16-lane group addresses
-    // row 4u + j, columns 16g + 4a .. +3, and lane i receives column 16g + i
-    // of rows 4u .. 4u+3), and p as two vectors holding p of rows 0-15 and
-    // 16-31 of the half in every 16-lane row (lane l: row l % 16), from
-    // which each multiply takes its row's p by a DPP row broadcast -- one LDS
-    // read per 16 positions instead of a 16-byte broadcast read per 4.  The
-    // bases are opaque 32-bit LDS addresses so that the reads of each kind
-    // share one base register and differ only in their immediate offsets.
-    const uint32_t tr_off = (4u * (((uint32_t)lane & 15u) >> 2)) * 32u +
-                            2u * (16u * ((uint32_t)lane >> 4) + 4u * ((uint32_t)lane & 3u));
-    auto read_half = [&](uint32_t bt, int half, float p16[2], i16x4_t v4[8]) {
-      uint32_t vbase = ring_off + (bt % VRING) * VB_BYTES + half * 32 * 128 + tr_off;
-      uint32_t pbase = kOffState + (bt * VB_ROWS + half * 32 + ((uint32_t)lane & 15u)) * 4;
-      asm volatile("" : "+v"(vbase), "+v"(pbase));
-      const lds_u8* vp = (const lds_u8*)smem + vbase;
-      const lds_u8* pp = (const lds_u8*)smem + pbase;
-      p16[0] = *(const __attribute__((address_space(3))) float*)(pp);
-      p16[1] = *(const __attribute__((address_space(3))) float*)(pp + 64);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) v4[u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vp + 512 * u));
-    };
+    // Round b (after barrier (6) of b): the score waves make batch b + 1's
+    // products while this wave adds batch b's.  Before that barrier this
+    // wave has batch b + 1 in LDS (the batches issued after it, at most
+    // VRING - 2 of them, may still be in flight) with the new value row in
+    // place; after it, batch b's ring slot (its products are made) takes
+    // batch b + VRING.  Lane = column colbase + lane: 16 reads of four
+    // ascending products each, t ascending.
+    const uint32_t pcol = kOffP + vw * (PSLOT_BYTES / 2) + (uint32_t)lane * 256u;
+    const uint32_t pswz = (uint32_t)lane & 15u;
     float acc = __uint_as_float(0u);
-    // once a batch's reads are done its slot takes batch bt + VRING; the
-    // empty asm on acc keeps the fold issued before it in front of the wait
-    auto refill = [&](uint32_t bt) {
-      asm volatile("" ::"v"(acc));
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-      asm volatile("" ::: "memory");
-      if (bt + VRING < nblk) issue(bt + VRING);
-    };
-    // products first (independent of acc), then the t-ascending chain; row
-    // 4u + e's p comes from lane (4u + e) % 16 of its 16-lane row
-    auto fold_regs = [&](const float p16[2], const i16x4_t v4[8]) {
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        float prod[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float pv = row_bcast(p16[u >> 2], (4 * u + e) & 15);
-          prod[e] = pv * bf16_to_f32((uint16_t)v4[u][e]);
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc = acc + prod[e];
-      }
-    };
-    // full batches: each half is read while the one before it folds
-    const uint32_t nfull = len / VB_ROWS;
-    float pa[2], pb[2];
-    i16x4_t va[8], vb8[8];
-    if (nfull > 0) {
-      wait_batch(0);
+    if (nblk > 0) {
+      wait_after(nblk - 1 < (uint32_t)(VRING - 1) ? nblk - 1 : (uint32_t)(VRING - 1));
       put_new_val(0);
-      read_half(0, 0, pa, va);
     }
-    uint32_t bt = 0;
-    for (; bt < nfull; ++bt) {
-      read_half(bt, 1, pb, vb8);
-      fold_regs(pa, va);
-      refill(bt);
-      if (bt + 1 < nfull) {
-        wait_batch(bt + 1);
-        put_new_val(bt + 1);
-        read_half(bt + 1, 0, pa, va);
+    lds_barrier();  // (5) batch 0 in LDS
+    for (uint32_t b = 0; b < nblk; ++b) {
+      if (b + 1 < nblk) {
+        wait_after(nblk - 2 - b < (uint32_t)(VRING - 2) ? nblk - 2 - b : (uint32_t)(VRING - 2));
+        put_new_val(b + 1);
       }
-      fold_regs(pb, vb8);
-    }
-    if (bt < nblk) {
-      // the last, partial batch
-      wait_batch(bt);
-      put_new_val(bt);
-      const uint16_t* st16 = reinterpret_cast<const uint16_t*>(smem + ring_off + (bt % VRING) * VB_BYTES);
-      const uint32_t t0 = bt * VB_ROWS;
-      for (uint32_t rr = 0; rr < len - t0; ++rr) {
-        const float prod = sp[t0 + rr] * bf16_to_f32(st16[rr * 64 + lane]);
-        acc = acc + prod;
-      }
+      lds_barrier();  // (6) batch b's products written, batch b + 1 in LDS
+      if (b + VRING < nblk) issue(b + VRING);
+      uint32_t pbase = pcol + (b & 1u) * PSLOT_BYTES;
+      asm volatile("" : "+v"(pbase));
+      const lds_u8* pp = (const lds_u8*)smem + pbase;
+      // four groups of four reads, each group added once it has landed
+      // (at most 12 reads in flight: the LDS counter holds 15)
+      f32x4_t pr[16];
+      auto add4 = [&](int k0) {
+#pragma unroll
+        for (int k = k0; k < k0 + 4; ++k)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc = acc + pr[k][e];
+      };
+#pragma unroll
+      for (uint32_t k = 0; k < 12; ++k) pr[k] = *(const lds_f32x4*)(pp + 16u * (k ^ pswz));
+      FEW_WAIT_LGKM(8);
+      add4(0);
+#pragma unroll
+      for (uint32_t k = 12; k < 16; ++k) pr[k] = *(const lds_f32x4*)(pp + 16u * (k ^ pswz));
+      FEW_WAIT_LGKM(8);
+      add4(4);
+      FEW_WAIT_LGKM(4);
+      add4(8);
+      FEW_WAIT_LGKM(0);
+      add4(12);
     }
     if (OUT_BF16)
       static_cast<uint16_t*>(o)[(uint64_t)qi * D + colbase + lane] = (uint16_t)f32_to_bf16_bits(acc);
@@ -355,16 +361,43 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* k,
 
   // ------------------------------------------------------------ K waves
   // this wave's q, requested ahead of its K rows so it lands first (lane l:
-  // elements 2l, 2l+1; partials mode: l and l + 64, rotated here)
+  // elements 2l, 2l+1; partials mode: l and l + 64, the q / k parts' loads
+  // first, then the K rows, then q / k added and rotated once the parts
+  // are in -- the K requests do not wait for the parts)
   uint16_t q_lo = 0, q_hi = 0;
+  uint32_t q_pair = 0;  // elements 2l, 2l+1 (unpacked after the K requests)
   uint16_t* kbuf = reinterpret_cast<uint16_t*>(smem + kOffKNew);  // the new key row, bf16
   const uint32_t blk_new = pos / 64u;  // the block holding the new row
+  RopeLoads lq, lk;
   if (qkv.parts) {
-    float x1, x2, y1, y2, kx1, kx2, ky1, ky2;
-    rope_pair(0, x1, x2, y1, y2);
+    rope_loads(0, lq);
     // every score wave requests the new key's pair too (its loads go out
     // with q's); the wave whose blocks hold it uses it
-    rope_pair(1, kx1, kx2, ky1, ky2);
+    rope_loads(1, lk);
+  } else {
+    q_pair = *reinterpret_cast<const uint32_t*>(q + (uint64_t)qi * D + 2 * lane);
+  }
+  const int lrow = lane >> 2, lchunk = lane & 3;
+  auto gload = [&](uint32_t blk, u32x4_t r[16]) {
+#pragma unroll
+    for (int seg = 0; seg < 4; ++seg)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t t = blk * 64 + lrow + 16 * i;
+        if (t >= len) t = 0;  // in bounds; such a score is never read
+        r[4 * seg + i] = *reinterpret_cast<const u32x4_t*>(kb + (uint64_t)t * D + seg * 32 + lchunk * 8);
+      }
+  };
+  // (loads are unconditional: rows past len read row 0, so no copies of
+  // the register blocks are needed to merge loaded and not-loaded paths)
+  u32x4_t ra[16], rb[16];
+  const uint32_t b0 = (uint32_t)wave;
+  gload(b0, ra);
+  gload(b0 + KWAVES, rb);
+  if (qkv.parts) {
+    float x1, x2, y1, y2, kx1, kx2, ky1, ky2;
+    rope_pair(lq, x1, x2, y1, y2);
+    rope_pair(lk, kx1, kx2, ky1, ky2);
     q_lo = (uint16_t)f32_to_bf16_bits(y1);
     q_hi = (uint16_t)f32_to_bf16_bits(y2);
     if (wave == 0) {
@@ -393,23 +426,9 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* k,
         dx[lane + 64] = kx2;
       }
     }
-  } else {
-    q_lo = q[(uint64_t)qi * D + 2 * lane];
-    q_hi = q[(uint64_t)qi * D + 2 * lane + 1];
   }
-  const int lrow = lane >> 2, lchunk = lane & 3;
   unsigned char* st = smem + kOffK + wave * KSTAGE_WAVE;
   float* qf = reinterpret_cast<float*>(smem + wave * 512);
-  auto gload = [&](uint32_t blk, u32x4_t r[16]) {
-#pragma unroll
-    for (int seg = 0; seg < 4; ++seg)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uint32_t t = blk * 64 + lrow + 16 * i;
-        if (t >= len) t = 0;  // in bounds; such a score is never read
-        r[4 * seg + i] = *reinterpret_cast<const u32x4_t*>(kb + (uint64_t)t * D + seg * 32 + lchunk * 8);
-      }
-  };
   // one block: its 64 scores into sp, its max-fold state into the block
   // state arrays
   auto fold = [&](uint32_t blk, const u32x4_t r[16]) {
@@ -464,12 +483,6 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* k,
                                __HIP_MEMORY_SCOPE_WORKGROUP);
     }
   };
-  // (loads are unconditional: rows past len read row 0, so no copies of
-  // the register blocks are needed to merge loaded and not-loaded paths)
-  u32x4_t ra[16], rb[16];
-  const uint32_t b0 = (uint32_t)wave;
-  gload(b0, ra);
-  gload(b0 + KWAVES, rb);
   if (wave == 0 && lane == 0) {
     *nan_word = 0u;
     key_word[0] = 0u;
@@ -480,8 +493,8 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* k,
     qf[lane] = bf16_to_f32(q_lo);
     qf[lane + 64] = bf16_to_f32(q_hi);
   } else {
-    qf[2 * lane] = bf16_to_f32(q_lo);
-    qf[2 * lane + 1] = bf16_to_f32(q_hi);
+    qf[2 * lane] = bf16lo(q_pair);
+    qf[2 * lane + 1] = bf16hi(q_pair);
   }
   wave_sync();
   // partials mode: the rows of block blk_new in registers r, row pos % 64
@@ -535,6 +548,66 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* k,
   const float den = *den_slot;
   for (uint32_t t = (uint32_t)(wave * 64 + lane); t < len; t += stride) sp[t] = sp[t] / den;
   lds_barrier();  // (4) p written
+
+  // Products p_t * v_{t,c} (one rounded multiply each) of batch b into
+  // product slot b % 2, in the order the V waves add them: column c of
+  // half h at kOffP + (b % 2) PSLOT_BYTES + h PSLOT_BYTES / 2 + 256 c, its
+  // 16-byte chunk t / 4 at chunk index (t / 4) ^ (c % 16).  A batch is 16
+  // units of 8 rows x 64 columns (unit u: half u / 8, rows 8 (u % 8) ..),
+  // wave w making units w, w + 6, w + 12.  Per unit: two transposing reads
+  // (lane 16g + i receives column 16g + i of rows 4j .. 4j + 3), p of the 8
+  // rows by a DPP row broadcast, one 16-byte write per four rows.  In the
+  // last, partial batch rows past len (they hold row 0 and sp holds no p for
+  // them) get +0, which the V waves' sums absorb unchanged (they start at +0
+  // and an add never turns them into -0).
+  const uint32_t tr_off = (4u * (((uint32_t)lane & 15u) >> 2)) * 32u +
+                          2u * (16u * ((uint32_t)lane >> 4) + 4u * ((uint32_t)lane & 3u));
+  const uint32_t nunits = wave < 4 ? 3u : 2u;
+  auto produce = [&](uint32_t b) {
+    i16x4_t v4[3][2];
+    float p8[3];
+#pragma unroll
+    for (uint32_t rep = 0; rep < 3; ++rep) {
+      if (rep < nunits) {
+        const uint32_t unit = (uint32_t)wave + 6u * rep, half = unit >> 3, o8 = unit & 7u;
+        uint32_t vbase = kOffV + half * (VRING * VB_BYTES) + (b % VRING) * VB_BYTES + o8 * 8u * 128u + tr_off;
+        uint32_t pbase = kOffState + (b * 64u + o8 * 8u + ((uint32_t)lane & 7u)) * 4u;
+        asm volatile("" : "+v"(vbase), "+v"(pbase));
+        p8[rep] = *(const __attribute__((address_space(3))) float*)((const lds_u8*)smem + pbase);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          v4[rep][j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)((const lds_u8*)smem + vbase + 512 * j));
+      }
+    }
+    const bool partial = (b + 1u) * 64u > len;
+#pragma unroll
+    for (uint32_t rep = 0; rep < 3; ++rep) {
+      if (rep < nunits) {
+        const uint32_t unit = (uint32_t)wave + 6u * rep, half = unit >> 3, o8 = unit & 7u;
+        const uint32_t t0 = b * 64u + o8 * 8u;
+        uint32_t wbase = kOffP + (b & 1u) * PSLOT_BYTES + half * (PSLOT_BYTES / 2) + (uint32_t)lane * 256u;
+        asm volatile("" : "+v"(wbase));
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          f32x4_t pr;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) pr[e] = row_bcast(p8[rep], 4 * j + e) * bf16_to_f32((uint16_t)v4[rep][j][e]);
+          if (partial) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (t0 + (uint32_t)(4 * j + e) >= len) pr[e] = __uint_as_float(0u);
+          }
+          *(lds_f32x4*)((lds_u8*)smem + wbase + 16u * ((2u * o8 + (uint32_t)j) ^ ((uint32_t)lane & 15u))) = pr;
+        }
+      }
+    }
+  };
+  lds_barrier();  // (5) batch 0 in LDS
+  if (nblk > 0) produce(0);
+  for (uint32_t b = 0; b < nblk; ++b) {
+    lds_barrier();  // (6) batch b's products written, batch b + 1 in LDS
+    if (b + 1 < nblk) produce(b + 1);
+  }
 }
 
 }  // namespace

@@ -165,6 +165,31 @@ def test_few_pairs_form_equals_many_pairs_form(L, lens):
     _bitwise(small, want)
 
 
+def test_few_pairs_form_ignores_rows_past_len():
+    """K and V rows past each sequence's length hold NaN and infinities
+    (inside the last, partial 64-row batch and beyond it); the eight-wave
+    kernel folds the partial batch with those rows' products replaced by +0
+    and gives the oracle's bits, which never read them."""
+    B, H, L = 4, 8, 640
+    lens = [600, 37, 64, 1]
+    rng = np.random.default_rng(23)
+    q16 = oracle.f32_to_bf16_bits_np(rng.normal(0, 1, (B, H, D)).astype(np.float32))
+    k32 = rng.normal(0, 1, (B, H, L, D)).astype(np.float32)
+    v32 = rng.normal(0, 1, (B, H, L, D)).astype(np.float32)
+    for b, n in enumerate(lens):
+        k32[b, :, n:, ::2] = np.nan
+        k32[b, :, n:, 1::2] = np.inf
+        v32[b, :, n:, ::3] = np.nan
+        v32[b, :, n:, 1::3] = -np.inf
+    k16, v16 = oracle.f32_to_bf16_bits_np(k32), oracle.f32_to_bf16_bits_np(v32)
+    qb, kb, vb = ca.Buffer.from_array(q16), ca.Buffer.from_array(k16), ca.Buffer.from_array(v16)
+    say("attention eight-wave form, NaN / inf rows past len")
+    got = _run(qb, kb, vb, lens, B, H, L, 0.088388)
+    want = oracle.attn_decode(q16, k16, v16, np.array(lens, np.uint32), 0.088388)
+    assert not np.isnan(want).any()
+    _bitwise(got, want)
+
+
 def test_few_pairs_form_nan_at_block_boundaries():
     """NaN and infinite scores at 64-row block boundaries (63 / 64, and 383 /
     384 where the six score waves' rotation wraps), several NaNs in one head
