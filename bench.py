@@ -568,6 +568,21 @@ def bench_ceilings(ev: HipEvents) -> dict:
         clk = c[:, 0] / (c[:, 1] / 100e6) / 1e9
         out[key] = {"TFLOP/s": round(flop / us / 1e6, 1), "frac_of_peak": round(flop / us / 1e6 / PEAK_BF16_TFLOPS, 4),
                     "clock_GHz_median": round(float(np.median(clk)), 3), "us_per_launch": round(us, 2)}
+    # the same LDS-fed loop with one wave per SIMD and 128 x 128 wave tiles
+    # (64 MFMAs : 24 LDS reads per step, accumulators in AGPRs)
+    grid4, block4, iters4 = 256, 256, 400
+    obuf4, cyc4 = ca.Buffer(grid4 * block4 * 4), ca.Buffer(grid4 * (block4 // 64) * 16)
+    flop4 = grid4 * (block4 // 64) * iters4 * 64 * 16 * 16 * 32 * 2
+    go = launcher(kernel("catena_calib_mfma_lds_4w_bf16"), grid4, block4,
+                  [vp(obuf4.ptr), vp(cyc4.ptr), ctypes.c_int(iters4), ctypes.c_uint32(0x9E3779B9)])
+    us = time_us(go, 300, 100)
+    c = cyc4.read(np.uint64).astype(np.float64).reshape(-1, 2)
+    clk = c[:, 0] / (c[:, 1] / 100e6) / 1e9
+    out["mfma_bf16_lds_fed_4w_128x128"] = {
+        "TFLOP/s": round(flop4 / us / 1e6, 1), "frac_of_peak": round(flop4 / us / 1e6 / PEAK_BF16_TFLOPS, 4),
+        "clock_GHz_median": round(float(np.median(clk)), 3),
+        "cycles_per_mfma_per_wave": round(float(np.median(c[:, 0])) / (iters4 * 64), 2), "us_per_launch": round(us, 2)}
+    del obuf4, cyc4
     nbytes = 2 << 30
     src, flag = ca.Buffer(nbytes), ca.Buffer(64)
     ca.fill_uniform_f32(src, nbytes // 4, 11, 0)

@@ -8,6 +8,11 @@
 //   catena_calib_mfma_lds_bf16  the same MFMAs fed from LDS at the bf16 GEMM's
 //                               ratio (per 32 MFMAs 8 ds_read_b128 + 8
 //                               ds_read_b64, two fragment sets alternating).
+//   catena_calib_mfma_lds_4w_bf16  the same LDS-fed loop shaped for one
+//                               wave per SIMD with a 128 x 128 wave tile: 64
+//                               MFMAs per step against 8 ds_read_b128 + 16
+//                               ds_read_b64 (a third fewer LDS bytes per
+//                               MFMA), the 256 accumulator registers in AGPRs.
 //   catena_calib_read           plain HBM read, one contiguous chunk per
 //                               workgroup, four 16-byte loads in flight.
 //   catena_calib_read_nt        the same with non-temporal loads.
@@ -166,6 +171,78 @@ extern "C" __global__ __launch_bounds__(512) void catena_calib_mfma_lds_bf16(flo
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < 32; ++i) s += acc[i][0] + acc[i][3];
+  out[tid] = s;
+  write_cycles(cyc, c0, r0, c1, r1);
+}
+
+namespace {
+struct LdsFrags8 {
+  bf16x8_t a[8];
+  bf16x8_t b[8];
+};
+
+// 64 MFMAs of `cur` (8 x 8 blocks) with the 24 reads of `nx` (from p)
+// interleaved one per MFMA.
+__device__ inline void lds_step64(f32x4_t (&acc)[64], LdsFrags8& nx, const LdsFrags8& cur, const char* p) {
+  u32x2_t lo[8], hi[8];
+#pragma unroll
+  for (int g = 0; g < 64; ++g) {
+    if (g < 8) {
+      nx.a[g] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(p + g * 1024));
+    } else if (g < 24) {
+      const int j = (g - 8) >> 1;
+      if ((g & 1) == 0)
+        lo[j] = *reinterpret_cast<const u32x2_t*>(p + 8192 + j * 1024);
+      else
+        hi[j] = *reinterpret_cast<const u32x2_t*>(p + 8192 + j * 1024 + 512);
+    }
+    acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.b[g >> 3], cur.a[g & 7], acc[g], 0, 0, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const u32x4_t v = {lo[j][0], lo[j][1], hi[j][0], hi[j][1]};
+    nx.b[j] = __builtin_bit_cast(bf16x8_t, v);
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+}
+}  // namespace
+
+// grid any, block 256 (one wave per SIMD), 64 KiB static LDS; out[grid * 256],
+// cyc[2 * grid * 4]; iters even, 64 MFMAs per iteration per wave.
+extern "C" __global__ __launch_bounds__(256, 1) void catena_calib_mfma_lds_4w_bf16(float* out, uint64_t* cyc,
+                                                                                   int iters, uint32_t seed) {
+  __shared__ __attribute__((aligned(16))) uint32_t lds[16384];
+  const uint32_t tid = blockIdx.x * blockDim.x + threadIdx.x;
+  for (uint32_t i = threadIdx.x; i < 16384; i += blockDim.x) {
+    const uint32_t h = mix32((tid * 131 + i) ^ seed), g = mix32(h);
+    lds[i] = rand_bf16(h) | (rand_bf16(g) << 16);
+  }
+  f32x4_t acc[64];
+#pragma unroll
+  for (int i = 0; i < 64; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  __syncthreads();
+  // Byte offsets read: 16 * lane (<= 1008) plus at most 32768 + 8192 + 7 * 1024
+  // + 512 + 8 bytes: 49,656 < 65,536.
+  const char* base = reinterpret_cast<const char*>(lds) + 16 * (threadIdx.x & 63);
+  LdsFrags8 f0, f1;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) f0.a[p] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(base + p * 1024));
+#pragma unroll
+  for (int p = 0; p < 8; ++p)
+    f0.b[p] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(base + 8192 + p * 1024));
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  uint64_t c0, r0, c1, r1;
+  stamp(c0, r0);
+  for (int it = 0; it < iters; it += 2) {
+    lds_step64(acc, f1, f0, base + 16384);
+    lds_step64(acc, f0, f1, base + 32768);
+  }
+  stamp(c1, r1);
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) s += acc[i][0] + acc[i][3];
   out[tid] = s;
   write_cycles(cyc, c0, r0, c1, r1);
 }
