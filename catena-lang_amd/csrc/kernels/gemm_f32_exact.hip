@@ -142,6 +142,31 @@ CATENA_DEV void load_slab(Slab& sl, const float* __restrict__ A, const float* __
 CATENA_DEV float live_or_zero(float v, uint32_t live, int bit) {
   return (live >> bit) & 1u ? v : 0.0f;
 }
+
+// 16 k values of the cell's row of A and column of B (k-contiguous in LDS)
+CATENA_DEV void read16(float4 (&a)[4], float4 (&b)[4], const float* ar, const float* br) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    a[u] = *reinterpret_cast<const float4*>(ar + 4 * u);
+    b[u] = *reinterpret_cast<const float4*>(br + 4 * u);
+  }
+}
+
+// acc = acc + fl(a_k * b_k) for the 16 k values in ascending order
+CATENA_DEV float fold16(float acc, const float4 (&a)[4], const float4 (&b)[4]) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    float prod = a[u].x * b[u].x;
+    acc = acc + prod;
+    prod = a[u].y * b[u].y;
+    acc = acc + prod;
+    prod = a[u].z * b[u].z;
+    acc = acc + prod;
+    prod = a[u].w * b[u].w;
+    acc = acc + prod;
+  }
+  return acc;
+}
 }  // namespace
 
 extern "C" __global__ __launch_bounds__(256) void catena_gemm_f32_exact_t16(
@@ -176,9 +201,38 @@ extern "C" __global__ __launch_bounds__(256) void catena_gemm_f32_exact_t16(
     }
     __syncthreads();
     if (k0 + S_K < k) load_slab(sl, A, B, n, m, k, row0, col0, k0 + S_K, tid);
-    // only the kt live k values enter the chain, in ascending order
+    // only the kt live k values enter the chain, in ascending order; the
+    // LDS reads of the next 16 k are issued before the current 16 are
+    // folded, so their latency sits under the chain instead of in front of it
     int kk = 0;
-#pragma unroll 4
+    // (two register sets in turn: set 0 holds k kk .. kk + 15 at the top of
+    // each pass)
+    if (kt >= 16) {
+      float4 a0[4], b0[4], a1[4], b1[4];
+      read16(a0, b0, &As[ty][0], &Bs[tx][0]);
+      // (the scheduling barriers keep each set's reads in front of the other
+      // set's fold; left alone the compiler moves them down to their use)
+      for (; kk + 48 <= kt; kk += 32) {
+        read16(a1, b1, &As[ty][kk + 16], &Bs[tx][kk + 16]);
+        __builtin_amdgcn_sched_barrier(0);
+        acc = fold16(acc, a0, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        read16(a0, b0, &As[ty][kk + 32], &Bs[tx][kk + 32]);
+        __builtin_amdgcn_sched_barrier(0);
+        acc = fold16(acc, a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (kk + 32 <= kt) {
+        read16(a1, b1, &As[ty][kk + 16], &Bs[tx][kk + 16]);
+        __builtin_amdgcn_sched_barrier(0);
+        acc = fold16(acc, a0, b0);
+        acc = fold16(acc, a1, b1);
+        kk += 32;
+      } else {
+        acc = fold16(acc, a0, b0);
+        kk += 16;
+      }
+    }
     for (; kk + 4 <= kt; kk += 4) {
       const float4 a = *reinterpret_cast<const float4*>(&As[ty][kk]);
       const float4 b = *reinterpret_cast<const float4*>(&Bs[tx][kk]);
@@ -199,4 +253,140 @@ extern "C" __global__ __launch_bounds__(256) void catena_gemm_f32_exact_t16(
   }
   const uint64_t gi = row0 + ty, gj = col0 + tx;
   if (gi < n && gj < m) C[gi * m + gj] = acc;
+}
+
+// The same contraction for small outputs with k % 64 == 0 and 16-byte
+// aligned rows of B (m % 4 == 0): a workgroup of 4 waves owns 4 rows x 64
+// columns of C, wave w row 4 blockIdx.y + w, lane l column 64 blockIdx.x + l,
+// so 256^3 launches 256 workgroups with one cell per lane.  A wave's A value
+// for a k is the same in every lane: for each 16 k of a slab, lane l holds
+// A[row][k0 + (l % 16)] in a register and the multiply takes k's value
+// through a DPP row broadcast (row_newbcast), so it costs no instruction of
+// its own (a broadcast LDS read costs the shared LDS more than the
+// multiply-add it feeds; v_readlane costs an instruction per k).  B goes through LDS: the k range runs in chunks of 4 slabs of
+// 64 k, every load of a chunk issued at once into registers, each slab
+// written to LDS ([64 k][64 cols] f32) as it lands, and after one barrier
+// the chunk is folded 16 k at a time, the next 16 k's B reads issued before
+// the current 16 are folded.  Loads outside the matrices return 0 or read
+// the next row of B; such values are never folded into a stored cell.  Each
+// cell's chain is the one above: acc = +0, then for kk ascending
+// acc = acc + fl(A[i,kk] * B[kk,j]).
+namespace {
+constexpr int R_ROWS = 4, R_COLS = 64, R_KS = 64, R_SLABS = 4;
+constexpr int R_SLOT = R_KS * R_COLS * 4;
+
+// k 16 g .. 16 g + 15 of a slab: this lane's B column (row stride 64
+// floats); bs points at k 16 g of the slab
+CATENA_DEV void r4_read16(float (&b)[16], const float* bs) {
+#pragma unroll
+  for (int q = 0; q < 16; ++q) b[q] = bs[q * R_COLS];
+}
+
+// Lane Q of each 16-lane row, broadcast to its row (DPP row_newbcast)
+template <int Q>
+CATENA_DEV float r4_bcast(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x150 + Q, 0xF, 0xF, false));
+}
+
+// acc = acc + fl(A_k * b_k) for 16 k in ascending order, A_k in lane k % 16
+// of every row of ra: the 16 products first, then the 16 dependent adds
+// (with one wave per SIMD nothing else fills the wait when each add follows
+// its own multiply)
+CATENA_DEV float r4_fold16(float acc, float ra, const float (&b)[16]) {
+  float prod[16];
+  prod[0] = r4_bcast<0>(ra) * b[0];
+  prod[1] = r4_bcast<1>(ra) * b[1];
+  prod[2] = r4_bcast<2>(ra) * b[2];
+  prod[3] = r4_bcast<3>(ra) * b[3];
+  prod[4] = r4_bcast<4>(ra) * b[4];
+  prod[5] = r4_bcast<5>(ra) * b[5];
+  prod[6] = r4_bcast<6>(ra) * b[6];
+  prod[7] = r4_bcast<7>(ra) * b[7];
+  prod[8] = r4_bcast<8>(ra) * b[8];
+  prod[9] = r4_bcast<9>(ra) * b[9];
+  prod[10] = r4_bcast<10>(ra) * b[10];
+  prod[11] = r4_bcast<11>(ra) * b[11];
+  prod[12] = r4_bcast<12>(ra) * b[12];
+  prod[13] = r4_bcast<13>(ra) * b[13];
+  prod[14] = r4_bcast<14>(ra) * b[14];
+  prod[15] = r4_bcast<15>(ra) * b[15];
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int q = 0; q < 16; ++q) acc = acc + prod[q];
+  return acc;
+}
+
+// the four 16-k groups of one slab (ra[g]: A of group g), each group's B
+// reads issued before the previous group is folded
+CATENA_DEV float r4_fold_slab(float acc, const float (&ra)[4], const float* bs) {
+  float b0[16], b1[16];
+  r4_read16(b0, bs);
+  r4_read16(b1, bs + 16 * R_COLS);
+  __builtin_amdgcn_sched_barrier(0);
+  acc = r4_fold16(acc, ra[0], b0);
+  __builtin_amdgcn_sched_barrier(0);
+  r4_read16(b0, bs + 32 * R_COLS);
+  __builtin_amdgcn_sched_barrier(0);
+  acc = r4_fold16(acc, ra[1], b1);
+  __builtin_amdgcn_sched_barrier(0);
+  r4_read16(b1, bs + 48 * R_COLS);
+  __builtin_amdgcn_sched_barrier(0);
+  acc = r4_fold16(acc, ra[2], b0);
+  __builtin_amdgcn_sched_barrier(0);
+  return r4_fold16(acc, ra[3], b1);
+}
+}  // namespace
+
+// LDS: R_SLABS * R_SLOT bytes (dynamic).
+extern "C" __global__ __launch_bounds__(256) void catena_gemm_f32_exact_r4(
+    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
+    uint64_t n, uint64_t m, uint64_t k) {
+  extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const uint64_t row0 = (uint64_t)blockIdx.y * R_ROWS, col0 = (uint64_t)blockIdx.x * R_COLS;
+  const uint64_t arow = row0 + wave;
+  // buffer loads with 32-bit byte offsets (the host keeps (n + 4) k 4 and
+  // (k + 256) m 4 below 2^31): a read past either matrix returns 0
+  const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, (int)(n * k * 4), 0x00020000);
+  const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc((void*)B, (short)0, (int)(k * m * 4), 0x00020000);
+  const uint32_t m4 = (uint32_t)m * 4u;
+  float acc = __uint_as_float(0u);
+  for (uint64_t c0 = 0; c0 < k; c0 += R_SLABS * R_KS) {
+    const uint64_t left = (k - c0) / R_KS;
+    const int ns = left < (uint64_t)R_SLABS ? (int)left : R_SLABS;
+    // thread t's share of slab s: B copy u covers row 16 u + t / 16 of the
+    // slab, columns 4 (t % 16) .. + 3; A group g: row arow, k 16 g + l % 16
+    // of the slab
+    const uint32_t bvo = (uint32_t)(((c0 + tid / 16) * m + col0 + 4 * (tid % 16)) * 4);
+    const uint32_t avo = (uint32_t)((arow * k + c0 + (lane & 15)) * 4);
+    float4 rb[R_SLABS][4];
+    float ra[R_SLABS][4];
+#pragma unroll
+    for (int s = 0; s < R_SLABS; ++s) {
+      if (s < ns) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          rb[s][u] = __builtin_bit_cast(
+              float4, __builtin_amdgcn_raw_buffer_load_b128(brs, (int)bvo, (int)((uint32_t)(R_KS * s + 16 * u) * m4), 0));
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          ra[s][g] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ars, (int)(avo + 4u * (R_KS * s + 16 * g)), 0, 0));
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < R_SLABS; ++s) {
+      if (s < ns) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          *reinterpret_cast<float4*>(smem + s * R_SLOT + (256 * u + tid) * 16) = rb[s][u];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < R_SLABS; ++s)
+      if (s < ns) acc = r4_fold_slab(acc, ra[s], reinterpret_cast<const float*>(smem + s * R_SLOT) + lane);
+    __syncthreads();
+  }
+  const uint64_t gj = col0 + lane;
+  if (arow < n && gj < m) C[arow * m + gj] = acc;
 }
