@@ -169,7 +169,20 @@ def bench_c1(steps: int, ev):
         call(10 + i)
         t.append((time.perf_counter() - t0) * 1e6)
     c = ca.Buffer(n * m * 4)
-    k_ms = timed(lambda i: ca.gemm_f32_exact(a, b, c, n, m, k), steps, 10, ev)
+    # the kernel alone: launches through the bare C entry point with its
+    # arguments bound once, so that the host's per-call cost (~4-5 us through
+    # the checked Python wrapper) stays below the kernel's own duration; the
+    # status of the last call is checked after the timed run
+    f = L.catena_mi355x_gemm_f32_exact
+    fargs = (ctypes.c_void_p(a.ptr), ctypes.c_void_p(b.ptr), ctypes.c_void_p(c.ptr),
+             ctypes.c_uint64(n), ctypes.c_uint64(m), ctypes.c_uint64(k))
+    st = [0]
+
+    def launch_exact(i):
+        st[0] = f(*fargs)
+
+    k_ms = timed(launch_exact, steps, 10, ev)
+    ca.check(st[0])
     flop = 2.0 * n * m * k
     return {"workload": "C1: f32 GEMM 256^3 as the program matmul-2x2-via-mem (program ABI, "
                         "by-value Mem), U[-1,1] from seeds 1 / 2",

@@ -53,7 +53,7 @@ struct KernelSpec {
 const KernelSpec kKernels[] = {
     {KernelId::GemmF32Exact, "gemm_f32_exact", "catena_gemm_f32_exact"},
     {KernelId::GemmF32ExactT16, "gemm_f32_exact", "catena_gemm_f32_exact_t16"},
-    {KernelId::GemmF32ExactR4, "gemm_f32_exact", "catena_gemm_f32_exact_r4"},
+    {KernelId::GemmF32ExactQ16, "gemm_f32_exact", "catena_gemm_f32_exact_q16"},
     {KernelId::GemmBf16EdgeBf16, "gemm_bf16", "catena_gemm_bf16_edge_bf16out"},
     {KernelId::GemmBf16EdgeF32, "gemm_bf16", "catena_gemm_bf16_edge_f32out"},
     {KernelId::GemmBf16LdsBf16, "gemm_bf16_lds", "catena_gemm_bf16_lds_bf16out"},

@@ -15,7 +15,7 @@ namespace catena {
 enum class KernelId : int {
   GemmF32Exact = 0,
   GemmF32ExactT16,  // 16x16 tiles for small outputs (gemm_f32_exact.hip)
-  GemmF32ExactR4,   // 4x64 tiles for small outputs, k % 64 == 0, m % 4 == 0
+  GemmF32ExactQ16,  // 16x16 tiles, A by DPP row broadcast: k % 16 == 0, m % 4 == 0
   GemmBf16EdgeBf16,  // general shapes, bounds-checked (gemm_bf16.hip)
   GemmBf16EdgeF32,
   GemmBf16LdsBf16,  // aligned tiles with K % 128 != 0: two 64-k stages (gemm_bf16_lds.hip)

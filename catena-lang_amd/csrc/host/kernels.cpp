@@ -301,19 +301,16 @@ int catena_mi355x_gemm_f32_exact(const float* a, const float* b, float* c, uint6
   if (!c || (k > 0 && (!a || !b))) return fail(CATENA_ERR_INVALID_ARGUMENT, "null operand");
   void* args[] = {&a, &b, &c, &n, &m, &k};
   // 64x64 tiles (16 cells per thread) unless they would leave CUs idle; then
-  // 4x64 tiles (one cell per lane, B rows staged through LDS with 16-byte
-  // loads, A broadcast within the wave) when k % 64 == 0, B's rows are
-  // 16-byte aligned and the buffer offsets fit 31 bits, else 16x16 tiles (one
-  // cell per thread).  Every cell is the same k-ascending chain in all three,
-  // so the choice never changes the bits.
+  // 16x16 tiles with one cell per thread: A by DPP row broadcast and B through
+  // LDS when k % 16 == 0, B's rows are 16-byte aligned and the buffer offsets
+  // fit 31 bits, else A and B both through LDS.  Every cell is the same
+  // k-ascending chain in all three, so the choice never changes the bits.
   const uint64_t gx = ceil_div(m, 64), gy = ceil_div(n, 64);
   if (gx * gy < kDecodeSpread) {
-    const uint64_t ry = ceil_div(n, 4);
-    if (k > 0 && k % 64 == 0 && m % 4 == 0 && aligned16(b) && reinterpret_cast<uintptr_t>(a) % 4 == 0 &&
-        (n + 4) * k * 4 < (1ull << 31) && (k + 256) * m * 4 < (1ull << 31) && ry <= 65535)
-      return launch(KernelId::GemmF32ExactR4, dim3((unsigned)gx, (unsigned)ry), dim3(256), 4 * 64 * 64 * 4,
-                    args);
     const uint64_t sx = ceil_div(m, 16), sy = ceil_div(n, 16);
+    if (k > 0 && k % 16 == 0 && m % 4 == 0 && aligned16(b) && reinterpret_cast<uintptr_t>(a) % 4 == 0 &&
+        (n + 16) * k * 4 < (1ull << 31) && (k + 256) * m * 4 < (1ull << 31) && sy <= 65535)
+      return launch(KernelId::GemmF32ExactQ16, dim3((unsigned)sx, (unsigned)sy), dim3(256), 256 * 16 * 4, args);
     return launch(KernelId::GemmF32ExactT16, dim3((unsigned)sx, (unsigned)sy), dim3(256), 0, args);
   }
   if (gx > 0x7FFFFFFFu || gy > 65535u) return fail(CATENA_ERR_UNSUPPORTED, "matrix too large");

@@ -255,36 +255,28 @@ extern "C" __global__ __launch_bounds__(256) void catena_gemm_f32_exact_t16(
   if (gi < n && gj < m) C[gi * m + gj] = acc;
 }
 
-// The same contraction for small outputs with k % 64 == 0 and 16-byte
-// aligned rows of B (m % 4 == 0): a workgroup of 4 waves owns 4 rows x 64
-// columns of C, wave w row 4 blockIdx.y + w, lane l column 64 blockIdx.x + l,
-// so 256^3 launches 256 workgroups with one cell per lane.  A wave's A value
-// for a k is the same in every lane: for each 16 k of a slab, lane l holds
-// A[row][k0 + (l % 16)] in a register and the multiply takes k's value
-// through a DPP row broadcast (row_newbcast), so it costs no instruction of
-// its own (a broadcast LDS read costs the shared LDS more than the
-// multiply-add it feeds; v_readlane costs an instruction per k).  B goes through LDS: the k range runs in chunks of 4 slabs of
-// 64 k, every load of a chunk issued at once into registers, each slab
-// written to LDS ([64 k][64 cols] f32) as it lands, and after one barrier
-// the chunk is folded 16 k at a time, the next 16 k's B reads issued before
-// the current 16 are folded.  Loads outside the matrices return 0 or read
-// the next row of B; such values are never folded into a stored cell.  Each
-// cell's chain is the one above: acc = +0, then for kk ascending
-// acc = acc + fl(A[i,kk] * B[kk,j]).
+// The same contraction for small outputs with k % 16 == 0 and 16-byte
+// aligned rows of B (m % 4 == 0), again on 16 x 16 tiles with one cell per
+// thread (256^3: 256 workgroups), but with A kept out of LDS: wave w owns
+// rows 16 blockIdx.y + 4 w + r, r = lane / 16, and lane l column
+// 16 blockIdx.x + l % 16, so a row of A is uniform within each 16-lane DPP
+// row.  For a 16-k group lane 16 r + q holds A[row r][k0 + q] (one 4-byte
+// buffer load) and the multiply takes it through a DPP row broadcast
+// (v_mul_f32_dpp row_newbcast:q), no instruction of its own: a broadcast
+// LDS read costs the shared LDS more than the multiply-add it feeds.  The B
+// tile of a chunk of 256 k (16 columns, 16 KB) goes through LDS, requested
+// at once with one 16-byte buffer load per thread and 64 k, and is folded
+// after one barrier, each 16-k group's B reads issued before the previous
+// group is folded; each group's 16 products are formed before its 16
+// dependent adds (one wave per SIMD: nothing else fills the wait when an
+// add follows its own multiply).  Each cell's chain is the one above:
+// acc = +0, then for kk ascending acc = acc + fl(A[i,kk] * B[kk,j]).
 namespace {
-constexpr int R_ROWS = 4, R_COLS = 64, R_KS = 64, R_SLABS = 4;
-constexpr int R_SLOT = R_KS * R_COLS * 4;
-
-// k 16 g .. 16 g + 15 of a slab: this lane's B column (row stride 64
-// floats); bs points at k 16 g of the slab
-CATENA_DEV void r4_read16(float (&b)[16], const float* bs) {
-#pragma unroll
-  for (int q = 0; q < 16; ++q) b[q] = bs[q * R_COLS];
-}
+constexpr int Q_T = 16, Q_KC = 256;
 
 // Lane Q of each 16-lane row, broadcast to its row (DPP row_newbcast)
 template <int Q>
-CATENA_DEV float r4_bcast(float x) {
+CATENA_DEV float row_bcast16(float x) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x150 + Q, 0xF, 0xF, false));
 }
 
@@ -292,101 +284,94 @@ CATENA_DEV float r4_bcast(float x) {
 // of every row of ra: the 16 products first, then the 16 dependent adds
 // (with one wave per SIMD nothing else fills the wait when each add follows
 // its own multiply)
-CATENA_DEV float r4_fold16(float acc, float ra, const float (&b)[16]) {
+CATENA_DEV float fold16_row_bcast(float acc, float ra, const float (&b)[16]) {
   float prod[16];
-  prod[0] = r4_bcast<0>(ra) * b[0];
-  prod[1] = r4_bcast<1>(ra) * b[1];
-  prod[2] = r4_bcast<2>(ra) * b[2];
-  prod[3] = r4_bcast<3>(ra) * b[3];
-  prod[4] = r4_bcast<4>(ra) * b[4];
-  prod[5] = r4_bcast<5>(ra) * b[5];
-  prod[6] = r4_bcast<6>(ra) * b[6];
-  prod[7] = r4_bcast<7>(ra) * b[7];
-  prod[8] = r4_bcast<8>(ra) * b[8];
-  prod[9] = r4_bcast<9>(ra) * b[9];
-  prod[10] = r4_bcast<10>(ra) * b[10];
-  prod[11] = r4_bcast<11>(ra) * b[11];
-  prod[12] = r4_bcast<12>(ra) * b[12];
-  prod[13] = r4_bcast<13>(ra) * b[13];
-  prod[14] = r4_bcast<14>(ra) * b[14];
-  prod[15] = r4_bcast<15>(ra) * b[15];
+  prod[0] = row_bcast16<0>(ra) * b[0];
+  prod[1] = row_bcast16<1>(ra) * b[1];
+  prod[2] = row_bcast16<2>(ra) * b[2];
+  prod[3] = row_bcast16<3>(ra) * b[3];
+  prod[4] = row_bcast16<4>(ra) * b[4];
+  prod[5] = row_bcast16<5>(ra) * b[5];
+  prod[6] = row_bcast16<6>(ra) * b[6];
+  prod[7] = row_bcast16<7>(ra) * b[7];
+  prod[8] = row_bcast16<8>(ra) * b[8];
+  prod[9] = row_bcast16<9>(ra) * b[9];
+  prod[10] = row_bcast16<10>(ra) * b[10];
+  prod[11] = row_bcast16<11>(ra) * b[11];
+  prod[12] = row_bcast16<12>(ra) * b[12];
+  prod[13] = row_bcast16<13>(ra) * b[13];
+  prod[14] = row_bcast16<14>(ra) * b[14];
+  prod[15] = row_bcast16<15>(ra) * b[15];
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int q = 0; q < 16; ++q) acc = acc + prod[q];
   return acc;
 }
 
-// the four 16-k groups of one slab (ra[g]: A of group g), each group's B
-// reads issued before the previous group is folded
-CATENA_DEV float r4_fold_slab(float acc, const float (&ra)[4], const float* bs) {
-  float b0[16], b1[16];
-  r4_read16(b0, bs);
-  r4_read16(b1, bs + 16 * R_COLS);
-  __builtin_amdgcn_sched_barrier(0);
-  acc = r4_fold16(acc, ra[0], b0);
-  __builtin_amdgcn_sched_barrier(0);
-  r4_read16(b0, bs + 32 * R_COLS);
-  __builtin_amdgcn_sched_barrier(0);
-  acc = r4_fold16(acc, ra[1], b1);
-  __builtin_amdgcn_sched_barrier(0);
-  r4_read16(b1, bs + 48 * R_COLS);
-  __builtin_amdgcn_sched_barrier(0);
-  acc = r4_fold16(acc, ra[2], b0);
-  __builtin_amdgcn_sched_barrier(0);
-  return r4_fold16(acc, ra[3], b1);
+// k 16 g .. 16 g + 15 of this lane's B column (row stride 16 floats)
+CATENA_DEV void q16_read16(float (&b)[16], const float* bs) {
+#pragma unroll
+  for (int q = 0; q < 16; ++q) b[q] = bs[q * Q_T];
 }
 }  // namespace
 
-// LDS: R_SLABS * R_SLOT bytes (dynamic).
-extern "C" __global__ __launch_bounds__(256) void catena_gemm_f32_exact_r4(
+// LDS: Q_KC * Q_T * 4 bytes (dynamic).
+extern "C" __global__ __launch_bounds__(256) void catena_gemm_f32_exact_q16(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
     uint64_t n, uint64_t m, uint64_t k) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const uint64_t row0 = (uint64_t)blockIdx.y * R_ROWS, col0 = (uint64_t)blockIdx.x * R_COLS;
-  const uint64_t arow = row0 + wave;
-  // buffer loads with 32-bit byte offsets (the host keeps (n + 4) k 4 and
-  // (k + 256) m 4 below 2^31): a read past either matrix returns 0
+  const uint64_t row0 = (uint64_t)blockIdx.y * Q_T, col0 = (uint64_t)blockIdx.x * Q_T;
+  const uint64_t arow = row0 + 4 * wave + (lane >> 4);
+  const uint64_t ccol = col0 + (lane & 15);
+  // buffer loads with 32-bit byte offsets (the host keeps (n + 16) k 4 and
+  // (k + 256) m 4 below 2^31): a read past either matrix returns 0; a B
+  // read past column m reads the next row.  Neither value is folded into a
+  // stored cell.
   const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, (int)(n * k * 4), 0x00020000);
   const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc((void*)B, (short)0, (int)(k * m * 4), 0x00020000);
   const uint32_t m4 = (uint32_t)m * 4u;
+  const float* bs = reinterpret_cast<const float*>(smem) + (lane & 15);
   float acc = __uint_as_float(0u);
-  for (uint64_t c0 = 0; c0 < k; c0 += R_SLABS * R_KS) {
-    const uint64_t left = (k - c0) / R_KS;
-    const int ns = left < (uint64_t)R_SLABS ? (int)left : R_SLABS;
-    // thread t's share of slab s: B copy u covers row 16 u + t / 16 of the
-    // slab, columns 4 (t % 16) .. + 3; A group g: row arow, k 16 g + l % 16
-    // of the slab
-    const uint32_t bvo = (uint32_t)(((c0 + tid / 16) * m + col0 + 4 * (tid % 16)) * 4);
+  for (uint64_t c0 = 0; c0 < k; c0 += Q_KC) {
+    const int ng = (k - c0) < (uint64_t)Q_KC ? (int)((k - c0) / 16) : Q_KC / 16;
+    // B copy u of thread t: chunk row 64 u + t / 4, columns 4 (t % 4) .. + 3;
+    // A group g: row arow, k 16 g + l % 16 of the chunk
+    const uint32_t bvo = (uint32_t)(((c0 + tid / 4) * m + col0 + 4 * (tid % 4)) * 4);
     const uint32_t avo = (uint32_t)((arow * k + c0 + (lane & 15)) * 4);
-    float4 rb[R_SLABS][4];
-    float ra[R_SLABS][4];
+    float4 rb[4];
+    float ra[Q_KC / 16];
 #pragma unroll
-    for (int s = 0; s < R_SLABS; ++s) {
-      if (s < ns) {
+    for (int u = 0; u < 4; ++u)
+      if (64 * u < 16 * ng)
+        rb[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(brs, (int)bvo, (int)((uint32_t)(64 * u) * m4), 0));
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-          rb[s][u] = __builtin_bit_cast(
-              float4, __builtin_amdgcn_raw_buffer_load_b128(brs, (int)bvo, (int)((uint32_t)(R_KS * s + 16 * u) * m4), 0));
+    for (int g = 0; g < Q_KC / 16; ++g)
+      if (g < ng) ra[g] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ars, (int)(avo + 64u * g), 0, 0));
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
-          ra[s][g] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ars, (int)(avo + 4u * (R_KS * s + 16 * g)), 0, 0));
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < R_SLABS; ++s) {
-      if (s < ns) {
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-          *reinterpret_cast<float4*>(smem + s * R_SLOT + (256 * u + tid) * 16) = rb[s][u];
-      }
-    }
+    for (int u = 0; u < 4; ++u)
+      if (64 * u < 16 * ng) *reinterpret_cast<float4*>(smem + (256 * u + tid) * 16) = rb[u];
     __syncthreads();
+    // 16-k groups, two register sets in turn, each group's B reads issued
+    // before the previous group is folded
+    float b0[16], b1[16];
+    q16_read16(b0, bs);
 #pragma unroll
-    for (int s = 0; s < R_SLABS; ++s)
-      if (s < ns) acc = r4_fold_slab(acc, ra[s], reinterpret_cast<const float*>(smem + s * R_SLOT) + lane);
+    for (int g = 0; g < Q_KC / 16; g += 2) {
+      if (g < ng) {
+        if (g + 1 < ng) q16_read16(b1, bs + (16 * (g + 1)) * Q_T);
+        __builtin_amdgcn_sched_barrier(0);
+        acc = fold16_row_bcast(acc, ra[g], b0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (g + 1 < ng) {
+          if (g + 2 < ng) q16_read16(b0, bs + (16 * (g + 2)) * Q_T);
+          __builtin_amdgcn_sched_barrier(0);
+          acc = fold16_row_bcast(acc, ra[g + 1], b1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
     __syncthreads();
   }
-  const uint64_t gj = col0 + lane;
-  if (arow < n && gj < m) C[arow * m + gj] = acc;
+  if (arow < n && ccol < m) C[arow * m + ccol] = acc;
 }

@@ -136,11 +136,11 @@ def test_softmax_rows_in_place_and_specials():
 
 @pytest.mark.parametrize("n,m,k", [(256, 256, 256), (1, 1, 1), (65, 33, 17), (130, 70, 300),
                                    (64, 64, 0), (3, 200, 5), (257, 129, 64), (100, 77, 131),
-                                   # 4x64 tiles (k % 64 == 0, m % 4 == 0): ragged rows and
-                                   # column blocks, one to three chunks of 256 k, a last
-                                   # chunk of one to four slabs
+                                   # 16x16 tiles with A by DPP row broadcast (k % 16 == 0,
+                                   # m % 4 == 0): ragged rows and column blocks, one to
+                                   # three chunks of 256 k, a last chunk of 1 to 16 groups
                                    (255, 196, 320), (3, 4, 64), (130, 260, 512), (257, 300, 576),
-                                   (1, 64, 128), (61, 1000, 192),
+                                   (1, 64, 128), (61, 1000, 192), (33, 20, 48), (100, 36, 272),
                                    # 64x64 tiles (at least 256 of them)
                                    (1040, 1030, 37), (1024, 1024, 130)])
 def test_gemm_f32_exact_bitwise(n, m, k):
@@ -172,25 +172,25 @@ def test_gemm_f32_exact_tile_instances_agree():
     assert np.array_equal(full.read(np.uint32, (n, m))[256:512], part.read(np.uint32, (256, m)))
 
 
-def test_gemm_f32_exact_r4_instance_agrees_and_specials():
+def test_gemm_f32_exact_dpp_instance_agrees_and_specials():
     """Rows 256..511 of a 1024 x 1024 x 320 product (64x64 tiles) computed
-    alone as a 256 x 1024 product (4x64 tiles: k % 64 == 0, m % 4 == 0):
-    the same bits.  Then special values through the 4x64 and 16x16 tile
-    kernels against the oracle: signed zeros, infinities, NaNs and products
-    below the normal range."""
+    alone as a 256 x 1024 product (16x16 tiles with A by DPP row broadcast:
+    k % 16 == 0, m % 4 == 0): the same bits.  Then special values through
+    that instance and the all-LDS 16x16 one (m % 4 != 0) against the oracle:
+    signed zeros, infinities, NaNs and products below the normal range."""
     n, m, k = 1024, 1024, 320
     rng = np.random.default_rng(78)
     a = rng.uniform(-1, 1, (n, k)).astype(np.float32)
     b = rng.uniform(-1, 1, (k, m)).astype(np.float32)
     ab, bb = ca.Buffer.from_array(a), ca.Buffer.from_array(b)
     full, part = ca.Buffer(n * m * 4), ca.Buffer(256 * m * 4)
-    say("gemm f32 exact 1024x1024x320 (64x64 tiles) and rows 256..511 alone (4x64 tiles)")
+    say("gemm f32 exact 1024x1024x320 (64x64 tiles) and rows 256..511 alone (DPP 16x16 tiles)")
     ca.gemm_f32_exact(ab, bb, full, n, m, k)
     ca.gemm_f32_exact(ca.Buffer.from_array(np.ascontiguousarray(a[256:512])), bb, part, 256, m, k)
     assert np.array_equal(full.read(np.uint32, (n, m))[256:512], part.read(np.uint32, (256, m)))
     specials = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-20, -1e-20, 3e-39, 1.0, -2.5],
                         np.float32)
-    for (n, m, k) in [(66, 132, 128), (66, 131, 128)]:  # 4x64 tiles; 16x16 tiles (m % 4 != 0)
+    for (n, m, k) in [(66, 132, 128), (66, 131, 128)]:  # DPP instance; all-LDS instance
         a = rng.uniform(-1, 1, (n, k)).astype(np.float32)
         b = rng.uniform(-1, 1, (k, m)).astype(np.float32)
         ai = rng.random((n, k)) < 0.01
