@@ -206,6 +206,33 @@ def test_gemm_f32_exact_dpp_instance_agrees_and_specials():
         assert _bits_equal_nan_aware(got, want)
 
 
+def test_gemm_f32_exact_random_shapes_all_instances():
+    """40 seeded random shapes spread over the three instances (64x64 tiles,
+    16x16 tiles through LDS, 16x16 tiles with A by DPP row broadcast) and
+    their edges (k = 16, m = 4, one row, one column, k a multiple of 16 but
+    not of 256): every cell bitwise the oracle's ascending chain."""
+    rng = np.random.default_rng(2024)
+    shapes = [(1, 4, 16), (17, 8, 16), (16, 16, 16), (2, 4, 4096), (300, 4, 32)]
+    while len(shapes) < 40:
+        n = int(rng.integers(1, 400))
+        m = int(rng.integers(1, 400))
+        k = int(rng.integers(0, 700))
+        if rng.random() < 0.5:
+            m = max(4, m - m % 4)      # 16-byte rows of B
+            k = 16 * (k // 16)         # the DPP instance's k
+        shapes.append((n, m, k))
+    for (n, m, k) in shapes:
+        a = rng.uniform(-1, 1, (n, k)).astype(np.float32)
+        b = rng.uniform(-1, 1, (k, m)).astype(np.float32)
+        say(f"gemm f32 exact random shape {n}x{m}x{k}")
+        cb = ca.Buffer(max(1, n * m) * 4)
+        ca.gemm_f32_exact(ca.Buffer.from_array(a) if a.size else ca.Buffer(4),
+                          ca.Buffer.from_array(b) if b.size else ca.Buffer(4), cb, n, m, k)
+        got = cb.read(np.float32, (n, m))
+        want = oracle.matmul_f32(a, b) if k else np.zeros((n, m), np.float32)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (n, m, k)
+
+
 def test_gemm_f32_exact_run_to_run():
     n = m = k = 256
     a = ca.Buffer(n * k * 4)
