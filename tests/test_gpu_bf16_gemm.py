@@ -239,6 +239,42 @@ def test_decode_kernel_full_compare(mrows, n, k):
         assert hash_bits(c16.read(np.uint16)) == h
 
 
+def test_decode_and_tile_kernels_random_shapes():
+    """Seeded random shapes through gemm_bf16: 16 decode shapes (M <= 16; N
+    and K multiples of 8, so both the streamed path (K % 32 == 0) and the
+    register path, ragged column blocks and one to many k groups) and 12
+    wider ones (M > 16: tile, 64-k and bounds-checked edge kernels by
+    shape), each against the oracle under the stated bound, f32 and bf16
+    outputs consistent and bitwise run to run."""
+    rng = np.random.default_rng(777)
+    shapes = []
+    for _ in range(16):
+        m_rows = int(rng.integers(1, 17))
+        n = 8 * int(rng.integers(1, 400))
+        k = 8 * int(rng.integers(1, 800))
+        if rng.random() < 0.5:
+            k = 32 * max(1, k // 32)
+        shapes.append((m_rows, n, k))
+    for _ in range(12):
+        m_rows = int(rng.integers(17, 600))
+        n = int(rng.integers(1, 600))
+        k = int(rng.integers(1, 600))
+        if rng.random() < 0.5:
+            m_rows, n, k = 256 * int(rng.integers(1, 3)), 128 * int(rng.integers(1, 5)), 128 * int(rng.integers(1, 5))
+        shapes.append((m_rows, n, k))
+    for i, (m_rows, n, k) in enumerate(shapes):
+        say(f"bf16 gemm random shape M={m_rows} N={n} K={k}")
+        a, b, a16, b16 = _inputs(m_rows, n, k, seed=1000 + i, wscale=0.02 if m_rows <= 16 else 1.0)
+        c16, c32 = ca.Buffer(m_rows * n * 2), ca.Buffer(m_rows * n * 4)
+        ca.gemm_bf16(a, b, c16, m_rows, n, k)
+        ca.gemm_bf16(a, b, c32, m_rows, n, k, out_f32=True)
+        g16, g32 = c16.read(np.uint16, (m_rows, n)), c32.read(np.float32, (m_rows, n))
+        assert np.array_equal(g16, oracle.f32_to_bf16_bits_np(g32)), (m_rows, n, k)
+        _check(a16, b16, g32, g16)
+        ca.gemm_bf16(a, b, c16, m_rows, n, k)
+        assert np.array_equal(c16.read(np.uint16, (m_rows, n)), g16), (m_rows, n, k)
+
+
 def test_program_bf16_matmul():
     rt = ca.Runtime([])
     n, m, k = 32, 40, 24
