@@ -165,6 +165,35 @@ def test_few_pairs_form_equals_many_pairs_form(L, lens):
     _bitwise(small, want)
 
 
+def test_attention_random_configs_bitwise():
+    """Twelve seeded random configurations, B and H so that both the
+    eight-wave few-pairs kernel (B * H <= 128, L >= 64) and the four-wave
+    kernel run, random lengths in [0, L] (zeros and full lengths included)
+    and random scales: every output bitwise the oracle's."""
+    rng = np.random.default_rng(4242)
+    for i in range(12):
+        if i < 8:
+            B, H = int(rng.integers(1, 9)), int(rng.integers(1, 17))
+        else:
+            B, H = int(rng.integers(9, 20)), int(rng.integers(9, 17))
+        L = int(rng.integers(64, 1500))
+        lens = rng.integers(0, L + 1, B)
+        if i % 4 == 0:
+            lens[0] = L
+        if i % 4 == 1:
+            lens[-1] = 0
+        scale = float(np.float32(rng.uniform(0.05, 0.2)))
+        say(f"attention random config B={B} H={H} L={L} lens={list(map(int, lens))} scale={scale}")
+        seed = 5000 + i
+        q = dev_normal_bf16(B * H * D, seed, 0)
+        k = dev_normal_bf16(B * H * L * D, seed, 1)
+        v = dev_normal_bf16(B * H * L * D, seed, 2)
+        got = _run(q, k, v, lens, B, H, L, scale)
+        want = oracle.attn_decode(q.read(np.uint16, (B, H, D)), k.read(np.uint16, (B, H, L, D)),
+                                  v.read(np.uint16, (B, H, L, D)), np.asarray(lens, np.uint32), scale)
+        _bitwise(got, want)
+
+
 def test_few_pairs_form_ignores_rows_past_len():
     """K and V rows past each sequence's length hold NaN and infinities
     (inside the last, partial 64-row batch and beyond it); the eight-wave
