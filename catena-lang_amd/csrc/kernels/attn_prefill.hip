@@ -393,7 +393,14 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
   uint32_t glen[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) glen[u] = qlen[4 * qg + u];
-  const uint32_t lmin4 = glen[0], lmax4 = glen[3];  // prefixes grow with the query
+  // Prefixes grow with the query, but queries past nq (a last block's
+  // padding) have length 0: the longest of the four is their maximum, not
+  // the last one's (with two or three real queries in the wave, the last
+  // slot is padding).  The shortest is the first's (padding only follows).
+  uint32_t lmax4 = glen[0];
+#pragma unroll
+  for (int u = 1; u < 4; ++u) lmax4 = glen[u] > lmax4 ? glen[u] : lmax4;
+  const uint32_t lmin4 = glen[0];
   float acc0[4], acc1[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) acc0[u] = acc1[u] = __uint_as_float(0u);

@@ -311,6 +311,34 @@ def test_attention_causal_matches_prefix_decode(B, Tq, H, L, lens):
     _bitwise(o16.read(np.uint16, (B * Tq, H * D)), oracle.f32_to_bf16_bits_np(want))
 
 
+def test_attention_causal_random_configs():
+    """Ten seeded random causal configurations (Tq from 2 to 80, so both the
+    16-query prefill kernel and the one-query kernel run; cached prefixes
+    with lens > Tq, sequences shorter than Tq, empty ones; random scales):
+    f32 output bitwise the oracle's causal attention, bf16 output its RNE."""
+    D = 128
+    rng = np.random.default_rng(31337)
+    for i in range(10):
+        B, H = int(rng.integers(1, 4)), int(rng.integers(1, 4))
+        Tq = int(rng.integers(2, 81))
+        L = int(rng.integers(Tq, 700))
+        lens = [int(x) for x in rng.integers(0, L + 1, B)]
+        if i % 3 == 0:
+            lens[0] = L
+        scale = float(np.float32(rng.uniform(0.05, 0.2)))
+        q, k, v = _attn_inputs(B, Tq, H, L, 900 + i)
+        lb = ca.Buffer.from_array(np.array(lens, np.uint32))
+        o32 = ca.Buffer(B * Tq * H * D * 4)
+        o16 = ca.Buffer(B * Tq * H * D * 2)
+        say(f"causal attention random config B={B} Tq={Tq} H={H} L={L} lens={lens} scale={scale}")
+        ca.attn_causal_bf16(q, k, v, lb, o32, B, Tq, H, L, D, scale, out_f32=True)
+        ca.attn_causal_bf16(q, k, v, lb, o16, B, Tq, H, L, D, scale, out_f32=False)
+        want = od.attn_causal(q.read(np.uint16), k.read(np.uint16, (B, H, L, D)),
+                              v.read(np.uint16, (B, H, L, D)), lens, B, Tq, H, D, scale)
+        _bitwise(o32.read(np.float32, (B * Tq, H * D)), want)
+        _bitwise(o16.read(np.uint16, (B * Tq, H * D)), oracle.f32_to_bf16_bits_np(want))
+
+
 def test_attention_causal_prefill_nan_inf_tie_scores():
     """The 16-query prefill kernel (Tq >= 8) on scores with a NaN inside the
     prefix (the max restarts after it), a NaN at exactly one query's last
