@@ -330,6 +330,42 @@ def test_decoder_generate_n_equals_n_single_steps(cfg):
     assert np.array_equal(runs[0][1].view(np.uint32), runs[1][1].view(np.uint32))
 
 
+def test_decoder_random_configs_stagewise():
+    """Eight seeded random small models (1-3 heads, SwiGLU width, vocabulary,
+    batch, prompt length 1-60 with partial 16-query blocks among them, one
+    or two layers, cache 4-80 positions past the prompt): the prefill and
+    three decode steps, each checked stage by stage against the oracle, and
+    the greedy tokens against the oracle's argmax of the GPU logits."""
+    rng = np.random.default_rng(555)
+    prompts = [14, 43, 1, 27]  # partial blocks of 14 and 11 queries, one row, 27 = 16 + 11
+    for i in range(8):
+        H = int(rng.integers(1, 4))
+        cfg = type(f"Rand{i}", (), dict(
+            H=H, d=H * D, F=64 * int(rng.integers(1, 12)), V=8 * int(rng.integers(8, 200)),
+            B=int(rng.integers(1, 5)), layers=int(rng.integers(1, 3)),
+            T=prompts[i] if i < len(prompts) else int(rng.integers(1, 61))))
+        cfg.L = cfg.T + int(rng.integers(4, 81))
+        say(f"random decoder {i}: d={cfg.d} F={cfg.F} V={cfg.V} B={cfg.B} layers={cfg.layers} "
+            f"T={cfg.T} L={cfg.L}")
+        dec = ca.Decoder(cfg.d, cfg.H, cfg.F, cfg.layers, cfg.V, cfg.B, cfg.L)
+        dec.init_weights(seed=600 + i, std=0.02)
+        w = _weights(dec, cfg)
+        tokens = rng.integers(0, cfg.V, (cfg.B, cfg.T)).astype(np.uint32)
+        nxt = ca.Buffer(cfg.B * 4)
+        dec.prefill(ca.Buffer.from_array(tokens), cfg.B, cfg.T, nxt)
+        want = _check_forward(dec, cfg, w, tokens, cfg.T, cfg.T)
+        prev = nxt.read(np.uint32)
+        assert np.array_equal(prev, want)
+        for s_ in range(3):
+            out = ca.Buffer(cfg.B * 4)
+            dec.generate(1, out)
+            want = _check_forward(dec, cfg, w, prev, 1, cfg.T + s_ + 1)
+            got = out.read(np.uint32)
+            assert np.array_equal(got, want), (i, s_)
+            prev = got
+        dec.close()
+
+
 class C5Step(Tiny):
     H, F, V, B, T, L, layers = 16, 5632, 32000, 8, 4, 8, 1
     d = H * D
