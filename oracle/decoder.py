@@ -76,14 +76,28 @@ def _rope_positions(lens, batch: int, tq: int):
     return pos
 
 
-def rope_qkv(qkv, inv_freq, lens, batch: int, tq: int, heads: int, head_dim: int):
-    """-> (q bf16 [R][H*D], k bf16 [R][H][D], v bf16 [R][H][D], pos [R])."""
+def _rotation_positions(lens, batch: int, tq: int, max_len):
+    """The position each row is rotated at.  A row has a cache position only
+    when its sequence holds at least tq positions (lens[b] >= tq) and the
+    position lies before max_len (when given); a row without one (a sequence
+    shorter than its query count, or a position past the cache) is rotated
+    at position 0 and appends nothing -- this build's convention for rows
+    the decoder never produces (the reference has no RoPE)."""
+    pos = _rope_positions(lens, batch, tq)
+    ok = np.array([int(lens[r // tq]) >= tq and (max_len is None or pos[r] < max_len)
+                   for r in range(batch * tq)], bool)
+    return pos, np.where(ok, pos, 0).astype(np.uint32)
+
+
+def rope_qkv(qkv, inv_freq, lens, batch: int, tq: int, heads: int, head_dim: int, max_len=None):
+    """-> (q bf16 [R][H*D], k bf16 [R][H][D], v bf16 [R][H][D], pos [R]);
+    pos is the row's position lens[b] - tq + t, the rotation uses
+    _rotation_positions."""
     qkv = np.ascontiguousarray(qkv, np.float32)
     R = batch * tq
     HD = heads * head_dim
     assert qkv.shape == (R, 3 * HD)
-    pos = _rope_positions(lens, batch, tq)
-    p32 = np.maximum(pos, 0).astype(np.uint32)
+    pos, p32 = _rotation_positions(lens, batch, tq, max_len)
     inv = np.ascontiguousarray(inv_freq, np.float32)
     q = np.empty((R, HD), np.uint16)
     k = np.empty((R, heads, head_dim), np.uint16)
@@ -94,7 +108,8 @@ def rope_qkv(qkv, inv_freq, lens, batch: int, tq: int, heads: int, head_dim: int
     return q, k, v, pos
 
 
-def rope_qkv_per_head(qkv, inv_freq, lens, batch: int, tq: int, heads: int, head_dim: int):
+def rope_qkv_per_head(qkv, inv_freq, lens, batch: int, tq: int, heads: int, head_dim: int,
+                      max_len=None):
     """The same stage head by head through or_rope_f32 (small inputs only):
     the composition the row form must equal."""
     qkv = np.ascontiguousarray(qkv, np.float32)
@@ -103,14 +118,14 @@ def rope_qkv_per_head(qkv, inv_freq, lens, batch: int, tq: int, heads: int, head
     q = np.empty((R, HD), np.uint16)
     k = np.empty((R, heads, head_dim), np.uint16)
     v = np.empty((R, heads, head_dim), np.uint16)
-    pos = _rope_positions(lens, batch, tq)
+    pos, prot = _rotation_positions(lens, batch, tq, max_len)
     for r in range(R):
-        p = int(pos[r])
+        p = int(prot[r])
         for h in range(heads):
             qs = qkv[r, h * head_dim:(h + 1) * head_dim]
             ks = qkv[r, HD + h * head_dim:HD + (h + 1) * head_dim]
-            q[r, h * head_dim:(h + 1) * head_dim] = f32_to_bf16_bits_np(rope_f32(qs, max(p, 0), inv_freq))
-            k[r, h] = f32_to_bf16_bits_np(rope_f32(ks, max(p, 0), inv_freq))
+            q[r, h * head_dim:(h + 1) * head_dim] = f32_to_bf16_bits_np(rope_f32(qs, p, inv_freq))
+            k[r, h] = f32_to_bf16_bits_np(rope_f32(ks, p, inv_freq))
             v[r, h] = f32_to_bf16_bits_np(qkv[r, 2 * HD + h * head_dim:2 * HD + (h + 1) * head_dim])
     return q, k, v, pos
 

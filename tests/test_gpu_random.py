@@ -1,0 +1,252 @@
+"""Seeded random configurations of the row kernels and fused epilogues.
+
+The parametrized tests elsewhere pin chosen shapes and special values; these
+draw shapes, lengths, groupings and special-value positions at random (fixed
+seeds, so a failure names its case and repeats) and hold every output to the
+same bar: bitwise the oracle for the elementwise and fold kernels, bitwise
+the unfused GPU pair for the fused GEMM epilogues.
+"""
+import numpy as np
+import pytest
+
+import catena_amd as ca
+import oracle
+from oracle import decoder as od
+from gpu_util import dev_normal_bf16, say
+
+pytestmark = pytest.mark.gpu
+
+SPECIALS = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 3e38, -3e38, 1e-40, -1e-40, 1e-30],
+                    np.float32)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _init():
+    say("init device 0")
+    ca.init(0)
+
+
+def _bits_nan_aware(got, want):
+    """Bitwise equality, NaN for NaN: a NaN's sign and payload are not part
+    of the result (the host's default NaN is negative, the GPU's positive).
+    uint16 arrays are bf16 bit patterns."""
+    got, want = np.asarray(got), np.asarray(want)
+    assert got.shape == want.shape, (got.shape, want.shape)
+    if got.dtype == np.float32:
+        gn, wn = np.isnan(got), np.isnan(want)
+        got, want = got[~gn].view(np.uint32), want[~wn].view(np.uint32)
+    elif got.dtype == np.uint16:
+        gn, wn = (got & 0x7FFF) > 0x7F80, (want & 0x7FFF) > 0x7F80
+        got, want = got[~gn], want[~wn]
+    else:
+        gn = wn = np.zeros(got.shape, bool)
+    assert np.array_equal(gn, wn), int(np.sum(gn != wn))
+    assert np.array_equal(got, want), int(np.sum(got != want))
+
+
+def _rows(rng, rows, n, specials_frac):
+    x = (rng.standard_normal((rows, n)) * np.exp(rng.uniform(-3, 3, (rows, 1)))).astype(np.float32)
+    if specials_frac:
+        m = rng.random((rows, n)) < specials_frac
+        x[m] = rng.choice(SPECIALS, int(m.sum()))
+    return x
+
+
+def test_softmax_random_rows():
+    rng = np.random.default_rng(71)
+    for i in range(12):
+        rows, n = int(rng.integers(1, 6)), int(rng.integers(1, 6000))
+        x = _rows(rng, rows, n, 0.002 if i % 2 else 0.0)
+        say(f"softmax random rows={rows} n={n}")
+        y = ca.Buffer(x.nbytes)
+        ca.softmax_f32(ca.Buffer.from_array(x), y, rows, n)
+        got = y.read(np.float32, (rows, n))
+        for r in range(rows):
+            _bits_nan_aware(got[r], oracle.softmax_f32(x[r]))
+
+
+def test_folds_random_rows():
+    rng = np.random.default_rng(72)
+    for i in range(12):
+        rows, n = int(rng.integers(1, 8)), int(rng.integers(1, 70000))
+        x = _rows(rng, rows, n, 0.0005 if i % 3 == 0 else 0.0)
+        xb, o = ca.Buffer.from_array(x), ca.Buffer(rows * 4)
+        say(f"sum / mean / max random rows={rows} n={n}")
+        ca.sum_f32(xb, o, rows, n)
+        _bits_nan_aware(o.read(np.float32), np.array([oracle.fold_sum_f32(r) for r in x], np.float32))
+        ca.mean_f32(xb, o, rows, n)
+        want = np.array([np.float32(oracle.fold_sum_f32(r)) / np.float32(n) for r in x], np.float32)
+        _bits_nan_aware(o.read(np.float32), want)
+        ca.max_f32(xb, o, rows, n)
+        _bits_nan_aware(o.read(np.float32), np.array([oracle.fold_max_f32(r) for r in x], np.float32))
+
+
+def test_argmax_random_rows():
+    """Random widths, values drawn from a small set so ties are common, and
+    NaNs at random positions (the last NaN restarts the first-maximum fold)."""
+    rng = np.random.default_rng(73)
+    for i in range(12):
+        rows, n = int(rng.integers(1, 10)), int(rng.integers(1, 70000))
+        x = rng.integers(-20, 20, (rows, n)).astype(np.float32)
+        if i % 2:
+            m = rng.random((rows, n)) < 0.0005
+            x[m] = np.nan
+        if i % 3 == 0:
+            x[0] = -np.inf
+        idx = ca.Buffer(rows * 4)
+        say(f"argmax random rows={rows} n={n}")
+        ca.argmax_f32(ca.Buffer.from_array(x), idx, rows, n)
+        assert list(idx.read(np.uint32)) == [oracle.argmax_f32(r) for r in x]
+
+
+def test_rmsnorm_random_rows():
+    rng = np.random.default_rng(74)
+    for i in range(10):
+        rows, n = int(rng.integers(1, 40)), int(rng.integers(1, 8000))
+        x = _rows(rng, rows, n, 0.001 if i % 2 else 0.0)
+        say(f"rmsnorm random rows={rows} n={n}")
+        y = ca.Buffer(x.nbytes)
+        ca.rmsnorm_f32(ca.Buffer.from_array(x), y, rows, n)
+        _bits_nan_aware(y.read(np.float32, (rows, n)), oracle.rmsnorm_f32(x))
+
+
+def test_residual_rmsnorm_random_rows():
+    rng = np.random.default_rng(75)
+    for i in range(10):
+        rows_in, n = int(rng.integers(1, 300)), 4 * int(rng.integers(1, 1500))
+        x = _rows(rng, rows_in, n, 0.0005 if i % 2 else 0.0)
+        r = _rows(rng, rows_in, n, 0.0)
+        use_index = i % 3 == 1
+        use_resid = i % 4 != 3
+        idx = rng.integers(0, rows_in, int(rng.integers(1, rows_in + 1))).astype(np.uint32) if use_index else None
+        rows_out = idx.size if use_index else rows_in
+        hb, yb = ca.Buffer(rows_out * n * 4), ca.Buffer(rows_out * n * 2)
+        say(f"residual rmsnorm random rows={rows_out} n={n} resid={use_resid} index={use_index}")
+        ca.residual_rmsnorm_bf16(ca.Buffer.from_array(x), ca.Buffer.from_array(r) if use_resid else None,
+                                 ca.Buffer.from_array(idx) if use_index else None, hb, yb, rows_out, n)
+        src = idx.astype(np.int64) if use_index else np.arange(rows_in)
+        h, y = od.residual_rmsnorm_bf16(x[src], r[src] if use_resid else None)
+        _bits_nan_aware(hb.read(np.float32, (rows_out, n)), h)
+        _bits_nan_aware(yb.read(np.uint16, (rows_out, n)), y)
+
+
+def test_silu_mul_random():
+    rng = np.random.default_rng(76)
+    for i in range(10):
+        group = int(rng.choice([0, 4, 8, 64]))
+        F = 4 * int(rng.integers(1, 2000))
+        if group:
+            F = group * max(1, F // group)
+        rows = int(rng.integers(1, 20))
+        gu = (rng.standard_normal((rows, 2 * F)) * 6).astype(np.float32)
+        if i % 2:
+            m = rng.random((rows, 2 * F)) < 0.002
+            gu[m] = rng.choice(SPECIALS, int(m.sum()))
+        out = ca.Buffer(rows * F * 2)
+        say(f"silu_mul random rows={rows} F={F} group={group}")
+        ca.silu_mul_bf16(ca.Buffer.from_array(gu), out, rows, F, group)
+        _bits_nan_aware(out.read(np.uint16, (rows, F)), od.silu_mul_bf16(gu, F, group))
+
+
+def test_rope_qkv_random():
+    D = 128
+    rng = np.random.default_rng(77)
+    for i in range(8):
+        B, Tq, H = int(rng.integers(1, 5)), int(rng.integers(1, 40)), int(rng.integers(1, 4))
+        L = int(rng.integers(1, 700))
+        lens = [int(x) for x in rng.integers(0, L + Tq + 3, B)]  # some past L, some shorter than Tq
+        R = B * Tq
+        qkv = (rng.standard_normal((R, 3 * H * D)) * 3).astype(np.float32)
+        inv = ca.rope_inv_freq(D, float(rng.choice([10000.0, 500000.0])))
+        kc, vc = ca.Buffer(B * H * L * D * 2), ca.Buffer(B * H * L * D * 2)
+        sentinel = np.full(B * H * L * D, 0xABCD, np.uint16)
+        kc.write(sentinel)
+        vc.write(sentinel)
+        qb = ca.Buffer(R * H * D * 2)
+        say(f"rope qkv random B={B} Tq={Tq} H={H} L={L} lens={lens}")
+        ca.rope_qkv_bf16(ca.Buffer.from_array(qkv), ca.Buffer.from_array(inv),
+                         ca.Buffer.from_array(np.array(lens, np.uint32)), qb, kc, vc, B, Tq, H, D, L)
+        q, k, v, pos = od.rope_qkv(qkv, inv, lens, B, Tq, H, D, max_len=L)
+        _bits_nan_aware(qb.read(np.uint16, (R, H * D)), q)
+        kg, vg = kc.read(np.uint16, (B, H, L, D)), vc.read(np.uint16, (B, H, L, D))
+        written = np.zeros((B, L), bool)
+        for r in range(R):
+            b = r // Tq
+            p = int(pos[r])
+            # a row whose position falls outside [0, L) writes no cache
+            if 0 <= p < L and lens[b] >= Tq:
+                _bits_nan_aware(kg[b, :, p], k[r])
+                _bits_nan_aware(vg[b, :, p], v[r])
+                written[b, p] = True
+        assert np.all(kg.transpose(0, 2, 1, 3)[~written] == 0xABCD)
+        assert np.all(vg.transpose(0, 2, 1, 3)[~written] == 0xABCD)
+
+
+def test_gemm_swiglu_random_tiles():
+    """The SwiGLU-fused tile GEMM on random tiled shapes: the bits of the f32
+    GEMM followed by silu_mul with group 64."""
+    rng = np.random.default_rng(78)
+    for i in range(6):
+        n = 256 * int(rng.integers(1, 5))
+        m = 128 * int(rng.integers(1, 17))
+        k = 128 * int(rng.integers(1, 9))
+        a = dev_normal_bf16(n * k, 800 + i, 0, 1.0)
+        b = dev_normal_bf16(k * m, 800 + i, 1, 0.5)
+        say(f"bf16 GEMM + SwiGLU random n={n} m={m} k={k}")
+        act = ca.Buffer(n * (m // 2) * 2)
+        ca.gemm_bf16_silu(a, b, act, n, m, k)
+        gu = ca.Buffer(n * m * 4)
+        ca.gemm_bf16(a, b, gu, n, m, k, out_f32=True)
+        want = ca.Buffer(n * (m // 2) * 2)
+        ca.silu_mul_bf16(gu, want, n, m // 2, 64)
+        assert np.array_equal(act.read(np.uint16), want.read(np.uint16)), (n, m, k)
+
+
+def test_gemm_rope_qkv_random():
+    """The RoPE-fused q / k / v projection on random batches, query counts,
+    head counts, cache lengths and sequence lengths: the bits of the f32
+    GEMM followed by the RoPE + cache-append kernel, caches included."""
+    D = 128
+    rng = np.random.default_rng(79)
+    for i in range(6):
+        Tq = int(rng.choice([1, 2, 16, 64, 128, 256]))
+        B = max(1, 256 * int(rng.integers(1, 3)) // Tq)
+        H = int(rng.integers(1, 4))
+        L = int(rng.integers(1, 400))
+        k = 128 * int(rng.integers(1, 4))
+        R, m = B * Tq, 3 * H * D
+        lens = [int(x) for x in rng.integers(0, L + Tq + 5, B)]
+        a = dev_normal_bf16(R * k, 900 + i, 0, 1.0)
+        w = dev_normal_bf16(k * m, 900 + i, 1, 0.2)
+        inv = ca.Buffer.from_array(ca.rope_inv_freq(D, 10000.0))
+        tab = ca.Buffer(L * D * 4)
+        ca.rope_table_f32(inv, tab, L, D)
+        lb = ca.Buffer.from_array(np.array(lens, np.uint32))
+        sentinel = np.full(B * H * L * D, 0xABCD, np.uint16)
+        caches = [ca.Buffer.from_array(sentinel) for _ in range(4)]
+        q_f, q_u = ca.Buffer(R * H * D * 2), ca.Buffer(R * H * D * 2)
+        say(f"fused q/k/v + RoPE random B={B} Tq={Tq} H={H} L={L} k={k}")
+        ca.gemm_bf16_rope_qkv(a, w, tab, lb, q_f, caches[0], caches[1], B, Tq, H, L, k)
+        qkv = ca.Buffer(R * m * 4)
+        ca.gemm_bf16(a, w, qkv, R, m, k, out_f32=True)
+        ca.rope_qkv_bf16(qkv, inv, lb, q_u, caches[2], caches[3], B, Tq, H, D, L)
+        assert np.array_equal(q_f.read(np.uint16), q_u.read(np.uint16)), i
+        for got, want in ((caches[0], caches[2]), (caches[1], caches[3])):
+            assert np.array_equal(got.read(np.uint16), want.read(np.uint16)), i
+
+
+def test_embed_random():
+    rng = np.random.default_rng(80)
+    for i in range(6):
+        V, d = 8 * int(rng.integers(1, 300)), 8 * int(rng.integers(1, 400))
+        n_tok = int(rng.integers(1, 200))
+        tok = rng.integers(0, V + 3, n_tok).astype(np.uint32)  # some out of range
+        table = dev_normal_bf16(V * d, 1000 + i, 0)
+        x = ca.Buffer(n_tok * d * 4)
+        say(f"embed random V={V} d={d} tokens={n_tok}")
+        ca.embed_bf16(ca.Buffer.from_array(tok), table, x, n_tok, V, d)
+        got = x.read(np.float32, (n_tok, d))
+        t = table.read(np.uint16, (V, d))
+        ok = tok < V
+        _bits_nan_aware(got[ok], oracle.bf16_bits_to_f32(t[tok[ok].astype(np.int64)]))
+        assert np.all(np.isnan(got[~ok]))

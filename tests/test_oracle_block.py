@@ -149,9 +149,11 @@ def test_row_forms_equal_the_elementwise_composition():
     B, tq, H, Dh = 2, 3, 3, 128
     inv = oracle.rope_inv_freq(Dh, 10000.0)
     qkv = rng.standard_normal((B * tq, 3 * H * Dh)).astype(np.float32)
-    for lens in ([3, 700], [1, 2]):   # the second: positions below 0 clamp to 0
-        fast = od.rope_qkv(qkv, inv, lens, B, tq, H, Dh)
-        slow = od.rope_qkv_per_head(qkv, inv, lens, B, tq, H, Dh)
+    # the second: sequences shorter than tq rotate at position 0; the third:
+    # positions past a 4-position cache rotate at 0
+    for lens, max_len in (([3, 700], None), ([1, 2], None), ([3, 6], 4)):
+        fast = od.rope_qkv(qkv, inv, lens, B, tq, H, Dh, max_len=max_len)
+        slow = od.rope_qkv_per_head(qkv, inv, lens, B, tq, H, Dh, max_len=max_len)
         for x, y in zip(fast, slow):
             assert np.array_equal(x, y)
     x = rng.standard_normal((4, 300)).astype(np.float32)
