@@ -250,3 +250,32 @@ def test_embed_random():
         ok = tok < V
         _bits_nan_aware(got[ok], oracle.bf16_bits_to_f32(t[tok[ok].astype(np.int64)]))
         assert np.all(np.isnan(got[~ok]))
+
+
+def test_lm_head_argmax_random():
+    """The LM-head GEMM with the argmax in its epilogue on random decode
+    shapes (ragged last column block), weights with NaN entries and
+    duplicated columns: logits bitwise the plain GEMM's, tokens the oracle's
+    argmax of those logits."""
+    rng = np.random.default_rng(81)
+    for i in range(8):
+        n = int(rng.integers(1, 17))
+        m = 8 * int(rng.integers(16, 5000))
+        k = 8 * int(rng.integers(4, 400))
+        x = rng.normal(0, 1, (n, k)).astype(np.float32)
+        w = rng.normal(0, 0.05, (k, m)).astype(np.float32)
+        if i % 2:
+            c1, c2 = sorted(rng.choice(m, 2, replace=False))
+            w[:, c2] = w[:, c1] = rng.normal(0, 1, k).astype(np.float32)  # a tie between two columns
+        if i % 3 == 0:
+            msk = rng.random((k, m)) < 0.0003
+            w[msk] = np.nan
+        a = ca.Buffer.from_array(oracle.f32_to_bf16_bits_np(x))
+        b = ca.Buffer.from_array(oracle.f32_to_bf16_bits_np(w))
+        c, idx, plain = ca.Buffer(n * m * 4), ca.Buffer(n * 4), ca.Buffer(n * m * 4)
+        say(f"LM head argmax random n={n} m={m} k={k}")
+        ca.gemm_bf16_argmax(a, b, c, idx, n, m, k)
+        ca.gemm_bf16(a, b, plain, n, m, k, out_f32=True)
+        lg = c.read(np.float32, (n, m))
+        _bits_nan_aware(lg, plain.read(np.float32, (n, m)))
+        assert list(idx.read(np.uint32)) == [oracle.argmax_f32(lg[r]) for r in range(n)], i

@@ -83,3 +83,33 @@ def test_noalloc_decode_gemm_limits():
     ca.gemm_bf16(x2, w2, a, 8, 32000, 2048)
     assert L.catena_mi355x_gemm_bf16_decode_noalloc(x2.ptr, w2.ptr, b.ptr, 8, 32000, 2048, 0) == 0
     assert np.array_equal(a.read(np.uint16), b.read(np.uint16))
+
+
+def test_noalloc_decode_gemm_random_shapes():
+    """Seeded random decode shapes within the scratch limit (split K or not,
+    ragged column blocks, both output types), each called twice through the
+    allocation-free entry point (the second call on the scratch the first
+    left) and compared with the allocating entry point."""
+    L = ca.lib()
+    rng = np.random.default_rng(65)
+    done = 0
+    while done < 10:
+        m = int(rng.integers(1, 17))
+        n = 8 * int(rng.integers(1, 3000))
+        k = 8 * int(rng.integers(1, 2000))
+        groups, pbytes = ca.gemm_bf16_decode_plan(m, n, k)
+        if pbytes > 4 << 20:
+            continue
+        out_f32 = bool(rng.integers(0, 2))
+        dt, es = (np.uint32, 4) if out_f32 else (np.uint16, 2)
+        x, w = _pair(m, n, k, 70 + done)
+        got, want = ca.Buffer(m * n * es), ca.Buffer(m * n * es)
+        say(f"allocation-free decode GEMM random M={m} N={n} K={k} groups={groups} out_f32={out_f32}")
+        for _ in range(2):
+            st = L.catena_mi355x_gemm_bf16_decode_noalloc(x.ptr, w.ptr, got.ptr, m, n, k,
+                                                          1 if out_f32 else 0)
+            assert st == 0, ca.last_error()
+        ca.gemm_bf16(x, w, want, m, n, k, out_f32=out_f32)
+        ca.synchronize()
+        assert np.array_equal(got.read(dt), want.read(dt)), (m, n, k, out_f32)
+        done += 1
