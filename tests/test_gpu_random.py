@@ -279,3 +279,42 @@ def test_lm_head_argmax_random():
         lg = c.read(np.float32, (n, m))
         _bits_nan_aware(lg, plain.read(np.float32, (n, m)))
         assert list(idx.read(np.uint32)) == [oracle.argmax_f32(lg[r]) for r in range(n)], i
+
+
+def _mem_f32(res):
+    m = res.get()
+    out = ca.mem_to_array(m, np.float32)
+    if m.data:
+        ca.mem_free(m)
+    return out
+
+
+def test_runtime_programs_random():
+    """The stdlib programs through Runtime::exec on seeded random inputs
+    (lengths from 0): producers against their definitions, folds and softmax
+    bitwise the oracle's sequential forms."""
+    rt = ca.Runtime([])
+    rng = np.random.default_rng(82)
+    for i in range(8):
+        n = int(rng.integers(0, 3000))
+        x = _rows(rng, 1, max(n, 1), 0.001 if i % 2 else 0.0)[0][:n]
+        v = float(np.float32(rng.normal()))
+        say(f"runtime programs random n={n}")
+        [r] = rt.exec("tensor.broadcast-f32", [ca.Value.f32(v), ca.Value.u64(n)], 1)
+        _bits_nan_aware(_mem_f32(r), np.full(n, v, np.float32))
+        [r] = rt.exec("tensor.arange-f32", [ca.Value.u64(n)], 1)
+        _bits_nan_aware(_mem_f32(r), np.arange(n, dtype=np.float64).astype(np.float32))
+        s0 = int(rng.integers(0, n + 1))
+        ln = int(rng.integers(0, n - s0 + 1))
+        [r] = rt.exec("tensor.slice-f32", [rt.mem_f32(x), ca.Value.u64(s0), ca.Value.u64(ln)], 1)
+        _bits_nan_aware(_mem_f32(r), x[s0:s0 + ln])
+        y = _rows(rng, 1, 1 + int(rng.integers(0, 500)), 0.0)[0]
+        [r] = rt.exec("tensor.concat-f32", [rt.mem_f32(x), rt.mem_f32(y)], 1)
+        _bits_nan_aware(_mem_f32(r), np.concatenate([x, y]))
+        if n:
+            [r] = rt.exec("sum-f32", [rt.mem_f32(x)], 1)
+            _bits_nan_aware(np.float32(r.get()), np.float32(oracle.fold_sum_f32(x)))
+            [r] = rt.exec("max-f32", [rt.mem_f32(x)], 1)
+            _bits_nan_aware(np.float32(r.get()), np.float32(oracle.fold_max_f32(x)))
+            [r] = rt.exec("nn.softmax", [rt.mem_f32(x)], 1)
+            _bits_nan_aware(_mem_f32(r), oracle.softmax_f32(x))
