@@ -318,3 +318,75 @@ def test_runtime_programs_random():
             _bits_nan_aware(np.float32(r.get()), np.float32(oracle.fold_max_f32(x)))
             [r] = rt.exec("nn.softmax", [rt.mem_f32(x)], 1)
             _bits_nan_aware(_mem_f32(r), oracle.softmax_f32(x))
+
+
+def test_tile_gemm_paths_random():
+    """Random shapes aimed at each tile path of gemm_bf16: M a multiple of
+    256 with N a multiple of 128 and K a multiple of 128 (32-k kernel, wide
+    or narrow tiles by the host's rule) or of 64 only (64-k kernel), and the
+    same with one dimension off the tile (bounds-checked kernel): the bf16
+    output within the stated bound of the sequential oracle, bitwise the RNE
+    of the f32 output, and bitwise run to run."""
+    from gpu_util import as_f32, bf16_ulp_of, U
+    rng = np.random.default_rng(83)
+    for i in range(12):
+        n = 256 * int(rng.integers(1, 3))
+        m = 128 * int(rng.integers(1, 9))
+        k = 128 * int(rng.integers(1, 6)) if i % 3 != 1 else 64 * (2 * int(rng.integers(1, 5)) + 1)
+        if i % 4 == 3:
+            which = int(rng.integers(0, 3))
+            n, m, k = (n + 3, m, k) if which == 0 else (n, m + 8, k) if which == 1 else (n, m, k + 8)
+        a = dev_normal_bf16(n * k, 1100 + i, 0, 1.0)
+        b = dev_normal_bf16(k * m, 1100 + i, 1, 1.0)
+        c16, c32 = ca.Buffer(n * m * 2), ca.Buffer(n * m * 4)
+        say(f"bf16 tile GEMM path random n={n} m={m} k={k}")
+        ca.gemm_bf16(a, b, c16, n, m, k)
+        ca.gemm_bf16(a, b, c32, n, m, k, out_f32=True)
+        g16, g32 = c16.read(np.uint16, (n, m)), c32.read(np.float32, (n, m))
+        assert np.array_equal(g16, oracle.f32_to_bf16_bits_np(g32)), (n, m, k)
+        a16, b16 = a.read(np.uint16, (n, k)), b.read(np.uint16, (k, m))
+        af, bf = as_f32(a16).astype(np.float64), as_f32(b16).astype(np.float64)
+        absprod = np.abs(af) @ np.abs(bf)
+        bound = 8 * (k / 32 + 1) * U * absprod
+        assert np.all(np.abs(g32.astype(np.float64) - af @ bf) <= bound), (n, m, k)
+        _, seq16 = oracle.matmul_bf16(a16, b16)
+        g, s = as_f32(g16).astype(np.float64), as_f32(seq16).astype(np.float64)
+        assert np.all(np.abs(g - s) <= bound + k * U * absprod + bf16_ulp_of(np.maximum(np.abs(g), np.abs(s))))
+        ca.gemm_bf16(a, b, c16, n, m, k)
+        assert np.array_equal(c16.read(np.uint16, (n, m)), g16), (n, m, k)
+
+
+def test_attention_long_and_prefill_boundary_random():
+    """Decode attention at random long caches (up to 6000 positions) and the
+    causal form around the prefill kernel's cache limit (max_len ~830, the
+    one-query kernel beyond it): bitwise the oracle."""
+    D = 128
+    rng = np.random.default_rng(84)
+    for i in range(4):
+        B, H = int(rng.integers(1, 5)), int(rng.integers(1, 5))
+        L = int(rng.integers(2000, 6000))
+        lens = [int(x) for x in rng.integers(0, L + 1, B)]
+        scale = float(np.float32(rng.uniform(0.05, 0.2)))
+        q = dev_normal_bf16(B * H * D, 1200 + i, 0)
+        k = dev_normal_bf16(B * H * L * D, 1200 + i, 1)
+        v = dev_normal_bf16(B * H * L * D, 1200 + i, 2)
+        lb, o = ca.Buffer.from_array(np.array(lens, np.uint32)), ca.Buffer(B * H * D * 4)
+        say(f"attention long random B={B} H={H} L={L} lens={lens}")
+        ca.attn_decode_bf16(q, k, v, lb, o, B, H, L, D, scale)
+        want = oracle.attn_decode(q.read(np.uint16, (B, H, D)), k.read(np.uint16, (B, H, L, D)),
+                                  v.read(np.uint16, (B, H, L, D)), np.array(lens, np.uint32), scale)
+        _bits_nan_aware(o.read(np.float32, (B, H, D)), want)
+    for i in range(4):
+        B, H, Tq = int(rng.integers(1, 3)), int(rng.integers(1, 3)), int(rng.integers(8, 60))
+        L = int(rng.integers(700, 1100))
+        lens = [int(x) for x in rng.integers(Tq, L + 1, B)]
+        scale = float(np.float32(rng.uniform(0.05, 0.2)))
+        q = dev_normal_bf16(B * Tq * H * D, 1300 + i, 0)
+        k = dev_normal_bf16(B * H * L * D, 1300 + i, 1)
+        v = dev_normal_bf16(B * H * L * D, 1300 + i, 2)
+        lb, o = ca.Buffer.from_array(np.array(lens, np.uint32)), ca.Buffer(B * Tq * H * D * 4)
+        say(f"causal attention near the prefill limit B={B} Tq={Tq} H={H} L={L} lens={lens}")
+        ca.attn_causal_bf16(q, k, v, lb, o, B, Tq, H, L, D, scale, out_f32=True)
+        want = od.attn_causal(q.read(np.uint16), k.read(np.uint16, (B, H, L, D)),
+                              v.read(np.uint16, (B, H, L, D)), lens, B, Tq, H, D, scale)
+        _bits_nan_aware(o.read(np.float32, (B * Tq, H * D)), want)
