@@ -366,6 +366,38 @@ def test_decoder_random_configs_stagewise():
         dec.close()
 
 
+def test_decoder_random_large_batches_stagewise():
+    """Random models with batches past the decode GEMM's 16 rows (17-40
+    sequences: the projections and the LM head take the tile / edge GEMMs and
+    the argmax its own launch) and up to three layers: prefill and two
+    decode steps, stage by stage."""
+    rng = np.random.default_rng(556)
+    for i in range(3):
+        H = int(rng.integers(1, 3))
+        cfg = type(f"RandBig{i}", (), dict(
+            H=H, d=H * D, F=64 * int(rng.integers(1, 8)), V=8 * int(rng.integers(8, 100)),
+            B=int(rng.integers(17, 41)), layers=int(rng.integers(1, 4)), T=int(rng.integers(1, 20))))
+        cfg.L = cfg.T + int(rng.integers(3, 40))
+        say(f"random decoder, large batch {i}: d={cfg.d} F={cfg.F} V={cfg.V} B={cfg.B} "
+            f"layers={cfg.layers} T={cfg.T} L={cfg.L}")
+        dec = ca.Decoder(cfg.d, cfg.H, cfg.F, cfg.layers, cfg.V, cfg.B, cfg.L)
+        dec.init_weights(seed=700 + i, std=0.02)
+        w = _weights(dec, cfg)
+        tokens = rng.integers(0, cfg.V, (cfg.B, cfg.T)).astype(np.uint32)
+        nxt = ca.Buffer(cfg.B * 4)
+        dec.prefill(ca.Buffer.from_array(tokens), cfg.B, cfg.T, nxt)
+        prev = nxt.read(np.uint32)
+        assert np.array_equal(prev, _check_forward(dec, cfg, w, tokens, cfg.T, cfg.T))
+        for s_ in range(2):
+            out = ca.Buffer(cfg.B * 4)
+            dec.generate(1, out)
+            want = _check_forward(dec, cfg, w, prev, 1, cfg.T + s_ + 1)
+            got = out.read(np.uint32)
+            assert np.array_equal(got, want), (i, s_)
+            prev = got
+        dec.close()
+
+
 class C5Step(Tiny):
     H, F, V, B, T, L, layers = 16, 5632, 32000, 8, 4, 8, 1
     d = H * D
