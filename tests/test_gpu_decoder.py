@@ -398,6 +398,36 @@ def test_decoder_random_large_batches_stagewise():
         dec.close()
 
 
+def test_decoder_random_long_caches_stagewise():
+    """Random models whose caches pass the prefill kernel's LDS limit (max_len
+    900-1300: the causal attention takes the one-query kernel) with prompts
+    of 100-400 positions: prefill and two decode steps, stage by stage."""
+    rng = np.random.default_rng(557)
+    for i in range(2):
+        H = int(rng.integers(1, 3))
+        cfg = type(f"RandLong{i}", (), dict(
+            H=H, d=H * D, F=64 * int(rng.integers(1, 6)), V=8 * int(rng.integers(8, 64)),
+            B=int(rng.integers(1, 4)), layers=1, T=int(rng.integers(100, 401))))
+        cfg.L = int(rng.integers(900, 1301))
+        say(f"random decoder, long cache {i}: d={cfg.d} F={cfg.F} V={cfg.V} B={cfg.B} T={cfg.T} L={cfg.L}")
+        dec = ca.Decoder(cfg.d, cfg.H, cfg.F, cfg.layers, cfg.V, cfg.B, cfg.L)
+        dec.init_weights(seed=710 + i, std=0.02)
+        w = _weights(dec, cfg)
+        tokens = rng.integers(0, cfg.V, (cfg.B, cfg.T)).astype(np.uint32)
+        nxt = ca.Buffer(cfg.B * 4)
+        dec.prefill(ca.Buffer.from_array(tokens), cfg.B, cfg.T, nxt)
+        prev = nxt.read(np.uint32)
+        assert np.array_equal(prev, _check_forward(dec, cfg, w, tokens, cfg.T, cfg.T))
+        for s_ in range(2):
+            out = ca.Buffer(cfg.B * 4)
+            dec.generate(1, out)
+            want = _check_forward(dec, cfg, w, prev, 1, cfg.T + s_ + 1)
+            got = out.read(np.uint32)
+            assert np.array_equal(got, want), (i, s_)
+            prev = got
+        dec.close()
+
+
 class C5Step(Tiny):
     H, F, V, B, T, L, layers = 16, 5632, 32000, 8, 4, 8, 1
     d = H * D
