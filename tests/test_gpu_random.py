@@ -390,3 +390,36 @@ def test_attention_long_and_prefill_boundary_random():
         want = od.attn_causal(q.read(np.uint16), k.read(np.uint16, (B, H, L, D)),
                               v.read(np.uint16, (B, H, L, D)), lens, B, Tq, H, D, scale)
         _bits_nan_aware(o.read(np.float32, (B * Tq, H * D)), want)
+
+
+def test_bf16_gemm_special_values_random():
+    """NaN, +-inf and zeros at random positions of A and B (finite values of
+    moderate size, so no partial sum overflows): for every path of gemm_bf16
+    (decode, tile, edge), each output is NaN exactly where the exact product
+    is (a NaN input, inf * 0, or infinities of both signs in the sum),
+    +-inf exactly where it is, and finite elsewhere; the bf16 output is the
+    RNE of the f32 output."""
+    from gpu_util import as_f32
+    rng = np.random.default_rng(85)
+    shapes = [(8, 1024, 512), (16, 520, 96), (256, 256, 256), (512, 384, 192), (300, 200, 100)]
+    for i, (n, m, k) in enumerate(shapes):
+        a = rng.normal(0, 1, (n, k)).astype(np.float32)
+        b = rng.normal(0, 1, (k, m)).astype(np.float32)
+        for x in (a, b):
+            msk = rng.random(x.shape) < 0.0015
+            x[msk] = rng.choice(np.array([np.nan, np.inf, -np.inf, 0.0], np.float32), int(msk.sum()))
+        a16, b16 = oracle.f32_to_bf16_bits_np(a), oracle.f32_to_bf16_bits_np(b)
+        ab, bb = ca.Buffer.from_array(a16), ca.Buffer.from_array(b16)
+        c16, c32 = ca.Buffer(n * m * 2), ca.Buffer(n * m * 4)
+        say(f"bf16 GEMM special values random n={n} m={m} k={k}")
+        ca.gemm_bf16(ab, bb, c32, n, m, k, out_f32=True)
+        ca.gemm_bf16(ab, bb, c16, n, m, k)
+        g32 = c32.read(np.float32, (n, m))
+        _bits_nan_aware(c16.read(np.uint16, (n, m)), oracle.f32_to_bf16_bits_np(g32))
+        af, bf = as_f32(a16).astype(np.float64), as_f32(b16).astype(np.float64)
+        with np.errstate(invalid="ignore", over="ignore"):
+            exact = af @ bf
+        assert np.array_equal(np.isnan(g32), np.isnan(exact)), (n, m, k)
+        inf = np.isinf(exact)
+        assert np.array_equal(np.isinf(g32), inf), (n, m, k)
+        assert np.array_equal(np.sign(g32[inf]), np.sign(exact[inf])), (n, m, k)
