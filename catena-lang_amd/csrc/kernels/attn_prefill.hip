@@ -249,6 +249,17 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
       ln4[u] = -1;
       fm4[u] = FirstMax{__uint_as_float(0xFF800000u), 0xFFFFFFFFu};
     }
+    // per lane the positions ascend, so its first maximum is kept by a
+    // strict comparison (a NaN never replaces it; a query with one takes the
+    // two-pass form below; a lane holding only -inf stays empty, which the
+    // combine treats as -inf)
+    float bv[4];
+    uint32_t bi[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      bv[u] = __uint_as_float(0xFF800000u);
+      bi[u] = 0xFFFFFFFFu;
+    }
     for (uint32_t t = lane; t < lmx; t += 64) {
       const float* row = sT + t * ST + wave;
 #pragma unroll
@@ -256,10 +267,15 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
         if (t < len4[u]) {
           const float sv = row[4 * u];
           if (sv != sv) ln4[u] = (int)t;
-          fm4[u] = first_max_combine(fm4[u], FirstMax{sv, t});
+          if (sv > bv[u]) {
+            bv[u] = sv;
+            bi[u] = t;
+          }
         }
       }
     }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) fm4[u] = FirstMax{bv[u], bi[u]};
     // the four queries' butterflies interleaved (independent shuffle chains)
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
