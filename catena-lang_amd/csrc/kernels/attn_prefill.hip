@@ -34,22 +34,22 @@
 // common.h) by one wave; exp~ elementwise; the denominators are 16
 // independent serial folds, one lane per query; p = e / den elementwise.
 // Output: wave w owns queries 4w .. 4w+3 and lane l columns 2l, 2l+1 (8
-// accumulators); keys are walked in ascending order through 64-row V blocks
-// staged in LDS, the next block's loads in flight while one is folded.  Keys
+// accumulators); keys are walked in ascending order, the wave loading V rows
+// itself (one coalesced row per load, the next 16 keys in flight while 16
+// are folded; no workgroup barrier); the p values of 16 keys are read once
+// per lane and broadcast by DPP.  LDS holds the q rows (bf16) and the score
+// matrix only, so three or four workgroups share a CU at the C5 shape.  Keys
 // below the shortest of the 4 prefixes need no mask; past it, a key beyond a
 // query's prefix leaves that accumulator untouched.
 #include "common.h"
 
 namespace {
 constexpr int D = 128;
-constexpr int QS = D + 4;            // qf row stride (floats)
 constexpr int QH = D + 8;            // qh row stride (bf16): the MFMA A-operand reads (16 rows,
                                      // 16 bytes each) cover the 64 banks once
 constexpr int QB = 16;               // queries per workgroup
 constexpr int HALF = QB / 2;         // queries per score item / output thread
 constexpr int ST = QB + 1;           // sT row stride (floats)
-constexpr int VBLK = 64;             // keys per V stage
-constexpr int VSTAGE = VBLK * D * 2; // bytes (bf16)
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
@@ -70,6 +70,24 @@ CATENA_DEV FirstMax wave_first_max(FirstMax a) {
   return a;
 }
 
+// Keys Q .. 15 of a group of 16 in the output fold: lane 16j + q holds the
+// p values of key q for the wave's 4 queries (pq[u]), w[Q] the lane's two V
+// columns of key Q.  acc = acc + fl(p * v) per query and column, keys in
+// ascending order; each key's p reaches its row by DPP broadcast.
+template <int Q>
+CATENA_DEV void pv_keys16(const float (&pq)[4], const uint32_t (&w)[16], float (&acc0)[4],
+                          float (&acc1)[4]) {
+  const float v0 = bf16lo(w[Q]), v1 = bf16hi(w[Q]);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const float x0 = row_bcast16<Q>(pq[u]) * v0;
+    const float x1 = row_bcast16<Q>(pq[u]) * v1;
+    acc0[u] = acc0[u] + x0;
+    acc1[u] = acc1[u] + x1;
+  }
+  if constexpr (Q + 1 < 16) pv_keys16<Q + 1>(pq, w, acc0, acc1);
+}
+
 CATENA_DEV uint32_t query_len(uint32_t lens_b, uint32_t L, uint32_t Tq, uint32_t tq) {
   uint32_t len = lens_b > L ? L : lens_b;
   const uint32_t later = Tq - 1 - tq;
@@ -83,11 +101,10 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
                              void* __restrict__ o, uint32_t B, uint32_t H, uint32_t L,
                              uint32_t Tq, float scale) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  float* qf = reinterpret_cast<float*>(smem);                      // [QB][QS]
-  uint16_t* qh = reinterpret_cast<uint16_t*>(smem + QB * QS * 4);  // [QB][QH] bf16
-  unsigned char* vstage = smem + QB * QS * 4 + QB * QH * 2;        // [VBLK][D] bf16
-  float* red = reinterpret_cast<float*>(vstage + VSTAGE);          // [QB] max, [QB] den
-  float* sT = red + 3 * QB;                                        // [Lmax][ST] (after qlen)
+  uint16_t* qh = reinterpret_cast<uint16_t*>(smem);                // [QB][QH] bf16
+  float* red = reinterpret_cast<float*>(smem + QB * QH * 2);       // [QB] max, [QB] den
+  float* sink = red + 3 * QB;                                      // (after qlen) unread
+  float* sT = red + 3 * QB + 4;                                    // [Lmax][ST]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t BH = B * H;
@@ -107,7 +124,7 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
 
   const uint16_t* kb = k + (uint64_t)bh * L * D;
   const uint16_t* vb = v + (uint64_t)bh * L * D;
-  // q rows of this block, widened (rows past nq are zero and never used);
+  // q rows of this block, bf16 (rows past nq are zero and never used);
   // `unsafe` notes a value outside the MFMA fold's exact range
   // thread t: row t / 16, values 8 (t % 16) .. +7 (one 16-byte load)
   int unsafe = 0;
@@ -120,8 +137,6 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
       const uint32_t lo = w[c] & 0x7FFFu, hi = (w[c] >> 16) & 0x7FFFu;
       unsafe |= (lo != 0u && lo < kSafeLo) || lo >= kSafeHi || (hi != 0u && hi < kSafeLo) || hi >= kSafeHi;
     }
-    *reinterpret_cast<f32x4_t*>(qf + i * QS + d0) = f32x4_t{bf16lo(w[0]), bf16hi(w[0]), bf16lo(w[1]), bf16hi(w[1])};
-    *reinterpret_cast<f32x4_t*>(qf + i * QS + d0 + 4) = f32x4_t{bf16lo(w[2]), bf16hi(w[2]), bf16lo(w[3]), bf16hi(w[3])};
     *reinterpret_cast<u32x4_t*>(qh + i * QH + d0) = w;
   }
   __syncthreads();
@@ -147,21 +162,21 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
   {
     // matrix-core fold: lane l, accumulator r holds key kblk*64 + 16 (r / 4)
     // + l % 16 against query 4 (l / 16) + r % 4
-    uint32_t ql[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) ql[u] = qlen[4 * (lane >> 4) + u];
     // lane l's A operand: query l % 16's row, packed bf16 in LDS, eight d
     // values per read, the next read issued before the current MFMAs
     const u32x4_t* qrow = reinterpret_cast<const u32x4_t*>(qh + (lane & 15) * QH);
     u16x2_t mn = {0xFFFF, 0xFFFF}, mx = {0, 0};
     const u16x2_t one = {1, 1};
+    // the K row chunks rotate through one set of registers: chunk c of the
+    // wave's next block (its row clamped like kload_rows; past the last
+    // block, a row in use) is loaded as soon as chunk c of the current one
+    // has been folded, a whole block ahead of its use
     u32x4_t raw[D / 8];
     if ((uint32_t)wave < nkb) kload_rows(wave, raw);
     for (uint32_t kblk = wave; kblk < nkb; kblk += 4) {
-      u32x4_t cur[D / 8];
-#pragma unroll
-      for (int c = 0; c < D / 8; ++c) cur[c] = raw[c];
-      if (kblk + 4 < nkb) kload_rows(kblk + 4, raw);
+      const uint32_t jn = (kblk + 4) * 64 + lane;
+      const u32x4_t* nsrc =
+          reinterpret_cast<const u32x4_t*>(kb + (uint64_t)(jn < lmax ? jn : lmax - 1u) * D);
       f32x16_t acc;
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[r] = __uint_as_float(0u);
@@ -172,18 +187,26 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
         if (c + 1 < D / 8) qnext = qrow[c + 1];
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-          const uint32_t word = cur[c][w], qword = qcur[w];
+          const uint32_t word = raw[c][w], qword = qcur[w];
           const u16x2_t mag = __builtin_bit_cast(u16x2_t, word & 0x7FFF7FFFu);
           mn = __builtin_elementwise_min(mn, mag - one);
           mx = __builtin_elementwise_max(mx, mag);
           acc = __builtin_amdgcn_mfma_f32_16x16x1f32(bf16lo(qword), bf16lo(word), acc, 0, 0, 0);
           acc = __builtin_amdgcn_mfma_f32_16x16x1f32(bf16hi(qword), bf16hi(word), acc, 0, 0, 0);
         }
+        raw[c] = nsrc[c];
+        // one chunk at a time: its conversions and range check are not
+        // hoisted ahead, nor the next block's load of it sunk behind
+        __builtin_amdgcn_sched_barrier(0);
       }
+      // a key past the query's prefix but inside the block's rows leaves an
+      // entry no later phase reads; one past the rows goes to `sink` (no
+      // branch around the stores)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const uint32_t j = kblk * 64 + 16 * (r >> 2) + (lane & 15);
-        if (j < ql[r & 3]) sT[j * ST + 4 * (lane >> 4) + (r & 3)] = acc[r] * scale;
+        float* dst = j < lmax ? sT + j * ST + 4 * (lane >> 4) + (r & 3) : sink;
+        *dst = acc[r] * scale;
       }
     }
     // x - 1 wraps a zero to 0xFFFF: a minimum below kSafeLo - 1 is a nonzero
@@ -193,36 +216,35 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
     unsafe |= lo < kSafeLo - 1u || hi >= kSafeHi;
   }
   if (__syncthreads_or(unsafe)) {
-    // the VALU fold: lane l owns key kb*64 + l, its 128 K values widened into
-    // registers once and folded against each of the 16 queries (LDS
-    // broadcasts), v_mul_f32 then v_add_f32 per product
-    u32x4_t raw[D / 8];
-    if ((uint32_t)wave < nkb) kload(wave, raw);
+    // the VALU fold: lane l owns key kb*64 + l, its 128 K values in registers
+    // (bf16 pairs, widened at each use) folded against each of the 16
+    // queries (LDS broadcasts of the bf16 q rows), v_mul_f32 then v_add_f32
+    // per product, d ascending
     for (uint32_t kblk = wave; kblk < nkb; kblk += 4) {
-      float kf[D];
-#pragma unroll
-      for (int c = 0; c < D / 8; ++c) {
-        kf[8 * c + 0] = bf16lo(raw[c][0]); kf[8 * c + 1] = bf16hi(raw[c][0]);
-        kf[8 * c + 2] = bf16lo(raw[c][1]); kf[8 * c + 3] = bf16hi(raw[c][1]);
-        kf[8 * c + 4] = bf16lo(raw[c][2]); kf[8 * c + 5] = bf16hi(raw[c][2]);
-        kf[8 * c + 6] = bf16lo(raw[c][3]); kf[8 * c + 7] = bf16hi(raw[c][3]);
-      }
-      if (kblk + 4 < nkb) kload(kblk + 4, raw);
+      u32x4_t raw[D / 8];
+      kload(kblk, raw);
       const uint32_t j = kblk * 64 + lane;
 #pragma unroll 1
       for (int i = 0; i < QB; ++i) {
         const uint32_t li = qlen[i];
         if (kblk * 64 >= li) continue;
-        const f32x4_t* q4 = reinterpret_cast<const f32x4_t*>(qf + i * QS);
+        // keeps the widened K values out of registers across queries (the
+        // compiler would otherwise hoist all 128 of them out of this loop)
+#pragma unroll
+        for (int c = 0; c < D / 8; ++c) asm volatile("" : "+v"(raw[c]));
+        const u32x4_t* q8 = reinterpret_cast<const u32x4_t*>(qh + i * QH);
         float acc = __uint_as_float(0u);
 #pragma unroll
-        for (int c = 0; c < D / 4; ++c) {
-          const f32x4_t qq = q4[c];
-          float p;
-          p = qq[0] * kf[4 * c + 0]; acc = acc + p;
-          p = qq[1] * kf[4 * c + 1]; acc = acc + p;
-          p = qq[2] * kf[4 * c + 2]; acc = acc + p;
-          p = qq[3] * kf[4 * c + 3]; acc = acc + p;
+        for (int c = 0; c < D / 8; ++c) {
+          const u32x4_t qq = q8[c];
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            float p;
+            p = bf16lo(qq[w]) * bf16lo(raw[c][w]); acc = acc + p;
+            p = bf16hi(qq[w]) * bf16hi(raw[c][w]); acc = acc + p;
+          }
+          // eight products in flight at a time, not all 128
+          __builtin_amdgcn_sched_barrier(0);
         }
         if (j < li) sT[j * ST + i] = acc * scale;
       }
@@ -421,59 +443,57 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
 #pragma unroll
   for (int u = 0; u < 4; ++u) acc0[u] = acc1[u] = __uint_as_float(0u);
 
-  const uint32_t nvb = (lmax + VBLK - 1) / VBLK;
-  // cooperative V stage: 64 rows x 256 B = 1024 x 16 B, 4 per thread
-  auto vload = [&](uint32_t blk, u32x4_t r[4]) {
+  // the wave reads V rows itself (lane cp: the row's 32-bit word cp, one
+  // coalesced 256-byte row per load), 16 keys ahead of the fold, up to its
+  // own longest prefix
+  const uint32_t* vrow = reinterpret_cast<const uint32_t*>(vb) + cp;
+  uint32_t t = 0;
+  uint32_t wn[16];
+  if (lmin4 >= 16) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) wn[j] = vrow[(uint64_t)j * (D / 2)];
+  }
+  // groups of 16 unmasked keys: one LDS read of p per query and group
+  // (lane 16j + q: key t + q) instead of a broadcast read per key
+  for (; t + 16 <= lmin4; t += 16) {
+    uint32_t w[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) w[j] = wn[j];
+    if (t + 32 <= lmin4) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) wn[j] = vrow[(uint64_t)(t + 16 + j) * (D / 2)];
+    }
+    const float* pl = sT + (t + (uint32_t)(lane & 15)) * ST + 4 * qg;
+    float pq[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) pq[u] = pl[u];
+    pv_keys16<0>(pq, w, acc0, acc1);
+  }
+  for (; t < lmin4; ++t) {
+    const uint32_t w = vrow[(uint64_t)t * (D / 2)];
+    const float v0 = bf16lo(w), v1 = bf16hi(w);
+    const float* prow = sT + t * ST + 4 * qg;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const uint32_t c = tid + 256 * u;  // 16-byte chunk
-      const uint32_t row = c >> 4, part = c & 15;
-      const uint32_t t = blk * VBLK + row;
-      r[u] = t < lmax ? *reinterpret_cast<const u32x4_t*>(vb + (uint64_t)t * D + part * 8)
-                      : u32x4_t{0u, 0u, 0u, 0u};
+      const float pu = prow[u];
+      const float x0 = pu * v0, x1 = pu * v1;
+      acc0[u] = acc0[u] + x0;
+      acc1[u] = acc1[u] + x1;
     }
-  };
-  u32x4_t vr[4];
-  if (nvb > 0) vload(0, vr);
-  const uint32_t* vs32 = reinterpret_cast<const uint32_t*>(vstage);
-  for (uint32_t blk = 0; blk < nvb; ++blk) {
+  }
+  for (; t < lmax4; ++t) {
+    const uint32_t w = vrow[(uint64_t)t * (D / 2)];
+    const float v0 = bf16lo(w), v1 = bf16hi(w);
+    const float* prow = sT + t * ST + 4 * qg;
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      reinterpret_cast<u32x4_t*>(vstage)[tid + 256 * u] = vr[u];
-    __syncthreads();
-    if (blk + 1 < nvb) vload(blk + 1, vr);
-    const uint32_t tb = blk * VBLK;
-    const uint32_t rows = lmax - tb < (uint32_t)VBLK ? lmax - tb : (uint32_t)VBLK;
-    const uint32_t full = lmin4 > tb ? (lmin4 - tb < rows ? lmin4 - tb : rows) : 0u;
-    const uint32_t part = lmax4 > tb ? (lmax4 - tb < rows ? lmax4 - tb : rows) : 0u;
-    for (uint32_t r = 0; r < full; ++r) {
-      const uint32_t w = vs32[r * (D / 2) + cp];
-      const float v0 = bf16lo(w), v1 = bf16hi(w);
-      const float* prow = sT + (tb + r) * ST + 4 * qg;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < 4; ++u) {
+      if (t < glen[u]) {
         const float pu = prow[u];
         const float x0 = pu * v0, x1 = pu * v1;
         acc0[u] = acc0[u] + x0;
         acc1[u] = acc1[u] + x1;
       }
     }
-    for (uint32_t r = full; r < part; ++r) {
-      const uint32_t t = tb + r;
-      const uint32_t w = vs32[r * (D / 2) + cp];
-      const float v0 = bf16lo(w), v1 = bf16hi(w);
-      const float* prow = sT + t * ST + 4 * qg;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        if (t < glen[u]) {
-          const float pu = prow[u];
-          const float x0 = pu * v0, x1 = pu * v1;
-          acc0[u] = acc0[u] + x0;
-          acc1[u] = acc1[u] + x1;
-        }
-      }
-    }
-    __syncthreads();
   }
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
@@ -488,7 +508,7 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
 }
 
 // grid = B * H * ceil(Tq / 16), block = 256, dynamic LDS =
-// 16*132*4 + 16*136*2 + 64*128*2 + 3*16*4 + Lmax*17*4 with Lmax >= min(max lens, L).
+// 16*136*2 + 3*16*4 + 16 + Lmax*17*4 with Lmax >= min(max lens, L).
 extern "C" __global__ __launch_bounds__(256) void catena_attn_prefill_bf16_d128_f32out(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint32_t* __restrict__ lens, float* __restrict__ o, uint32_t B, uint32_t H, uint32_t L,

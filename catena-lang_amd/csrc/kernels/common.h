@@ -453,6 +453,12 @@ CATENA_DEV uint32_t wave_umax(uint32_t x) {
 #undef CATENA_DPP_MAX
   return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
 }
+// Lane Q of each 16-lane row, broadcast to its row (DPP row_newbcast; the
+// compiler folds it into the consuming VALU instruction's operand)
+template <int Q>
+CATENA_DEV float row_bcast16(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x150 + Q, 0xF, 0xF, false));
+}
 CATENA_DEV float key_score(uint64_t key) {
   const uint32_t mono = (uint32_t)(key >> 32);
   const uint32_t canon = (mono & 0x80000000u) ? (mono & 0x7FFFFFFFu) : ~mono;

@@ -274,12 +274,6 @@ extern "C" __global__ __launch_bounds__(256) void catena_gemm_f32_exact_t16(
 namespace {
 constexpr int Q_T = 16, Q_KC = 256;
 
-// Lane Q of each 16-lane row, broadcast to its row (DPP row_newbcast)
-template <int Q>
-CATENA_DEV float row_bcast16(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x150 + Q, 0xF, 0xF, false));
-}
-
 // acc = acc + fl(A_k * b_k) for 16 k in ascending order, A_k in lane k % 16
 // of every row of ra: the 16 products first, then the 16 dependent adds
 // (with one wave per SIMD nothing else fills the wait when each add follows
