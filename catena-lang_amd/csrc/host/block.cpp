@@ -113,7 +113,8 @@ int catena_mi355x_attn_causal_bf16(const uint16_t* q, const uint16_t* k, const u
   // it is used while two workgroups still fit a CU; it reads q rows with
   // 16-byte loads); otherwise the one-query-per-workgroup kernel.  Both give
   // the same bits.
-  const size_t lds_pf = 16 * 136 * 2 + 3 * 16 * 4 + 16 + (size_t)max_len * 17 * 4;
+  const size_t lds_pf =
+      16 * 136 * 2 + 3 * 16 * 4 + 3 * 4 * 16 * 4 + (size_t)ceil_div(max_len, 64) * 64 * 17 * 4;
   if (tq >= 8 && lds_pf <= 80 * 1024 && aligned16(q)) {
     const uint64_t nqb = ceil_div(tq, 16);
     const uint64_t grid = (uint64_t)batch * heads * nqb;

@@ -59,6 +59,9 @@ typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
 // 64 .. 189, i.e. magnitude in [2^-63, 2^63).
 constexpr uint32_t kSafeLo = 0x2000u, kSafeHi = 0x5F00u;
 
+// Raw buffer descriptor word 3 (stride 0, bounds-checked by byte offset)
+constexpr int kRsrcWord3 = 0x00020000;
+
 CATENA_DEV FirstMax wave_first_max(FirstMax a) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
@@ -68,6 +71,15 @@ CATENA_DEV FirstMax wave_first_max(FirstMax a) {
     a = first_max_combine(a, b);
   }
   return a;
+}
+
+// a combined with the value CTRL's DPP row pattern brings to this lane
+template <int CTRL>
+CATENA_DEV FirstMax row_first_max(FirstMax a) {
+  FirstMax b;
+  b.v = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a.v), CTRL, 0xF, 0xF, false));
+  b.i = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)a.i, CTRL, 0xF, 0xF, false);
+  return first_max_combine(a, b);
 }
 
 // Keys Q .. 15 of a group of 16 in the output fold: lane 16j + q holds the
@@ -103,8 +115,8 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   uint16_t* qh = reinterpret_cast<uint16_t*>(smem);                // [QB][QH] bf16
   float* red = reinterpret_cast<float*>(smem + QB * QH * 2);       // [QB] max, [QB] den
-  float* sink = red + 3 * QB;                                      // (after qlen) unread
-  float* sT = red + 3 * QB + 4;                                    // [Lmax][ST]
+  float* part = red + 3 * QB;  // [3][4 waves][QB]: first-max value, its index, last NaN
+  float* sT = part + 3 * 4 * QB;                                   // [Lmax][ST]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t BH = B * H;
@@ -149,34 +161,44 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
 #pragma unroll
     for (int c = 0; c < D / 8; ++c) r[c] = j < lmax ? src[c] : u32x4_t{0u, 0u, 0u, 0u};
   };
-  // the MFMA path's form: every lane loads a row in use (a key past lmax
-  // reads row lmax - 1; its scores are never stored), so the loads need no
-  // branch and the range check sees only rows the scores use
-  auto kload_rows = [&](uint32_t kblk, u32x4_t r[D / 8]) {
-    const uint32_t j = kblk * 64 + lane;
-    const uint32_t jr = j < lmax ? j : lmax - 1u;
-    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(kb + (uint64_t)jr * D);
-#pragma unroll
-    for (int c = 0; c < D / 8; ++c) r[c] = src[c];
+  // the MFMA path's form: buffer loads over the block's rows (a key past
+  // lmax reads zeros, which the range check passes and whose scores are
+  // never used), so the loads need no branch
+  const __amdgpu_buffer_rsrc_t krs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)kb, (short)0,
+                                        __builtin_amdgcn_readfirstlane((int)(lmax * (uint32_t)D * 2u)), kRsrcWord3);
+  auto kchunk = [&](uint32_t j, int c) -> u32x4_t {
+    return __builtin_amdgcn_raw_buffer_load_b128(krs, (int)(j * (uint32_t)D * 2u) + 16 * c, 0, 0);
   };
   {
     // matrix-core fold: lane l, accumulator r holds key kblk*64 + 16 (r / 4)
-    // + l % 16 against query 4 (l / 16) + r % 4
+    // + l % 16 against query 4 (l / 16) + r % 4.  Each lane also keeps, per
+    // query, the first maximum and the last NaN position of the scores it
+    // produces (positions ascend per lane), the max phase's partials
     // lane l's A operand: query l % 16's row, packed bf16 in LDS, eight d
     // values per read, the next read issued before the current MFMAs
     const u32x4_t* qrow = reinterpret_cast<const u32x4_t*>(qh + (lane & 15) * QH);
     u16x2_t mn = {0xFFFF, 0xFFFF}, mx = {0, 0};
     const u16x2_t one = {1, 1};
+    uint32_t ql[4];
+    float bv[4];
+    uint32_t bi[4];
+    int ln[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      ql[u] = qlen[4 * (lane >> 4) + u];
+      bv[u] = __uint_as_float(0xFF800000u);
+      bi[u] = 0xFFFFFFFFu;
+      ln[u] = -1;
+    }
     // the K row chunks rotate through one set of registers: chunk c of the
-    // wave's next block (its row clamped like kload_rows; past the last
-    // block, a row in use) is loaded as soon as chunk c of the current one
-    // has been folded, a whole block ahead of its use
+    // wave's next block (zeros past the rows) is loaded as soon as chunk c
+    // of the current one has been folded, a whole block ahead of its use
     u32x4_t raw[D / 8];
-    if ((uint32_t)wave < nkb) kload_rows(wave, raw);
+#pragma unroll
+    for (int c = 0; c < D / 8; ++c) raw[c] = kchunk((uint32_t)wave * 64 + lane, c);
     for (uint32_t kblk = wave; kblk < nkb; kblk += 4) {
       const uint32_t jn = (kblk + 4) * 64 + lane;
-      const u32x4_t* nsrc =
-          reinterpret_cast<const u32x4_t*>(kb + (uint64_t)(jn < lmax ? jn : lmax - 1u) * D);
       f32x16_t acc;
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[r] = __uint_as_float(0u);
@@ -194,19 +216,49 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
           acc = __builtin_amdgcn_mfma_f32_16x16x1f32(bf16lo(qword), bf16lo(word), acc, 0, 0, 0);
           acc = __builtin_amdgcn_mfma_f32_16x16x1f32(bf16hi(qword), bf16hi(word), acc, 0, 0, 0);
         }
-        raw[c] = nsrc[c];
+        raw[c] = kchunk(jn, c);
         // one chunk at a time: its conversions and range check are not
         // hoisted ahead, nor the next block's load of it sunk behind
         __builtin_amdgcn_sched_barrier(0);
       }
-      // a key past the query's prefix but inside the block's rows leaves an
-      // entry no later phase reads; one past the rows goes to `sink` (no
-      // branch around the stores)
+      // scores of the block (sT has rows for every key of the last block;
+      // one past a query's prefix is never read), and the running first
+      // maximum (strict comparison: the first one, never a NaN) and last NaN
+      // of the positions inside each query's prefix
+      float* base = sT + (kblk * 64 + (lane & 15)) * ST + 4 * (lane >> 4);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const uint32_t j = kblk * 64 + 16 * (r >> 2) + (lane & 15);
-        float* dst = j < lmax ? sT + j * ST + 4 * (lane >> 4) + (r & 3) : sink;
-        *dst = acc[r] * scale;
+        const float sv = acc[r] * scale;
+        base[16 * (r >> 2) * ST + (r & 3)] = sv;
+        const int u = r & 3;
+        const bool in = j < ql[u];
+        ln[u] = in && sv != sv ? (int)j : ln[u];
+        const bool up = in && sv > bv[u];
+        bv[u] = up ? sv : bv[u];
+        bi[u] = up ? j : bi[u];
+      }
+    }
+    // the 16 lanes of a row hold the same 4 queries: combine them (rotations
+    // by 8, 4, 2, 1 within the row give every lane all 16), then one lane per
+    // row writes the wave's partials
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      FirstMax f{bv[u], bi[u]};
+      f = row_first_max<0x128>(f);
+      f = row_first_max<0x124>(f);
+      f = row_first_max<0x122>(f);
+      f = row_first_max<0x121>(f);
+      int n = ln[u];
+      n = max(n, __builtin_amdgcn_update_dpp(0, n, 0x128, 0xF, 0xF, false));
+      n = max(n, __builtin_amdgcn_update_dpp(0, n, 0x124, 0xF, 0xF, false));
+      n = max(n, __builtin_amdgcn_update_dpp(0, n, 0x122, 0xF, 0xF, false));
+      n = max(n, __builtin_amdgcn_update_dpp(0, n, 0x121, 0xF, 0xF, false));
+      if ((lane & 15) == 0) {
+        const int qi = 4 * (lane >> 4) + u;
+        part[wave * QB + qi] = f.v;
+        part[4 * QB + wave * QB + qi] = __uint_as_float(f.i);
+        part[8 * QB + wave * QB + qi] = __int_as_float(n);
       }
     }
     // x - 1 wraps a zero to 0xFFFF: a minimum below kSafeLo - 1 is a nonzero
@@ -215,7 +267,8 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
     const uint32_t hi = mx[0] > mx[1] ? mx[0] : mx[1];
     unsafe |= lo < kSafeLo - 1u || hi >= kSafeHi;
   }
-  if (__syncthreads_or(unsafe)) {
+  const bool refold = __syncthreads_or(unsafe) != 0;
+  if (refold) {
     // the VALU fold: lane l owns key kb*64 + l, its 128 K values in registers
     // (bf16 pairs, widened at each use) folded against each of the 16
     // queries (LDS broadcasts of the bf16 q rows), v_mul_f32 then v_add_f32
@@ -253,62 +306,78 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
   __syncthreads();
 
   // ---------------------------------------------------------------- max per query
-  // Wave w takes queries w, w + 4, w + 8, w + 12 in one pass over the
-  // scores: per lane and query, the last NaN position and the first max of
-  // every value the lane read (positions ascending).  Without a NaN in the
-  // query's prefix, the first-max combine of those over the lanes
-  // (associative and commutative) is the sequential fold's result, as in the
-  // two-pass form; a query with a NaN takes that form (first max after the
-  // last NaN, or the NaN itself when it is the last position).
+  // Wave w takes queries w, w + 4, w + 8, w + 12: the last NaN position and
+  // the first max of the query's scores, from the four waves' partials of
+  // the matrix-core fold, or (after a VALU refold) from one pass over the
+  // scores in which each lane keeps them for the positions it reads
+  // (ascending).  Without a NaN in the query's prefix, the first-max combine
+  // of those (associative and commutative) is the sequential fold's result,
+  // as in the two-pass form; a query with a NaN takes that form (first max
+  // after the last NaN, or the NaN itself when it is the last position).
   {
-    uint32_t len4[4], lmx = 0;
+    uint32_t len4[4];
     int ln4[4];
     FirstMax fm4[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      len4[u] = qlen[wave + 4 * u];
-      lmx = len4[u] > lmx ? len4[u] : lmx;
-      ln4[u] = -1;
-      fm4[u] = FirstMax{__uint_as_float(0xFF800000u), 0xFFFFFFFFu};
-    }
-    // per lane the positions ascend, so its first maximum is kept by a
-    // strict comparison (a NaN never replaces it; a query with one takes the
-    // two-pass form below; a lane holding only -inf stays empty, which the
-    // combine treats as -inf)
-    float bv[4];
-    uint32_t bi[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      bv[u] = __uint_as_float(0xFF800000u);
-      bi[u] = 0xFFFFFFFFu;
-    }
-    for (uint32_t t = lane; t < lmx; t += 64) {
-      const float* row = sT + t * ST + wave;
+    for (int u = 0; u < 4; ++u) len4[u] = qlen[wave + 4 * u];
+    if (!refold) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        if (t < len4[u]) {
-          const float sv = row[4 * u];
-          if (sv != sv) ln4[u] = (int)t;
-          if (sv > bv[u]) {
-            bv[u] = sv;
-            bi[u] = t;
+        const int i = wave + 4 * u;
+        FirstMax f{__uint_as_float(0xFF800000u), 0xFFFFFFFFu};
+        int n = -1;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          f = first_max_combine(f, FirstMax{part[w * QB + i], __float_as_uint(part[4 * QB + w * QB + i])});
+          const int nw = __float_as_int(part[8 * QB + w * QB + i]);
+          n = nw > n ? nw : n;
+        }
+        fm4[u] = f;
+        ln4[u] = n;
+      }
+    } else {
+      uint32_t lmx = 0;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) lmx = len4[u] > lmx ? len4[u] : lmx;
+      // per lane the positions ascend, so its first maximum is kept by a
+      // strict comparison (a NaN never replaces it; a lane holding only
+      // -inf stays empty, which the combine treats as -inf)
+      float bv[4];
+      uint32_t bi[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        bv[u] = __uint_as_float(0xFF800000u);
+        bi[u] = 0xFFFFFFFFu;
+        ln4[u] = -1;
+      }
+      for (uint32_t t = lane; t < lmx; t += 64) {
+        const float* row = sT + t * ST + wave;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (t < len4[u]) {
+            const float sv = row[4 * u];
+            if (sv != sv) ln4[u] = (int)t;
+            if (sv > bv[u]) {
+              bv[u] = sv;
+              bi[u] = t;
+            }
           }
         }
       }
-    }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) fm4[u] = FirstMax{bv[u], bi[u]};
-    // the four queries' butterflies interleaved (independent shuffle chains)
+      for (int u = 0; u < 4; ++u) fm4[u] = FirstMax{bv[u], bi[u]};
+      // the four queries' butterflies interleaved (independent shuffle chains)
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
+      for (int off = 32; off >= 1; off >>= 1) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int o = __shfl_xor(ln4[u], off, 64);
-        ln4[u] = o > ln4[u] ? o : ln4[u];
-        FirstMax b;
-        b.v = __shfl_xor(fm4[u].v, off, 64);
-        b.i = (uint32_t)__shfl_xor((int)fm4[u].i, off, 64);
-        fm4[u] = first_max_combine(fm4[u], b);
+        for (int u = 0; u < 4; ++u) {
+          const int o = __shfl_xor(ln4[u], off, 64);
+          ln4[u] = o > ln4[u] ? o : ln4[u];
+          FirstMax b;
+          b.v = __shfl_xor(fm4[u].v, off, 64);
+          b.i = (uint32_t)__shfl_xor((int)fm4[u].i, off, 64);
+          fm4[u] = first_max_combine(fm4[u], b);
+        }
       }
     }
 #pragma unroll
@@ -508,7 +577,8 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
 }
 
 // grid = B * H * ceil(Tq / 16), block = 256, dynamic LDS =
-// 16*136*2 + 3*16*4 + 16 + Lmax*17*4 with Lmax >= min(max lens, L).
+// 16*136*2 + 3*16*4 + 3*4*16*4 + R*17*4 with R >= min(max lens, L) rounded up
+// to a multiple of 64 (the score rows of whole 64-key blocks).
 extern "C" __global__ __launch_bounds__(256) void catena_attn_prefill_bf16_d128_f32out(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint32_t* __restrict__ lens, float* __restrict__ o, uint32_t B, uint32_t H, uint32_t L,
