@@ -82,24 +82,6 @@ CATENA_DEV FirstMax row_first_max(FirstMax a) {
   return first_max_combine(a, b);
 }
 
-// Keys Q .. 15 of a group of 16 in the output fold: lane 16j + q holds the
-// p values of key q for the wave's 4 queries (pq[u]), w[Q] the lane's two V
-// columns of key Q.  acc = acc + fl(p * v) per query and column, keys in
-// ascending order; each key's p reaches its row by DPP broadcast.
-template <int Q>
-CATENA_DEV void pv_keys16(const float (&pq)[4], const uint32_t (&w)[16], float (&acc0)[4],
-                          float (&acc1)[4]) {
-  const float v0 = bf16lo(w[Q]), v1 = bf16hi(w[Q]);
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const float x0 = row_bcast16<Q>(pq[u]) * v0;
-    const float x1 = row_bcast16<Q>(pq[u]) * v1;
-    acc0[u] = acc0[u] + x0;
-    acc1[u] = acc1[u] + x1;
-  }
-  if constexpr (Q + 1 < 16) pv_keys16<Q + 1>(pq, w, acc0, acc1);
-}
-
 CATENA_DEV uint32_t query_len(uint32_t lens_b, uint32_t L, uint32_t Tq, uint32_t tq) {
   uint32_t len = lens_b > L ? L : lens_b;
   const uint32_t later = Tq - 1 - tq;
@@ -495,98 +477,101 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
   __syncthreads();
 
   // ---------------------------------------------------------------- P V
-  const int qg = wave;                       // queries 4qg .. 4qg+3
-  const uint32_t cp = (uint32_t)lane;        // columns 2cp, 2cp+1
+  // Wave w owns output columns 32w .. 32w + 31 of the 16 queries.  For each
+  // group of 4 keys t .. t + 3, two v_mfma_f32_16x16x1_4b_f32 with a zero
+  // accumulator form the 16 x 16 x 4 products (K = 1: one product, one
+  // rounding, so each is fl(p * v), the reference's product; a -0 product
+  // comes out +0, which no add below can tell apart: every sum starts at +0
+  // and never becomes -0): block b = key t + b, row i = query i (A: lane
+  // 16b + i holds p[i][t + b]), column j = column pair j of the wave (B:
+  // lane 16b + j holds v[t + b][32w + 2j], the second MFMA the odd column).
+  // Lane l receives in register 4kk + u the product of key t + kk, query
+  // 4(l / 16) + u and its column pair l % 16, and adds it to that query's
+  // two sums on the VALU, keys in ascending order (a key past the query's
+  // prefix is skipped).
+  const uint32_t jp = (uint32_t)lane & 15, kq = (uint32_t)lane >> 4;
   uint32_t glen[4];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) glen[u] = qlen[4 * qg + u];
-  // Prefixes grow with the query, but queries past nq (a last block's
-  // padding) have length 0: the longest of the four is their maximum, not
-  // the last one's (with two or three real queries in the wave, the last
-  // slot is padding).  The shortest is the first's (padding only follows).
-  uint32_t lmax4 = glen[0];
+  for (int u = 0; u < 4; ++u) glen[u] = qlen[4 * kq + u];
+  // every real query of the block sees at least qlen[0] keys (padding rows'
+  // sums are never stored)
+  const uint32_t ng = (lmax + 3) / 4, nfull = qlen[0] / 4;
+  float s0[4], s1[4];
 #pragma unroll
-  for (int u = 1; u < 4; ++u) lmax4 = glen[u] > lmax4 ? glen[u] : lmax4;
-  const uint32_t lmin4 = glen[0];
-  float acc0[4], acc1[4];
+  for (int u = 0; u < 4; ++u) s0[u] = s1[u] = __uint_as_float(0u);
+  // V words by range-checked buffer loads (keys past lmax read zeros),
+  // eight groups ahead of their use
+  const __amdgpu_buffer_rsrc_t vrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)vb, (short)0,
+                                        __builtin_amdgcn_readfirstlane((int)(lmax * (uint32_t)D * 2u)), kRsrcWord3);
+  const int voff = (int)((kq * D + 32 * (uint32_t)wave + 2 * jp) * 2u);
+  auto vload = [&](uint32_t t) -> uint32_t {
+    return __builtin_amdgcn_raw_buffer_load_b32(vrs, voff + (int)(t * (uint32_t)D * 2u), 0, 0);
+  };
+  const float* pcol = sT + kq * ST + jp;  // p[jp][t + kq] at pcol[t * ST]
+  const f32x16_t zero16 = {};
+  uint32_t vw[8];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) acc0[u] = acc1[u] = __uint_as_float(0u);
-
-  // the wave reads V rows itself (lane cp: the row's 32-bit word cp, one
-  // coalesced 256-byte row per load), 16 keys ahead of the fold, up to its
-  // own longest prefix
-  const uint32_t* vrow = reinterpret_cast<const uint32_t*>(vb) + cp;
-  uint32_t t = 0;
-  uint32_t wn[16];
-  if (lmin4 >= 16) {
+  for (int i = 0; i < 8; ++i) vw[i] = vload(4u * i);
+  for (uint32_t g = 0; g < ng; g += 8) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) wn[j] = vrow[(uint64_t)j * (D / 2)];
-  }
-  // groups of 16 unmasked keys: one LDS read of p per query and group
-  // (lane 16j + q: key t + q) instead of a broadcast read per key
-  for (; t + 16 <= lmin4; t += 16) {
-    uint32_t w[16];
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t t = 4 * (g + i);
+      const uint32_t w = vw[i];
+      vw[i] = vload(t + 32);
+      if (g + i < ng) {
+        const float pv = pcol[t * ST];
+        const f32x16_t x0 = __builtin_amdgcn_mfma_f32_16x16x1f32(pv, bf16lo(w), zero16, 0, 0, 0);
+        const f32x16_t x1 = __builtin_amdgcn_mfma_f32_16x16x1f32(pv, bf16hi(w), zero16, 0, 0, 0);
+        if (g + i < nfull) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) w[j] = wn[j];
-    if (t + 32 <= lmin4) {
+          for (int kk = 0; kk < 4; ++kk) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) wn[j] = vrow[(uint64_t)(t + 16 + j) * (D / 2)];
-    }
-    const float* pl = sT + (t + (uint32_t)(lane & 15)) * ST + 4 * qg;
-    float pq[4];
+            for (int u = 0; u < 4; ++u) {
+              s0[u] = s0[u] + x0[4 * kk + u];
+              s1[u] = s1[u] + x1[4 * kk + u];
+            }
+          }
+        } else {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) pq[u] = pl[u];
-    pv_keys16<0>(pq, w, acc0, acc1);
-  }
-  for (; t < lmin4; ++t) {
-    const uint32_t w = vrow[(uint64_t)t * (D / 2)];
-    const float v0 = bf16lo(w), v1 = bf16hi(w);
-    const float* prow = sT + t * ST + 4 * qg;
+          for (int kk = 0; kk < 4; ++kk) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float pu = prow[u];
-      const float x0 = pu * v0, x1 = pu * v1;
-      acc0[u] = acc0[u] + x0;
-      acc1[u] = acc1[u] + x1;
-    }
-  }
-  for (; t < lmax4; ++t) {
-    const uint32_t w = vrow[(uint64_t)t * (D / 2)];
-    const float v0 = bf16lo(w), v1 = bf16hi(w);
-    const float* prow = sT + t * ST + 4 * qg;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      if (t < glen[u]) {
-        const float pu = prow[u];
-        const float x0 = pu * v0, x1 = pu * v1;
-        acc0[u] = acc0[u] + x0;
-        acc1[u] = acc1[u] + x1;
+            for (int u = 0; u < 4; ++u) {
+              const bool in = t + kk < glen[u];
+              s0[u] = in ? s0[u] + x0[4 * kk + u] : s0[u];
+              s1[u] = in ? s1[u] + x1[4 * kk + u] : s1[u];
+            }
+          }
+        }
       }
     }
   }
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    const uint32_t qi = 4 * qg + u;
+    const uint32_t qi = 4 * kq + u;
     if (qi >= nq) continue;
-    const uint64_t off = (((uint64_t)b * Tq + t0 + qi) * H + h) * D + 2 * cp;
+    const uint64_t off = (((uint64_t)b * Tq + t0 + qi) * H + h) * D + 32 * (uint32_t)wave + 2 * jp;
     if (OUT_BF16)
-      *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(o) + off) = pack_bf16x2(acc0[u], acc1[u]);
+      *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(o) + off) = pack_bf16x2(s0[u], s1[u]);
     else
-      *reinterpret_cast<float2*>(static_cast<float*>(o) + off) = make_float2(acc0[u], acc1[u]);
+      *reinterpret_cast<float2*>(static_cast<float*>(o) + off) = make_float2(s0[u], s1[u]);
   }
 }
 
+// At least two waves per SIMD: the register budget is then 256, so the
+// matrix-core results are placed in ordinary VGPRs (no AGPR copies before
+// the VALU adds).
 // grid = B * H * ceil(Tq / 16), block = 256, dynamic LDS =
 // 16*136*2 + 3*16*4 + 3*4*16*4 + R*17*4 with R >= min(max lens, L) rounded up
 // to a multiple of 64 (the score rows of whole 64-key blocks).
-extern "C" __global__ __launch_bounds__(256) void catena_attn_prefill_bf16_d128_f32out(
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void catena_attn_prefill_bf16_d128_f32out(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint32_t* __restrict__ lens, float* __restrict__ o, uint32_t B, uint32_t H, uint32_t L,
     uint32_t Tq, float scale) {
   prefill_body<false>(q, k, v, lens, o, B, H, L, Tq, scale);
 }
 
-extern "C" __global__ __launch_bounds__(256) void catena_attn_prefill_bf16_d128_bf16out(
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void catena_attn_prefill_bf16_d128_bf16out(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint32_t* __restrict__ lens, uint16_t* __restrict__ o, uint32_t B, uint32_t H, uint32_t L,
     uint32_t Tq, float scale) {
