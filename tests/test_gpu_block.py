@@ -399,6 +399,51 @@ def test_attention_prefill_mfma_fold_range_guard():
     _bitwise(o32.read(np.float32, (B * Tq, H * D)), want)
 
 
+def test_attention_prefill_pv_products_specials():
+    """The prefill kernel forms the P·V products on the matrix cores with a
+    zero accumulator (fl(p * v), then the adds on the VALU).  Heads that
+    push those products to the edges: head 0 spreads the scores over
+    hundreds (exp~ of the shifted scores, wrapped powers of two included,
+    gives tiny and denormal p); head 1 puts NaN, +-inf, +-0, bf16 denormals
+    and the largest bf16 values into V at random positions; head 2 pairs
+    tiny p with denormal V (products underflow to denormals or zero); head
+    3 plain.  L = 100 (not a multiple of the 64-key blocks), Tq = 40 (a
+    partial last query block), and a sequence shorter than Tq.  f32 output
+    bitwise the oracle (NaN positions equal)."""
+    B, Tq, H, L, D = 3, 40, 4, 100, 128
+    lens = [100, 60, 25]
+    rng = np.random.default_rng(707)
+    q32 = rng.normal(0, 1, (B, Tq, H, D)).astype(np.float32)
+    k32 = rng.normal(0, 1, (B, H, L, D)).astype(np.float32)
+    v32 = rng.normal(0, 1, (B, H, L, D)).astype(np.float32)
+    q32[:, :, 0] *= 16.0
+    k32[:, 0] *= 4.0
+    q32[:, :, 2] *= 12.0
+    k32[:, 2] *= 4.0
+    v16 = oracle.f32_to_bf16_bits_np(v32)
+    specials = np.array([0x7FC0, 0xFFC1, 0x7F80, 0xFF80, 0x0000, 0x8000, 0x0001, 0x807F,
+                         0x0040, 0x7F7F, 0xFF7F], np.uint16)
+    msk = rng.random((B, L, D)) < 0.02
+    v16[:, 1][msk] = rng.choice(specials, int(msk.sum()))
+    v16[:, 2] = (rng.integers(1, 0x80, (B, L, D)) | (rng.integers(0, 2, (B, L, D)) << 15)).astype(np.uint16)
+    q16 = oracle.f32_to_bf16_bits_np(q32).reshape(-1)
+    k16 = oracle.f32_to_bf16_bits_np(k32)
+    q, k, v = ca.Buffer.from_array(q16), ca.Buffer.from_array(k16), ca.Buffer.from_array(v16)
+    lb = ca.Buffer.from_array(np.array(lens, np.uint32))
+    scale = 1.0 / math.sqrt(D)
+    o32 = ca.Buffer(B * Tq * H * D * 4)
+    say("prefill attention: P.V products at the edges (tiny p, V specials, denormal V)")
+    ca.attn_causal_bf16(q, k, v, lb, o32, B, Tq, H, L, D, scale, out_f32=True)
+    want = od.attn_causal(q16, k16, v16, lens, B, Tq, H, D, scale)
+    got = o32.read(np.float32, (B * Tq, H * D))
+    _bitwise(got, want)
+    # the heads reach the cases they are for
+    w = want.reshape(B, Tq, H, D)
+    assert np.isnan(w[:, :, 1]).any() and np.isinf(w[:, :, 1]).any()
+    tiny = np.abs(w[:, :, 2])
+    assert ((tiny > 0) & (tiny < np.float32(2.0 ** -126))).any()
+
+
 def test_attention_causal_tq1_equals_decode_kernel():
     B, H, L, D = 4, 8, 1024, 128
     q, k, v = _attn_inputs(B, 1, H, L, 99)
