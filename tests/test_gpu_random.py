@@ -358,8 +358,10 @@ def test_tile_gemm_paths_random():
 
 def test_attention_long_and_prefill_boundary_random():
     """Decode attention at random long caches (up to 6000 positions) and the
-    causal form around the prefill kernel's cache limit (max_len ~830, the
-    one-query kernel beyond it): bitwise the oracle."""
+    causal form around the prefill kernel's cache limit (max_len 1,088: the
+    score matrix of whole 64-key blocks fits 80 KB of LDS; the one-query
+    kernel beyond it), at the limit, one past it and at random lengths:
+    bitwise the oracle."""
     D = 128
     rng = np.random.default_rng(84)
     for i in range(4):
@@ -376,9 +378,8 @@ def test_attention_long_and_prefill_boundary_random():
         want = oracle.attn_decode(q.read(np.uint16, (B, H, D)), k.read(np.uint16, (B, H, L, D)),
                                   v.read(np.uint16, (B, H, L, D)), np.array(lens, np.uint32), scale)
         _bits_nan_aware(o.read(np.float32, (B, H, D)), want)
-    for i in range(4):
+    for i, L in enumerate([1088, 1089, int(rng.integers(700, 1300)), int(rng.integers(700, 1300))]):
         B, H, Tq = int(rng.integers(1, 3)), int(rng.integers(1, 3)), int(rng.integers(8, 60))
-        L = int(rng.integers(700, 1100))
         lens = [int(x) for x in rng.integers(Tq, L + 1, B)]
         scale = float(np.float32(rng.uniform(0.05, 0.2)))
         q = dev_normal_bf16(B * Tq * H * D, 1300 + i, 0)
