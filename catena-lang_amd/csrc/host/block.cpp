@@ -109,10 +109,10 @@ int catena_mi355x_attn_causal_bf16(const uint16_t* q, const uint16_t* k, const u
     return fail(CATENA_ERR_INVALID_ARGUMENT, "K/V caches must be 16-byte aligned");
   if (blocks > 0x7FFFFFFFu) return fail(CATENA_ERR_UNSUPPORTED, "too many queries");
   // Many queries per sequence: the block-of-16-queries kernel, which reads
-  // each K / V row once per block (its score buffer grows with max_len, so
-  // it is used while two workgroups still fit a CU; it reads q rows with
-  // 16-byte loads); otherwise the one-query-per-workgroup kernel.  Both give
-  // the same bits.
+  // each K / V row once per block (its score buffer grows with max_len in
+  // whole 64-key blocks, so it is used while two workgroups still fit a CU,
+  // max_len <= 1088; it reads q rows with 16-byte loads); otherwise the
+  // one-query-per-workgroup kernel.  Both give the same bits.
   const size_t lds_pf =
       16 * 136 * 2 + 3 * 16 * 4 + 3 * 4 * 16 * 4 + (size_t)ceil_div(max_len, 64) * 64 * 17 * 4;
   if (tq >= 8 && lds_pf <= 80 * 1024 && aligned16(q)) {

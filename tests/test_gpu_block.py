@@ -497,11 +497,11 @@ def test_argmax_chunked_nan_and_tie_patterns():
 
 @pytest.mark.parametrize("B,Tq,H,L,lens", [(2, 37, 3, 200, [200, 37]), (1, 512, 2, 640, [512]),
                                            (3, 8, 2, 96, [96, 8, 30]), (2, 100, 1, 700, [700, 120]),
-                                           (1, 12, 2, 1000, [1000])])
+                                           (1, 12, 2, 1000, [1000]), (1, 20, 2, 1200, [1200])])
 def test_attention_prefill_kernel_equals_per_query_kernel(B, Tq, H, L, lens):
     """The causal attention (the 16-query-block kernel for Tq >= 8 while its
-    score buffer fits, L <= ~830; the one-query kernel beyond, as in the last
-    case) against the decode kernel run once per query on that query's
+    score buffer fits, L <= 1,088; the one-query kernel beyond, as in the
+    last case) against the decode kernel run once per query on that query's
     prefix (same bits by construction), including cached prefixes
     (lens > Tq), partial last blocks and sequences shorter than Tq."""
     D = 128
