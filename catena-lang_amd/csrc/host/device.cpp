@@ -78,6 +78,8 @@ const KernelSpec kKernels[] = {
     {KernelId::AttnDecodeD128, "attn_decode", "catena_attn_decode_bf16_d128"},
     {KernelId::AttnFewD128F32, "attn_few", "catena_attn_few_bf16_d128_f32out"},
     {KernelId::AttnFewD128Bf16, "attn_few", "catena_attn_few_bf16_d128_bf16out"},
+    {KernelId::AttnFewSplitD128F32, "attn_few", "catena_attn_few_split_bf16_d128_f32out"},
+    {KernelId::AttnFewSplitD128Bf16, "attn_few", "catena_attn_few_split_bf16_d128_bf16out"},
     {KernelId::AttnCausalD128F32, "attn_decode", "catena_attn_causal_bf16_d128_f32out"},
     {KernelId::AttnCausalD128Bf16, "attn_decode", "catena_attn_causal_bf16_d128_bf16out"},
     {KernelId::AttnPrefillD128F32, "attn_prefill", "catena_attn_prefill_bf16_d128_f32out"},

@@ -40,6 +40,8 @@ enum class KernelId : int {
   AttnDecodeD128,
   AttnFewD128F32,  // eight waves per pair for few pairs (attn_few.hip)
   AttnFewD128Bf16,
+  AttnFewSplitD128F32,  // two seven-wave workgroups per pair (attn_few.hip)
+  AttnFewSplitD128Bf16,
   AttnCausalD128F32,
   AttnCausalD128Bf16,
   AttnPrefillD128F32,
@@ -113,6 +115,14 @@ constexpr uint64_t kAttnFewMaxQueries = 256;
 constexpr size_t kAttnFewFixed = 4096 + 2 * 32768 + 2 * 5 * 8192;
 inline size_t attn_few_lds_bytes(uint32_t max_len) {
   return kAttnFewFixed + (size_t)((max_len + 63) / 64) * (64 * 4);
+}
+// The split form (up to 128 pairs, so at most 256 workgroups): two
+// seven-wave workgroups per pair, each with one column half's product
+// slots and V ring (77,824 B fixed).
+constexpr uint64_t kAttnFewSplitMaxQueries = 128;
+constexpr size_t kAttnFewSplitFixed = 4096 + 2 * 16384 + 5 * 8192;
+inline size_t attn_few_split_lds_bytes(uint32_t max_len) {
+  return kAttnFewSplitFixed + (size_t)((max_len + 63) / 64) * (64 * 4);
 }
 // A decode step's q / k / v as its fused projection's k-group partials
 // (FewQkv in attn_few.hip, field for field): parts[n_parts][rows][3 H 128]

@@ -226,6 +226,12 @@ int attn_few_launch(const uint16_t* q, const uint16_t* k, const uint16_t* v, con
     return fail(CATENA_ERR_INVALID_ARGUMENT, "attention q/k/v partials operands");
   FewQkvArgs a = qkv;
   void* args[] = {&q, &k, &v, &lens, &o, &heads, &max_len, &tq, &scale, &a};
+  // up to 128 pairs: two workgroups per pair (each makes all the scores and
+  // adds one half of the output columns), so that 2 x pairs CUs stream K
+  // and V instead of one per pair
+  if (nq <= kAttnFewSplitMaxQueries)
+    return launch(out_f32 ? KernelId::AttnFewSplitD128F32 : KernelId::AttnFewSplitD128Bf16,
+                  dim3((unsigned)(2 * nq)), dim3(448), attn_few_split_lds_bytes(max_len), args);
   return launch(out_f32 ? KernelId::AttnFewD128F32 : KernelId::AttnFewD128Bf16, dim3((unsigned)nq),
                 dim3(512), attn_few_lds_bytes(max_len), args);
 }

@@ -53,19 +53,24 @@ CATENA_DEV uint32_t kswz(uint32_t row, uint32_t chunk) { return 16u * (chunk ^ (
 constexpr int VB_ROWS = 64;              // rows per V batch
 constexpr int VB_BYTES = VB_ROWS * 128;  // 64 rows x 64 columns bf16
 constexpr int VRING = 5;                 // batches in flight per V wave (8 loads each)
-constexpr int PSLOT_BYTES = 2 * 64 * 64 * 4;  // one batch's products, both column halves
+constexpr int HALF_PSLOT = 64 * 64 * 4;  // one batch's products of one column half
 
 // LDS: q copies [6][128] f32 | den, last score, last NaN, max keys | new key
 // row | K stages [6][4 KiB] until the scores are done, then the product
-// slots [2][PSLOT_BYTES] | V rings [2][VRING][8 KiB] | scores
-// sp[64 * ceil(L/64)]
+// slots [2][NH][HALF_PSLOT] | V rings [NH][VRING][8 KiB] | scores
+// sp[64 * ceil(L/64)], with NH = 2 column halves per workgroup, or 1 in the
+// split form (two workgroups per pair, one column half each)
 constexpr uint32_t kOffDen = KWAVES * 512;
 constexpr uint32_t kOffKNew = kOffDen + 256;  // the new key row (partials mode), 256 B
 constexpr uint32_t kOffK = 4096;
 constexpr uint32_t kOffP = 4096;
-constexpr uint32_t kOffV = kOffP + 2 * PSLOT_BYTES;
-constexpr uint32_t kOffState = kOffV + 2 * VRING * VB_BYTES;
-static_assert(kOffK + KWAVES * KSTAGE_WAVE <= kOffV, "K stages inside the product slots' space");
+template <int NH>
+struct FewLayout {
+  static constexpr uint32_t PSLOT = NH * HALF_PSLOT;
+  static constexpr uint32_t OffV = kOffP + 2 * PSLOT;
+  static constexpr uint32_t OffState = OffV + NH * VRING * VB_BYTES;
+  static_assert(kOffK + KWAVES * KSTAGE_WAVE <= OffV, "K stages inside the product slots' space");
+};
 
 CATENA_DEV void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -141,11 +146,19 @@ struct FewQkv {
 
 namespace {
 
-template <bool OUT_BF16>
+// SPLIT: two workgroups per pair (grid = 2 x pairs, 7 waves each): both
+// make all the scores and the softmax, workgroup half hf (the upper half of
+// the grid) adds output columns 64 hf .. 64 hf + 63 with its one V wave.
+// The same operands in the same order, so the same bits; in partials mode
+// both write the same q, k and f32 sums (identical values), each its half
+// of the new value row.
+template <bool OUT_BF16, bool SPLIT>
 CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* k, const uint16_t* v,
                               const uint32_t* __restrict__ lens, void* __restrict__ o, uint32_t H, uint32_t L,
                               uint32_t Tq, float scale, const FewQkv& qkv) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
+  typedef FewLayout<SPLIT ? 1 : 2> Lay;
+  constexpr uint32_t PSLOT_BYTES = Lay::PSLOT, kOffV = Lay::OffV, kOffState = Lay::OffState;
   float* den_slot = reinterpret_cast<float*>(smem + kOffDen);
   float* last_slot = den_slot + 1;                                          // score at len - 1
   uint32_t* nan_word = reinterpret_cast<uint32_t*>(smem + kOffDen + 8);     // last NaN + 1
@@ -153,7 +166,12 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* k,
   float* sp = reinterpret_cast<float*>(smem + kOffState);  // 16-byte aligned
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t qi = blockIdx.x;
+  uint32_t qi = blockIdx.x, hf = 0;
+  if (SPLIT) {
+    const uint32_t np = gridDim.x / 2;
+    hf = blockIdx.x >= np ? 1u : 0u;
+    qi = blockIdx.x - hf * np;
+  }
   const uint32_t row = qi / H, h = qi % H;
   const uint32_t b = row / Tq, tq = row % Tq;
   uint32_t len = lens[b];
@@ -226,8 +244,8 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* k,
 
   if (wave >= KWAVES) {
     // ---------------------------------------------------------- V waves
-    const uint32_t vw = (uint32_t)wave - KWAVES;  // column half
-    const uint32_t colbase = 64u * vw;
+    const uint32_t vw = (uint32_t)wave - KWAVES;  // this workgroup's column half
+    const uint32_t colbase = 64u * (SPLIT ? hf : vw);
     // the ring's LDS offset, uniform across the wave (so M0 is set from a
     // scalar register)
     const uint32_t ring_off = __builtin_amdgcn_readfirstlane(kOffV + vw * (VRING * VB_BYTES));
@@ -312,7 +330,7 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* k,
     // place; after it, batch b's ring slot (its products are made) takes
     // batch b + VRING.  Lane = column colbase + lane: 16 reads of four
     // ascending products each, t ascending.
-    const uint32_t pcol = kOffP + vw * (PSLOT_BYTES / 2) + (uint32_t)lane * 256u;
+    const uint32_t pcol = kOffP + vw * HALF_PSLOT + (uint32_t)lane * 256u;
     const uint32_t pswz = (uint32_t)lane & 15u;
     float acc = __uint_as_float(0u);
     if (nblk > 0) {
@@ -551,10 +569,11 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* k,
 
   // Products p_t * v_{t,c} (one rounded multiply each) of batch b into
   // product slot b % 2, in the order the V waves add them: column c of
-  // half h at kOffP + (b % 2) PSLOT_BYTES + h PSLOT_BYTES / 2 + 256 c, its
-  // 16-byte chunk t / 4 at chunk index (t / 4) ^ (c % 16).  A batch is 16
-  // units of 8 rows x 64 columns (unit u: half u / 8, rows 8 (u % 8) ..),
-  // wave w making units w, w + 6, w + 12.  Per unit: two transposing reads
+  // half h (of the workgroup's halves) at kOffP + (b % 2) PSLOT_BYTES +
+  // h HALF_PSLOT + 256 c, its 16-byte chunk t / 4 at chunk index
+  // (t / 4) ^ (c % 16).  A batch is 16 units of 8 rows x 64 columns (unit
+  // u: half u / 8, rows 8 (u % 8) ..; the split form: 8 units of its one
+  // half), wave w making units w, w + 6, w + 12.  Per unit: two transposing reads
   // (lane 16g + i receives column 16g + i of rows 4j .. 4j + 3), p of the 8
   // rows by a DPP row broadcast, one 16-byte write per four rows.  In the
   // last, partial batch rows past len (they hold row 0 and sp holds no p for
@@ -562,14 +581,14 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* k,
   // and an add never turns them into -0).
   const uint32_t tr_off = (4u * (((uint32_t)lane & 15u) >> 2)) * 32u +
                           2u * (16u * ((uint32_t)lane >> 4) + 4u * ((uint32_t)lane & 3u));
-  const uint32_t nunits = wave < 4 ? 3u : 2u;
+  const uint32_t nunits = SPLIT ? (wave < 2 ? 2u : 1u) : (wave < 4 ? 3u : 2u);
   auto produce = [&](uint32_t b) {
     i16x4_t v4[3][2];
     float p8[3];
 #pragma unroll
     for (uint32_t rep = 0; rep < 3; ++rep) {
       if (rep < nunits) {
-        const uint32_t unit = (uint32_t)wave + 6u * rep, half = unit >> 3, o8 = unit & 7u;
+        const uint32_t unit = (uint32_t)wave + 6u * rep, half = SPLIT ? 0u : unit >> 3, o8 = unit & 7u;
         uint32_t vbase = kOffV + half * (VRING * VB_BYTES) + (b % VRING) * VB_BYTES + o8 * 8u * 128u + tr_off;
         uint32_t pbase = kOffState + (b * 64u + o8 * 8u + ((uint32_t)lane & 7u)) * 4u;
         asm volatile("" : "+v"(vbase), "+v"(pbase));
@@ -583,9 +602,9 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* k,
 #pragma unroll
     for (uint32_t rep = 0; rep < 3; ++rep) {
       if (rep < nunits) {
-        const uint32_t unit = (uint32_t)wave + 6u * rep, half = unit >> 3, o8 = unit & 7u;
+        const uint32_t unit = (uint32_t)wave + 6u * rep, half = SPLIT ? 0u : unit >> 3, o8 = unit & 7u;
         const uint32_t t0 = b * 64u + o8 * 8u;
-        uint32_t wbase = kOffP + (b & 1u) * PSLOT_BYTES + half * (PSLOT_BYTES / 2) + (uint32_t)lane * 256u;
+        uint32_t wbase = kOffP + (b & 1u) * PSLOT_BYTES + half * HALF_PSLOT + (uint32_t)lane * 256u;
         asm volatile("" : "+v"(wbase));
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -615,11 +634,24 @@ CATENA_DEV void attn_few_body(const uint16_t* __restrict__ q, const uint16_t* k,
 extern "C" __global__ __launch_bounds__(512) void catena_attn_few_bf16_d128_f32out(
     const uint16_t* __restrict__ q, const uint16_t* k, const uint16_t* v, const uint32_t* __restrict__ lens,
     float* __restrict__ o, uint32_t H, uint32_t L, uint32_t Tq, float scale, FewQkv qkv) {
-  attn_few_body<false>(q, k, v, lens, o, H, L, Tq, scale, qkv);
+  attn_few_body<false, false>(q, k, v, lens, o, H, L, Tq, scale, qkv);
 }
 
 extern "C" __global__ __launch_bounds__(512) void catena_attn_few_bf16_d128_bf16out(
     const uint16_t* __restrict__ q, const uint16_t* k, const uint16_t* v, const uint32_t* __restrict__ lens,
     uint16_t* __restrict__ o, uint32_t H, uint32_t L, uint32_t Tq, float scale, FewQkv qkv) {
-  attn_few_body<true>(q, k, v, lens, o, H, L, Tq, scale, qkv);
+  attn_few_body<true, false>(q, k, v, lens, o, H, L, Tq, scale, qkv);
+}
+
+// the split form: grid = 2 x pairs, block = 448 (7 waves)
+extern "C" __global__ __launch_bounds__(448) void catena_attn_few_split_bf16_d128_f32out(
+    const uint16_t* __restrict__ q, const uint16_t* k, const uint16_t* v, const uint32_t* __restrict__ lens,
+    float* __restrict__ o, uint32_t H, uint32_t L, uint32_t Tq, float scale, FewQkv qkv) {
+  attn_few_body<false, true>(q, k, v, lens, o, H, L, Tq, scale, qkv);
+}
+
+extern "C" __global__ __launch_bounds__(448) void catena_attn_few_split_bf16_d128_bf16out(
+    const uint16_t* __restrict__ q, const uint16_t* k, const uint16_t* v, const uint32_t* __restrict__ lens,
+    uint16_t* __restrict__ o, uint32_t H, uint32_t L, uint32_t Tq, float scale, FewQkv qkv) {
+  attn_few_body<true, true>(q, k, v, lens, o, H, L, Tq, scale, qkv);
 }
