@@ -141,10 +141,11 @@ def test_attention_program_abi():
                                     (2000, [2000, 1999, 1025, 256, 257, 255, 1024, 1500]),
                                     (600, [600, 384, 385, 383, 448, 63, 2, 599])])
 def test_few_pairs_form_equals_many_pairs_form(L, lens):
-    """Eight sequences x 16 heads (128 pairs) take the eight-wave kernel; the
-    same sequences inside a batch of 40 (640 pairs) take the four-wave
-    kernel: per (b, h) the outputs are the same bits, and both equal the
-    oracle.  Lengths cross the 64-row blocks and the six score waves'
+    """Eight sequences x 16 heads (128 pairs) take the few-pair kernel's
+    split form (two workgroups per pair); the same sequences inside a batch
+    of 12 (192 pairs) its one-workgroup form, inside a batch of 40 (640
+    pairs) the four-wave kernel: per (b, h) the outputs are the same bits,
+    and all equal the oracle.  Lengths cross the 64-row blocks and the six score waves'
     rotation (384 rows), down to 1 and 0, around the 1024 switch of the
     denominator's chain, with ceil(L / 64) not a multiple of 4."""
     H = 16
@@ -157,8 +158,11 @@ def test_few_pairs_form_equals_many_pairs_form(L, lens):
     lens_l = list(lens) + [L] * (Bl - Bs)
     say(f"attention eight-wave form B={Bs} H={H} L={L}")
     small = _run(q, k, v, lens, Bs, H, L, scale)
+    say(f"attention eight-wave form B=12 H={H} L={L}")
+    mid = _run(q, k, v, lens_l[:12], 12, H, L, scale)
     say(f"attention four-wave form B={Bl} H={H} L={L}")
     large = _run(q, k, v, lens_l, Bl, H, L, scale)
+    assert np.array_equal(small.view(np.uint32), mid[:Bs].view(np.uint32))
     assert np.array_equal(small.view(np.uint32), large[:Bs].view(np.uint32))
     want = oracle.attn_decode(q.read(np.uint16, (Bl, H, D))[:Bs], k.read(np.uint16, (Bl, H, L, D))[:Bs],
                               v.read(np.uint16, (Bl, H, L, D))[:Bs], np.array(lens, np.uint32), scale)
