@@ -14,33 +14,38 @@
 // positions (clamped to [0, L]).
 //
 // Scores: waves take 64-key blocks round robin; lane l owns key kb*64 + l
-// and holds its K row in registers (the next block's row is loaded while the
-// current one is folded).  The fold over d runs on the matrix cores:
-// v_mfma_f32_16x16x1_4b_f32 with A = the 16 queries' q_d (lane l: query
-// l % 16, every block) and B = the 64 keys' k_d (lane l: key l) adds
-// q_d * k_{t,d} to each of the 16 x 64 accumulators with one rounding, d
-// ascending from +0.  The product of two bf16 values is exact in f32 unless
-// it leaves the normal range, so one rounding of acc + q_d k_{t,d} is the
-// reference's fl(acc + fl(q_d * k_{t,d})) bit for bit whenever every nonzero
-// q and k value has magnitude in [2^-63, 2^63) (products in [2^-126, 2^126)).
-// That range is checked on the same registers while the MFMAs run (packed
-// u16 min / max of the magnitude bits); if any value of the workgroup's q
-// rows or K rows lies outside it (tiny, huge, inf or NaN), the workgroup
-// recomputes its scores with the VALU fold (v_mul_f32 + v_add_f32 per
-// product) before anything reads them.  Scores go to sT[key][query] (row
-// stride QB + 1 floats: the per-query reads of softmax are bank-conflict
-// free).
+// and holds its K row in registers (chunk c of the next block's row is
+// loaded as soon as chunk c of the current one is folded).  The fold over d
+// runs on the matrix cores: v_mfma_f32_16x16x1_4b_f32 with A = the 16
+// queries' q_d (lane l: query l % 16, every block) and B = the 64 keys'
+// k_d (lane l: key l) adds q_d * k_{t,d} to each of the 16 x 64
+// accumulators with one rounding, d ascending from +0.  The product of two
+// bf16 values is exact in f32 unless it leaves the normal range, so one
+// rounding of acc + q_d k_{t,d} is the reference's fl(acc + fl(q_d *
+// k_{t,d})) bit for bit whenever every nonzero q and k value has magnitude
+// in [2^-63, 2^63) (products in [2^-126, 2^126)).  That range is checked on
+// the same registers while the MFMAs run (packed u16 min / max of the
+// magnitude bits); if any value of the workgroup's q rows or K rows lies
+// outside it (tiny, huge, inf or NaN), the workgroup recomputes its scores
+// with the VALU fold (v_mul_f32 + v_add_f32 per product) before anything
+// reads them.  Scores go to sT[key][query] (row stride QB + 1 floats: the
+// per-query reads of softmax are bank-conflict free; rows for whole 64-key
+// blocks).
 // Softmax: per query, the exact parallel form of the max fold (FirstMax,
-// common.h) by one wave; exp~ elementwise; the denominators are 16
-// independent serial folds, one lane per query; p = e / den elementwise.
-// Output: wave w owns queries 4w .. 4w+3 and lane l columns 2l, 2l+1 (8
-// accumulators); keys are walked in ascending order, the wave loading V rows
-// itself (one coalesced row per load, the next 16 keys in flight while 16
-// are folded; no workgroup barrier); the p values of 16 keys are read once
-// per lane and broadcast by DPP.  LDS holds the q rows (bf16) and the score
-// matrix only, so three or four workgroups share a CU at the C5 shape.  Keys
-// below the shortest of the 4 prefixes need no mask; past it, a key beyond a
-// query's prefix leaves that accumulator untouched.
+// common.h): each lane tracks the first maximum and the last NaN of the
+// scores it produces, rows of 16 lanes combine them by DPP and the max
+// phase combines the four waves' partials; exp~ elementwise; the
+// denominators are 16 independent serial folds, one lane per query;
+// p = e / den elementwise.
+// Output: wave w owns columns 32w .. 32w + 31 of all 16 queries.  The
+// products p_t * v_{t,c} come from v_mfma_f32_16x16x1_4b_f32 with a zero
+// accumulator (one product, one rounding: fl(p * v)), four keys per
+// instruction; the VALU adds them to the running sums in ascending key
+// order.  LDS holds the q rows (bf16), the per-query scalars, the max
+// partials and the score matrix only (V is read by each wave itself), so
+// three workgroups share a CU at the C5 shape.  Keys below the shortest
+// prefix of the block need no mask; past it, a key beyond a query's prefix
+// leaves that query's sums untouched.
 #include "common.h"
 
 namespace {
