@@ -97,6 +97,15 @@ int catena_mi355x_attn_causal_bf16(const uint16_t* q, const uint16_t* k, const u
                                    const uint32_t* lens, void* o, uint32_t batch, uint32_t tq,
                                    uint32_t heads, uint32_t max_len, uint32_t head_dim,
                                    float scale, int out_f32) {
+  return catena::attn_causal(q, k, v, lens, o, batch, tq, heads, max_len, max_len, head_dim, scale,
+                             out_f32);
+}
+}  // extern "C"
+
+namespace catena {
+int attn_causal(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint32_t* lens,
+                void* o, uint32_t batch, uint32_t tq, uint32_t heads, uint32_t max_len,
+                uint32_t len_bound, uint32_t head_dim, float scale, int out_f32) {
   int st = ensure_init();
   if (st) return st;
   if (head_dim != 128)
@@ -109,12 +118,15 @@ int catena_mi355x_attn_causal_bf16(const uint16_t* q, const uint16_t* k, const u
     return fail(CATENA_ERR_INVALID_ARGUMENT, "K/V caches must be 16-byte aligned");
   if (blocks > 0x7FFFFFFFu) return fail(CATENA_ERR_UNSUPPORTED, "too many queries");
   // Many queries per sequence: the block-of-16-queries kernel, which reads
-  // each K / V row once per block (its score buffer grows with max_len in
-  // whole 64-key blocks, so it is used while two workgroups still fit a CU,
-  // max_len <= 1088; it reads q rows with 16-byte loads); otherwise the
-  // one-query-per-workgroup kernel.  Both give the same bits.
+  // each K / V row once per block (its score buffer holds whole 64-key
+  // blocks of rows up to the longest prefix, bounded by len_bound (every
+  // lens[b] <= len_bound) and max_len, so it is used while two workgroups
+  // still fit a CU, bound <= 1088, and four share one for bounds up to 512;
+  // it reads q rows with 16-byte loads); otherwise the one-query-per-
+  // workgroup kernel.  Both give the same bits.
+  const uint32_t rows_bound = len_bound < max_len ? len_bound : max_len;
   const size_t lds_pf =
-      16 * 136 * 2 + 3 * 16 * 4 + 3 * 4 * 16 * 4 + (size_t)ceil_div(max_len, 64) * 64 * 17 * 4;
+      16 * 136 * 2 + 3 * 16 * 4 + 3 * 4 * 16 * 4 + (size_t)ceil_div(rows_bound, 64) * 64 * 17 * 4;
   if (tq >= 8 && lds_pf <= 80 * 1024 && aligned16(q)) {
     const uint64_t nqb = ceil_div(tq, 16);
     const uint64_t grid = (uint64_t)batch * heads * nqb;
@@ -134,6 +146,9 @@ int catena_mi355x_attn_causal_bf16(const uint16_t* q, const uint16_t* k, const u
   return launch(out_f32 ? KernelId::AttnCausalD128F32 : KernelId::AttnCausalD128Bf16,
                 dim3((unsigned)blocks), dim3(256), lds, args);
 }
+}  // namespace catena
+
+extern "C" {
 
 int catena_mi355x_rmsnorm_f32(const float* x, float* y, uint64_t rows, uint64_t n) {
   if (x && x == y) return fail(CATENA_ERR_INVALID_ARGUMENT, "rmsnorm output may not alias input");

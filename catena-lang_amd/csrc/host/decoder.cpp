@@ -145,14 +145,15 @@ void release(catena_decoder* m) {
   } while (0)
 
 // One forward pass over rows = batch * tq tokens (tq per sequence), caches
-// already holding the earlier positions; lens = positions after the append;
+// already holding the earlier positions; lens = positions after the append
+// (every sequence at the same length len, a row of the lens table);
 // final_rows selects each sequence's last row (NULL when tq == 1); next
 // receives the greedy tokens.  A decode step (tq == 1, batch <= 16) runs the
 // projections on the decode-shape GEMM with fused epilogues: RoPE and the
 // cache append after W_qkv, the SwiGLU gate after W_gu, greedy argmax after
 // W_lm; the embedding gather is fused into the first RMSNorm in both cases.
 int forward(catena_decoder& m, const uint32_t* tokens, uint32_t batch, uint32_t tq,
-            const uint32_t* lens, const uint32_t* final_rows, uint32_t* next,
+            const uint32_t* lens, uint32_t len, const uint32_t* final_rows, uint32_t* next,
             const uint32_t* in_sums = nullptr, bool defer_argmax = false) {
   const catena_decoder_config_t& c = m.cfg;
   const uint64_t rows = (uint64_t)batch * tq, d = m.d, f = m.f;
@@ -275,8 +276,8 @@ int forward(catena_decoder& m, const uint32_t* tokens, uint32_t batch, uint32_t 
                                       c.max_len));
     }
     if (!(step && few_attn))
-      TRY(catena_mi355x_attn_causal_bf16(Q, kc, vc, lens, ATT, batch, tq, c.n_heads, c.max_len,
-                                         c.head_dim, scale, 0));
+      TRY(attn_causal(Q, kc, vc, lens, ATT, batch, tq, c.n_heads, c.max_len, len, c.head_dim, scale,
+                      0));
     if (step) {
       // W_o without its split-K hand-off: the norm below adds the k-group
       // partials (and writes their sum to AP)
@@ -565,7 +566,7 @@ int catena_mi355x_decoder_prefill(catena_decoder_t* dec, const uint32_t* tokens,
   const uint32_t* lens = static_cast<const uint32_t*>(m.lens_table) + (uint64_t)t * c.max_batch;
   m.batch = batch;
   m.last_rows = batch * t;
-  TRY(forward(m, tokens, batch, t, lens, static_cast<const uint32_t*>(m.final_rows),
+  TRY(forward(m, tokens, batch, t, lens, t, static_cast<const uint32_t*>(m.final_rows),
               static_cast<uint32_t*>(m.cur_tok)));
   m.cur_len = t;
   TRY(hip_check(hipMemcpyAsync(m.act[CATENA_DEC_LENS], lens, batch * 4, hipMemcpyDeviceToDevice,
@@ -598,7 +599,8 @@ int catena_mi355x_decoder_generate(catena_decoder_t* dec, uint32_t steps, uint32
     const uint32_t* lens =
         static_cast<const uint32_t*>(m.lens_table) + (uint64_t)(m.cur_len + 1) * c.max_batch;
     m.last_rows = B;
-    TRY(forward(m, in, B, 1, lens, nullptr, out + (uint64_t)s * B, defer && s > 0 ? sums : nullptr, defer));
+    TRY(forward(m, in, B, 1, lens, m.cur_len + 1, nullptr, out + (uint64_t)s * B,
+                defer && s > 0 ? sums : nullptr, defer));
     m.cur_len += 1;
   }
   if (defer)

@@ -141,6 +141,12 @@ struct FewQkvArgs {
 };
 // Whether the eight-wave attention serves this shape.
 bool attn_few_fits(uint32_t batch, uint32_t tq, uint32_t heads, uint32_t max_len);
+// catena_mi355x_attn_causal_bf16 for a caller that knows every lens[b] <=
+// len_bound: the prefill kernel's score buffer is sized for len_bound
+// instead of max_len (the decoder's prefill: lens = t)
+int attn_causal(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint32_t* lens,
+                void* o, uint32_t batch, uint32_t tq, uint32_t heads, uint32_t max_len,
+                uint32_t len_bound, uint32_t head_dim, float scale, int out_f32);
 // Launch the eight-wave attention when it applies; returns -1 (nothing
 // launched) when it does not.
 int attn_few_launch(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint32_t* lens,

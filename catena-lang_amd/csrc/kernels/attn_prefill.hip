@@ -563,20 +563,21 @@ CATENA_DEV void prefill_body(const uint16_t* __restrict__ q, const uint16_t* __r
   }
 }
 
-// At least two waves per SIMD: the register budget is then 256, so the
-// matrix-core results are placed in ordinary VGPRs (no AGPR copies before
-// the VALU adds).
+// Four waves per SIMD: the register budget is then 128 (the matrix-core
+// results in ordinary VGPRs, no AGPR copies before the VALU adds; one value
+// spilled to 8 bytes of scratch), so four workgroups share a CU when the
+// score buffer allows (up to 512 rows): C5 prefill 256 -> 234 us.
 // grid = B * H * ceil(Tq / 16), block = 256, dynamic LDS =
 // 16*136*2 + 3*16*4 + 3*4*16*4 + R*17*4 with R >= min(max lens, L) rounded up
 // to a multiple of 64 (the score rows of whole 64-key blocks).
-extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void catena_attn_prefill_bf16_d128_f32out(
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void catena_attn_prefill_bf16_d128_f32out(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint32_t* __restrict__ lens, float* __restrict__ o, uint32_t B, uint32_t H, uint32_t L,
     uint32_t Tq, float scale) {
   prefill_body<false>(q, k, v, lens, o, B, H, L, Tq, scale);
 }
 
-extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void catena_attn_prefill_bf16_d128_bf16out(
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void catena_attn_prefill_bf16_d128_bf16out(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint32_t* __restrict__ lens, uint16_t* __restrict__ o, uint32_t B, uint32_t H, uint32_t L,
     uint32_t Tq, float scale) {
