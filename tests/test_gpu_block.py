@@ -84,7 +84,7 @@ def test_rmsnorm_specials(n):
     _bitwise(yb.read(np.float32, (6, n)), oracle.rmsnorm_f32(x))
 
 
-@pytest.mark.parametrize("n", [2048, 12, 5632])
+@pytest.mark.parametrize("n", [2048, 12, 5632, 1028, 8, 2044])
 def test_rmsnorm_many_rows(n):
     """2,100 rows (more than one round of workgroups on the device): bitwise
     the oracle on normal and special rows (zero, NaN, inf, overflowing and
